@@ -1,0 +1,179 @@
+"""Benchmark: decode attention over the int8ring_int4 tiered KV cache at a 262,144-token context, all 12 layers.
+
+Workload (one "step" = one decode token through all 12 attention layers): 16 query / 2 KV heads, head_dim 256;
+per layer an 8,192-slot INT8 ring (newest positions) + 253,952 older positions in 3,968 INT4-G32 pages of 64 tokens
+at randomly permuted physical pages.  The cache is filled through the real write path (quantize-append, with the
+oldest ring rows requantized INT8 -> INT4 on eviction).  Synthetic data: K ~ N(0,1) with 8 of 256 channels per
+head x8 (seeded per layer), V ~ N(0,1), Q ~ N(0,1)/16, bf16.
+
+Prints ONE JSON line: value = KV GB/s (algorithmic KV payload + scale bytes read per step / step time), with
+us/token over all layers, the roofline of the decode kernel (live HIP-event timing of its launches) and the CPU
+oracle timed on a bounded sample (one layer at the full context) as the baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl mfma|ref]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HQ, H, D, LAYERS = 16, 2, 256, 12
+CTX, RING = 262_144, 8192
+PAGE = 64
+PEAK_HBM = 8.0e12
+
+
+def build_cache(seed: int = 0):
+    import kvtier  # noqa: F401
+    from kvtier.kvt import PosTieredCache
+    n_cold = CTX - RING
+    n_pages = n_cold // PAGE
+    cache = PosTieredCache(LAYERS, H, D, n_pages=n_pages, ring_total=RING, max_seqs=1, max_pages=n_pages + 1,
+                           device="cuda", page_seed=seed)
+    cache.add_seq(RING)
+    gens = []
+    outl = []
+    for layer in range(LAYERS):
+        g = torch.Generator(device="cuda").manual_seed(seed * 1000 + layer)
+        gens.append(g)
+        gc = torch.Generator().manual_seed(seed * 1000 + layer)
+        ch = torch.stack([torch.randperm(D, generator=gc)[:8] for _ in range(H)])
+        mul = torch.ones(H, D)
+        for h in range(H):
+            mul[h, ch[h]] = 8.0
+        outl.append(mul.to("cuda"))
+    for a in range(0, CTX, RING):
+        plan = cache.plan_append([0], [RING])
+        for layer in range(LAYERS):
+            k = (torch.randn(RING, H, D, device="cuda", generator=gens[layer]) * outl[layer]).to(torch.bfloat16)
+            v = torch.randn(RING, H, D, device="cuda", generator=gens[layer]).to(torch.bfloat16)
+            cache.append(layer, plan, k, v)
+        cache.commit(plan)
+    torch.cuda.synchronize()
+    gq = torch.Generator(device="cuda").manual_seed(seed + 77)
+    q = (torch.randn(LAYERS, 1, HQ, D, device="cuda", generator=gq) / 16).to(torch.bfloat16)
+    return cache, q
+
+
+def cpu_baseline(cache, q, layer: int = 0):
+    """The oracle (torch, CPU) on one layer at the full context: gather + dequant of every position, fp32 attention.
+    Returns GB/s of KV bytes processed, the thread count and the sample description."""
+    from oracle import ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    st = ref.SeqState(0, RING, 0, cache.h_len[0], list(cache.h_pages[0]))
+    oc = ref.PosTieredCache.__new__(ref.PosTieredCache)
+    oc.H, oc.D, oc.group8 = H, D, cache.group8
+    for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
+        setattr(oc, name, getattr(cache, name)[layer].cpu())
+    oc.seqs = [st]
+    qc = q[layer, 0].cpu()
+    t0 = time.perf_counter()
+    kk, vv = oc.rows(0)
+    ref.attention_rows(qc, kk, vv, D ** -0.5)
+    dt = time.perf_counter() - t0
+    nbytes = cache.kv_bytes()
+    return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"oracle/ref.py dequant + fp32 attention of 1 of {LAYERS} layers at {CTX} tokens "
+                       f"({nbytes} KV bytes, {dt:.2f} s)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--impl", default=os.environ.get("KVT_DECODE_IMPL", "mfma"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is a design in "
+              "DESIGN.md, not a measured path", file=sys.stderr)
+        sys.exit(2)
+    import kvtier  # noqa: F401
+    from kvtier.kvt import kvt_decode_attn
+
+    cache, q = build_cache()
+    ws = {}
+    outs = [torch.empty(1, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
+
+    def step(events=None):
+        for layer in range(LAYERS):
+            kvt_decode_attn(cache, layer, q[layer], out=outs[layer], impl=args.impl, workspace=ws, events=events)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # kernel timing: HIP events on the launch stream around every decode-kernel launch of the timed steps
+    kev = []
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for _ in range(args.steps):
+        step(kev)
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_total = t_start.elapsed_time(t_end)
+    ms_step = ms_total / args.steps
+    kern_ms = [a.elapsed_time(b) for a, b in kev]
+    kern_avg_s = sum(kern_ms) / len(kern_ms) / 1e3
+    bytes_layer = cache.kv_bytes()
+    bytes_step = bytes_layer * LAYERS
+    value = bytes_step / (ms_step / 1e3) / 1e9
+    achieved = bytes_layer / kern_avg_s
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "decode_262k_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            t = json.load(f)
+        if t.get("impl") == args.impl:
+            traffic = t.get("hbm_bytes_per_launch")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(cache, q)
+    line = {
+        "metric": "decode-attn KV GB/s and % HBM peak at 256k ctx; us/token all layers",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "us_per_token_all_layers": round(ms_step * 1e3, 1),
+        "hbm_frac_of_step": round(value * 1e9 / PEAK_HBM, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16-mfma/f32" if args.impl == "mfma" else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode 262144-token context x 12 layers: 16 Q / 2 KV heads, D 256, INT8-G64 ring 8192 + "
+                        "253952 tokens in 3968 INT4-G32 pages (permuted), batch 1",
+            "impl": args.impl,
+            "kv_bytes_per_layer": bytes_layer,
+            "kv_bytes_per_step": bytes_step,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved / 1e9, 2),
+            "peak": PEAK_HBM / 1e9,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM, 4),
+            "traffic": traffic,
+            "kernel": "decode split-K (per layer launch)",
+            "kernel_avg_us": round(kern_avg_s * 1e6, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,132 @@
+/* C ABI of the MI355X tiered quantized KV cache (int8ring_int4) -- libkvtier.so.
+ *
+ * Conventions (every entry point):
+ *   - all tensor memory is owned and allocated by the caller (device pointers of torch tensors); the library
+ *     keeps no state and allocates nothing;
+ *   - work is enqueued on `stream` (a hipStream_t, e.g. torch.cuda.current_stream().cuda_stream); no entry point
+ *     synchronizes the host, grid sizes depend only on the integer arguments (capture-safe);
+ *   - the return value is KVT_OK (0) or a negative status: KVT_EINVAL (-1) unsupported shape / dtype / size,
+ *     KVT_ELAUNCH (-2) the launch failed, KVT_ERANGE (-3) a size beyond a documented maximum.
+ *
+ * Layouts (reference: patches/kv_int4.py:57-60, patches/kv_tiers.py:63-67):
+ *   INT4 pool   k_buf/v_buf uint8 [rows, H, D/2] (low nibble = even channel, q + 8);
+ *               k_scale/v_scale fp16 [rows, H, D/32]
+ *   INT8 ring   ring_k/ring_v int8 [R, H, D]; ring_ks/ring_vs fp16 [R, H, D/group8] (group8 = 64, or D for the
+ *               per-(token, head) form); owner int32 [R] (slot rings only)
+ *   sm_k/sm_v, sm_k_inv/sm_v_inv: fp16 [H, D] smoothing constants (identity in the served setup), may be NULL.
+ * Element type codes for K/V inputs: 0 = bf16, 1 = fp16, 2 = fp32.
+ */
+#ifndef KVTIER_H
+#define KVTIER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVT_OK 0
+#define KVT_EINVAL -1
+#define KVT_ELAUNCH -2
+#define KVT_ERANGE -3
+
+/* ----------------------------------------------------------------------------------------- write path */
+
+/* Dual write of N tokens: stamps owner[slot & ring_mask] = slot, then writes the INT8 ring row (owner only) and
+ * the INT4 pool row (always).  k/v: [N, H, D] with element strides (sk_n, sk_h), unit last stride; loc int32 or
+ * int64 [N].  Replaces quant_store_kv_tiered + _stamp_ring_owner + _quant_store_kv_tiered
+ * (patches/kv_tiers.py:272-443). */
+int kvt_quant_store_tiered(const void* k, const void* v, int dtype, int64_t sk_n, int64_t sk_h, int64_t sv_n,
+                           int64_t sv_h, const void* loc, int loc_is_int64, int64_t N, int H, int D, void* k_buf,
+                           void* v_buf, void* k_scale, void* v_scale, void* ring_k, void* ring_v, void* ring_ks,
+                           void* ring_vs, void* owner, const void* sm_k_inv, const void* sm_v_inv, int64_t ring_mask,
+                           int group8, void* stream);
+
+/* INT8-G quantize + scatter into int8 [rows, H, D] + fp16 [rows, H, D/group8] at loc.  Replaces
+ * quant_store_kv_int8 / _quant_store_kv_int8 (patches/kv_int8.py:281-362; scale clamped to fp16 max as in the
+ * tiered writer, patches/kv_tiers.py:336-337). */
+int kvt_quant_store_int8(const void* k, const void* v, int dtype, int64_t sk_n, int64_t sk_h, int64_t sv_n,
+                         int64_t sv_h, const void* loc, int loc_is_int64, int64_t N, int H, int D, void* k_buf,
+                         void* v_buf, void* k_scale, void* v_scale, const void* sm_k_inv, const void* sm_v_inv,
+                         int group8, void* stream);
+
+/* INT4-G32 quantize + nibble pack + scatter at loc.  Replaces quant_store_kv_int4 / _quant_store_kv_int4
+ * (patches/kv_int4.py:289-393). */
+int kvt_quant_store_int4(const void* k, const void* v, int dtype, int64_t sk_n, int64_t sk_h, int64_t sv_n,
+                         int64_t sv_h, const void* loc, int loc_is_int64, int64_t N, int H, int D, void* k_buf,
+                         void* v_buf, void* k_scale, void* v_scale, const void* sm_k_inv, const void* sm_v_inv,
+                         void* stream);
+
+/* page_table[seq[i] * pt_stride + lpage[i]] = ppage[i] for i < n (int32 arrays on the device).  The page-table
+ * update of the evict-mode write path; no reference counterpart (the reference only specifies the compactor's
+ * bookkeeping, docs/KV_TIERS_PLAN.md:63-67). */
+int kvt_page_table_update(void* page_table, int64_t pt_stride, int64_t n, const void* seq, const void* lpage,
+                          const void* ppage, void* stream);
+
+/* Position-ring append of N tokens (seq_ids int32 [N], positions int64 [N]; per sequence ring_base int64,
+ * ring_len int32 (power of two), ring_start int64): if e = p - ring_len >= ring_start, ring row
+ * ring_base + (p & (ring_len - 1)) is first requantized (f32(q8) * f32(s8) -> INT4-G32) into pool row
+ * page_table[seq][e / 64] * 64 + e % 64, then the token is quantized into that ring row.  Tokens of one call
+ * must use distinct ring rows.  Implements the compactor's _requant_kv_int8_to_int4 (docs/KV_TIERS_PLAN.md:53,
+ * :82) fused with the ring write of _quant_store_kv_tiered (patches/kv_tiers.py:325-351). */
+int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int64_t sk_h, int64_t sv_n, int64_t sv_h,
+                     const void* seq_ids, const void* positions, int64_t N, int H, int D, void* k_buf, void* v_buf,
+                     void* k_scale, void* v_scale, void* ring_k, void* ring_v, void* ring_ks, void* ring_vs,
+                     const void* ring_base, const void* ring_len, const void* ring_start, const void* page_table,
+                     int64_t pt_stride, const void* sm_k_inv, const void* sm_v_inv, int group8, void* stream);
+
+/* ----------------------------------------------------------------------------------------- gathers */
+
+/* Top-k gather-dequant into a bf16 scratch [*, H, D]: column c of request b is written at row cu_k[b] + c iff
+ * c < cu_k[b+1] - cu_k[b] and 0 <= indices[b][c] < seq_lens[b]; nothing else is written.  kind 0 = INT8 pool
+ * (k/v are the int8 codes, ring arguments unused), 1 = INT4 pool, 2 = tiered (owner test per row).  Replaces
+ * qwen_sparse_kv_extraction_compact_triton's int8 / int4 / tiered branches (_compact_kv_int8
+ * patches/kv_int8.py:365-420, _compact_kv_int4 patches/kv_int4.py:396-460, _compact_kv_tiered
+ * patches/kv_tiers.py:446-538, wrapper :688-737). */
+int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_scale, const void* v_scale,
+                       const void* ring_k, const void* ring_v, const void* ring_ks, const void* ring_vs,
+                       const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,
+                       const void* req_to_token, int64_t req_stride, const void* req_indices, int req_is_int64,
+                       const void* indices, int64_t idx_stride, const void* seq_lens, const void* cu_k,
+                       int cu_is_int64, int batch, int topk, int H, int D, int group8, void* out_k, void* out_v,
+                       void* stream);
+
+/* Whole-prefix gather-dequant: rows [0, seq_lens[b]) of request req_indices[b] packed at cu_k[b]; rows at or
+ * beyond seq_lens[b] are not written.  Replaces qwen_sparse_prefix_gather_dequant_{int8,int4,tiered}
+ * (patches/kv_int8.py:469-504, patches/kv_int4.py:519-557, patches/kv_tiers.py:639-683). */
+int kvt_prefix_gather(int kind, const void* k, const void* v, const void* k_scale, const void* v_scale,
+                      const void* ring_k, const void* ring_v, const void* ring_ks, const void* ring_vs,
+                      const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,
+                      const void* req_to_token, int64_t req_stride, const void* req_indices, int req_is_int64,
+                      const void* seq_lens, const void* cu_k, int cu_is_int64, int batch, int64_t max_len, int H,
+                      int D, int group8, void* out_k, void* out_v, void* stream);
+
+/* ----------------------------------------------------------------------------------------- decode attention */
+
+/* Split-K GQA decode attention, reference precision (exact bf16 dequant, fp32 softmax).  One query per sequence:
+ * q bf16 [batch, Hq, D] (batch stride q_stride_b elements).  mode 0 = position rings (ring_base/ring_len/
+ * ring_start per sequence + page_table), mode 1 = slot rings (req_to_token, req_indices int64, owner, ring_mask).
+ * Writes per (sequence, KV head, chunk) partials part_o fp32 [batch*H*n_chunks, Hq/H, D] and part_ml fp32
+ * [.., Hq/H, 2] (running max, sum of exp).  chunk <= 512.  Stands in for the reference's decode attention
+ * (top-k compact gather + flash_attn_varlen_func, flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882),
+ * dense over the whole context. */
+int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
+                   int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
+                   const void* rv, const void* rks, const void* rvs, const void* sm_k, const void* sm_v,
+                   const void* ring_base, const void* ring_len, const void* ring_start, const void* page_table,
+                   int64_t pt_stride, const void* req_to_token, int64_t req_stride, const void* req_indices,
+                   const void* owner, int64_t ring_mask, float scale, int chunk, int n_chunks, void* part_o,
+                   void* part_ml, void* stream);
+
+/* Merge the split-K partials: out[b, hq, :] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c (fp32 and/or bf16
+ * output, either may be NULL; batch stride out_stride_b elements).  An empty context yields NaN (0/0), as the
+ * reference's chunk kernel (gemv/test_kv_paged_prefix.py:524-526). */
+int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
+                       int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVTIER_H */

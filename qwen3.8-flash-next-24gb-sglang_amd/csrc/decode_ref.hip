@@ -1,0 +1,256 @@
+// Split-K GQA decode attention over the tiered cache, reference-precision variant, and the split combine.
+//
+// Every K/V element is dequantized exactly as the reference's gathers do (bf16(q * s * sm),
+// patches/kv_tiers.py:516-526) and the softmax attention runs in fp32 (the oracle form,
+// gemv/test_kv_paged_prefix.py:520-528).  It serves the slot-indexed (dual-write) layout, where the tier of a
+// token is only known from the owner table, and is the on-device cross-check of the MFMA kernel.
+//
+// Work item = (sequence, KV head, chunk of `chunk` positions); 256 threads:
+//   phase 1  thread-per-token scores for the GQA group's q heads (q * scale in LDS, fp32)
+//   phase 2  per-head max / exp / sum over the chunk in LDS
+//   phase 3  thread-per-channel P.V accumulation
+// and writes an unnormalized partial (m, l, o) per q head.  kvt_decode_combine merges the chunks.
+
+#include "kvt_common.h"
+
+using namespace kvt;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxChunk = 512;
+constexpr int kMaxGroup = 16;  // q heads per KV head
+
+struct TierArgs {
+  // pools (INT4 codes [rows, H, D/2], scales [rows, H, D/32]; INT8 ring [R, H, D], scales [R, H, D/G8])
+  const uint8_t* k4;
+  const uint8_t* v4;
+  const uint16_t* ks4;
+  const uint16_t* vs4;
+  const int8_t* rk;
+  const int8_t* rv;
+  const uint16_t* rks;
+  const uint16_t* rvs;
+  const uint16_t* sm_k;  // may be null (identity)
+  const uint16_t* sm_v;
+  // mode 0 (position rings): per sequence
+  const int64_t* ring_base;
+  const int32_t* ring_len;
+  const int64_t* ring_start;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  // mode 1 (slot rings): req_to_token[req_indices[b]][p] -> slot, owner table
+  const int32_t* req_to_token;
+  int64_t req_stride;
+  const int64_t* req_indices;
+  const int32_t* owner;
+  int64_t ring_mask;
+};
+
+// Resolve position p of sequence b to (hot, row): row is the ring row when hot, the INT4 pool row otherwise.
+template <int MODE>
+KVT_DEV bool resolve(const TierArgs& A, int b, int64_t p, int64_t hot_start, int64_t* row) {
+  if constexpr (MODE == 0) {
+    if (p >= hot_start) {
+      *row = A.ring_base[b] + (p & ((int64_t)A.ring_len[b] - 1));
+      return true;
+    }
+    *row = (int64_t)A.page_table[b * A.pt_stride + (p >> 6)] * kPage + (p & (kPage - 1));
+    return false;
+  } else {
+    const int64_t slot = A.req_to_token[A.req_indices[b] * A.req_stride + p];
+    const int64_t r = slot & A.ring_mask;
+    if ((int64_t)A.owner[r] == slot) {
+      *row = r;
+      return true;
+    }
+    *row = slot;
+    return false;
+  }
+}
+
+template <int D, int G8>
+KVT_DEV float dequant_elem(bool hot, const int8_t* r8, const uint16_t* rs8, const uint8_t* p4, const uint16_t* ps4,
+                           int64_t row, int H, int h, int c, const uint16_t* sm) {
+  float x;
+  if (hot) {
+    x = (float)r8[(row * H + h) * D + c] * f16_bits_to_f32(rs8[(row * H + h) * (D / G8) + c / G8]);
+  } else {
+    const uint32_t b = p4[(row * H + h) * (D / 2) + (c >> 1)];
+    const int n = (int)((c & 1) ? (b >> 4) : (b & 15u)) - 8;
+    x = (float)n * f16_bits_to_f32(ps4[(row * H + h) * (D / kG4) + c / kG4]);
+  }
+  if (sm) x *= f16_bits_to_f32(sm[h * D + c]);
+  return bf16_to_f32(bf16_rne(x));
+}
+
+template <int MODE, int D, int G8>
+__global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const uint16_t* q, int64_t q_stride_b,
+                                                              const int32_t* seq_lens, int H, int gs, int chunk,
+                                                              int n_chunks, float scale, float* part_o,
+                                                              float* part_ml) {
+  __shared__ float q_s[kMaxGroup * D];
+  __shared__ float p_s[kMaxGroup * kMaxChunk];
+  __shared__ float red[kThreads / 64][kMaxGroup];
+  const int c = blockIdx.x;
+  const int b = blockIdx.y / H;
+  const int h = blockIdx.y - b * H;
+  const int tid = threadIdx.x;
+  const int64_t L = seq_lens[b];
+  const int64_t p0 = (int64_t)c * chunk;
+  const int64_t item = ((int64_t)b * H + h) * n_chunks + c;
+  const int n = (int)max((int64_t)0, min((int64_t)chunk, L - p0));
+  int64_t hot_start = 0;
+  if constexpr (MODE == 0) hot_start = max(A.ring_start[b], L - (int64_t)A.ring_len[b]);
+
+  for (int i = tid; i < gs * D; i += kThreads) {
+    const int hq = i / D, d = i - hq * D;
+    q_s[i] = bf16_to_f32(q[b * q_stride_b + (int64_t)(h * gs + hq) * D + d]) * scale;
+  }
+  __syncthreads();
+
+  // phase 1: scores
+  for (int t = tid; t < n; t += kThreads) {
+    int64_t row;
+    const bool hot = resolve<MODE>(A, b, p0 + t, hot_start, &row);
+    float acc[kMaxGroup];
+    for (int j = 0; j < gs; ++j) acc[j] = 0.0f;
+    for (int d = 0; d < D; ++d) {
+      const float kv = dequant_elem<D, G8>(hot, A.rk, A.rks, A.k4, A.ks4, row, H, h, d, A.sm_k);
+      for (int j = 0; j < gs; ++j) acc[j] = fmaf(q_s[j * D + d], kv, acc[j]);
+    }
+    for (int j = 0; j < gs; ++j) p_s[j * kMaxChunk + t] = acc[j];
+  }
+  __syncthreads();
+
+  // phase 2: per-head max and sum of exp (each wave reduces all heads over its slice, then across waves)
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int j = 0; j < gs; ++j) {
+    float m = -INFINITY;
+    for (int t = tid; t < n; t += kThreads) m = fmaxf(m, p_s[j * kMaxChunk + t]);
+    m = group_max<64>(m);
+    if (lane == 0) red[wave][j] = m;
+  }
+  __syncthreads();
+  float mrow[kMaxGroup];
+  for (int j = 0; j < gs; ++j) {
+    float m = red[0][j];
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red[w][j]);
+    mrow[j] = m;
+  }
+  __syncthreads();
+  for (int j = 0; j < gs; ++j) {
+    float s = 0.0f;
+    for (int t = tid; t < n; t += kThreads) {
+      const float e = expf(p_s[j * kMaxChunk + t] - mrow[j]);
+      p_s[j * kMaxChunk + t] = e;
+      s += e;
+    }
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) red[wave][j] = s;
+  }
+  __syncthreads();
+  if (tid < gs) {
+    float s = 0.0f;
+    for (int w = 0; w < kThreads / 64; ++w) s += red[w][tid];
+    part_ml[(item * gs + tid) * 2 + 0] = n > 0 ? mrow[tid] : -INFINITY;
+    part_ml[(item * gs + tid) * 2 + 1] = s;
+  }
+
+  // phase 3: o[j][d] = sum_t p[j][t] * v[t][d]
+  for (int d = tid; d < D; d += kThreads) {
+    float acc[kMaxGroup];
+    for (int j = 0; j < gs; ++j) acc[j] = 0.0f;
+    for (int t = 0; t < n; ++t) {
+      int64_t row;
+      const bool hot = resolve<MODE>(A, b, p0 + t, hot_start, &row);
+      const float vv = dequant_elem<D, G8>(hot, A.rv, A.rvs, A.v4, A.vs4, row, H, h, d, A.sm_v);
+      for (int j = 0; j < gs; ++j) acc[j] = fmaf(p_s[j * kMaxChunk + t], vv, acc[j]);
+    }
+    for (int j = 0; j < gs; ++j) part_o[(item * gs + j) * D + d] = acc[j];
+  }
+}
+
+// out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the chunks of (b, hq / gs).
+// grid (Hq, batch); block D threads.  An empty context gives 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
+__global__ void decode_combine_kernel(const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks,
+                                      int64_t chunk, const int32_t* seq_lens, float* out_f32, uint16_t* out_bf16,
+                                      int64_t out_stride_b) {
+  const int hq = blockIdx.x;
+  const int b = blockIdx.y;
+  const int h = hq / gs, j = hq - h * gs;
+  const int64_t L = seq_lens[b];
+  const int used = (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk);
+  const int64_t base = ((int64_t)b * H + h) * n_chunks;
+  float M = -INFINITY;
+  for (int c = 0; c < used; ++c) M = fmaxf(M, part_ml[((base + c) * gs + j) * 2]);
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float num = 0.0f, den = 0.0f;
+    for (int c = 0; c < used; ++c) {
+      const float mc = part_ml[((base + c) * gs + j) * 2];
+      const float w = expf(mc - M);
+      num = fmaf(w, part_o[((base + c) * gs + j) * D + d], num);
+      den = fmaf(w, part_ml[((base + c) * gs + j) * 2 + 1], den);
+    }
+    const float o = num / den;
+    const int64_t oi = b * out_stride_b + (int64_t)hq * D + d;
+    if (out_f32) out_f32[oi] = o;
+    if (out_bf16) out_bf16[oi] = bf16_rne(o);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// mode 0: position rings + page tables; mode 1: slot rings + owner table (req_to_token).
+int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
+                   int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
+                   const void* rv, const void* rks, const void* rvs, const void* sm_k, const void* sm_v,
+                   const void* ring_base, const void* ring_len, const void* ring_start, const void* page_table,
+                   int64_t pt_stride, const void* req_to_token, int64_t req_stride, const void* req_indices,
+                   const void* owner, int64_t ring_mask, float scale, int chunk, int n_chunks, void* part_o,
+                   void* part_ml, void* stream) {
+  if (batch <= 0 || H <= 0 || Hq % H != 0) return KVT_EINVAL;
+  const int gs = Hq / H;
+  if (gs > kMaxGroup || chunk <= 0 || chunk > kMaxChunk || n_chunks <= 0) return KVT_EINVAL;
+  TierArgs A{(const uint8_t*)k4,      (const uint8_t*)v4,         (const uint16_t*)ks4,       (const uint16_t*)vs4,
+             (const int8_t*)rk,       (const int8_t*)rv,          (const uint16_t*)rks,       (const uint16_t*)rvs,
+             (const uint16_t*)sm_k,   (const uint16_t*)sm_v,      (const int64_t*)ring_base,  (const int32_t*)ring_len,
+             (const int64_t*)ring_start, (const int32_t*)page_table, pt_stride,               (const int32_t*)req_to_token,
+             req_stride,              (const int64_t*)req_indices, (const int32_t*)owner,     ring_mask};
+  const dim3 grid((unsigned)n_chunks, (unsigned)(batch * H));
+  hipStream_t st = (hipStream_t)stream;
+#define KVT_DR(MODE_, D_, G_)                                                                                     \
+  hipLaunchKernelGGL((decode_ref_kernel<MODE_, D_, G_>), grid, dim3(kThreads), 0, st, A, (const uint16_t*)q,      \
+                     q_stride_b, (const int32_t*)seq_lens, H, gs, chunk, n_chunks, scale, (float*)part_o,        \
+                     (float*)part_ml)
+  if (D != 256) return KVT_EINVAL;
+  if (mode == 0 && group8 == 64) {
+    KVT_DR(0, 256, 64);
+  } else if (mode == 0 && group8 == 256) {
+    KVT_DR(0, 256, 256);
+  } else if (mode == 1 && group8 == 64) {
+    KVT_DR(1, 256, 64);
+  } else if (mode == 1 && group8 == 256) {
+    KVT_DR(1, 256, 256);
+  } else {
+    return KVT_EINVAL;
+  }
+#undef KVT_DR
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
+}
+
+int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
+                       int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
+                       void* stream) {
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk <= 0) return KVT_EINVAL;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)Hq, (unsigned)batch), dim3(256), 0, (hipStream_t)stream,
+                     (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
+                     (const int32_t*)seq_lens, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b);
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
+}
+
+}  // extern "C"

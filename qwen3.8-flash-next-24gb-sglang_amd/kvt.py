@@ -1,0 +1,294 @@
+"""Position-indexed tiered KV cache (evict mode) and the decode-attention entry points.
+
+The reference writes every token twice (INT4 row + INT8 ring row, slot-indexed ring, patches/kv_tiers.py:4-16).
+This module adds the mode the reference specifies but never built: the ring holds the newest R positions of each
+sequence (row = ring_base + position mod R) and a token leaving the ring is requantized INT8 -> INT4-G32 into the
+page of its position (docs/KV_TIERS_PLAN.md:53, :63-67, :82).  Pages come from a host free list in a seeded
+random order and are recorded in a per-sequence page table (int32 [S, max_pages]) by a device kernel.
+
+    cache = PosTieredCache(layers, H, D, n_pages, ring_total, max_seqs, max_pages, device)
+    s = cache.add_seq(ring_len=8192)
+    plan = cache.plan_append([s], [n])      # positions, new pages (page-table update launch)
+    for layer: cache.append(layer, plan, k, v)
+    cache.commit(plan)
+    out = kvt_decode_attn(cache, layer, q)  # split-K over INT4 pages + INT8 ring
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+
+PAGE = 64
+G4 = 32
+
+
+class PageAllocator:
+    """Host free list of physical INT4 pages in a seeded random order ("physical pages randomly permuted from
+    seed"): pop() hands them out in that order."""
+
+    def __init__(self, n_pages: int, seed: int = 0):
+        g = torch.Generator().manual_seed(seed)
+        self.free: List[int] = torch.randperm(n_pages, generator=g).tolist()
+        self.next = 0
+
+    def pop(self) -> int:
+        if self.next >= len(self.free):
+            raise RuntimeError("INT4 page pool exhausted")
+        p = self.free[self.next]
+        self.next += 1
+        return p
+
+    @property
+    def n_free(self) -> int:
+        return len(self.free) - self.next
+
+
+@dataclass
+class AppendPlan:
+    seq_ids: torch.Tensor      # int32 [N] device
+    positions: torch.Tensor    # int64 [N] device
+    counts: List[int]
+    seqs: List[int]
+
+    @property
+    def n(self) -> int:
+        return int(self.seq_ids.numel())
+
+
+class PosTieredCache:
+    """Per layer: INT4 pool k4/v4 uint8 [n_pages * 64, H, D // 2] + fp16 scales [.., H, D // 32], INT8 ring rk/rv
+    int8 [ring_total, H, D] + fp16 scales [ring_total, H, D // group8].  Shared by all layers: per-sequence ring
+    placement (ring_base, ring_len, ring_start), lengths and the page table."""
+
+    def __init__(self, layers: int, H: int, D: int, n_pages: int, ring_total: int, max_seqs: int, max_pages: int,
+                 device="cuda", group8: int = 64, page_seed: int = 0, sm: bool = False):
+        assert D == 256, "the kernels are built for head_dim 256"
+        assert group8 in (64, D)
+        self.L, self.H, self.D, self.group8 = layers, H, D, group8
+        self.device = torch.device(device)
+        rows = n_pages * PAGE
+        z = dict(device=self.device)
+        self.k4 = [torch.zeros(rows, H, D // 2, dtype=torch.uint8, **z) for _ in range(layers)]
+        self.v4 = [torch.zeros(rows, H, D // 2, dtype=torch.uint8, **z) for _ in range(layers)]
+        self.ks4 = [torch.zeros(rows, H, D // G4, dtype=torch.float16, **z) for _ in range(layers)]
+        self.vs4 = [torch.zeros(rows, H, D // G4, dtype=torch.float16, **z) for _ in range(layers)]
+        self.rk = [torch.zeros(ring_total, H, D, dtype=torch.int8, **z) for _ in range(layers)]
+        self.rv = [torch.zeros(ring_total, H, D, dtype=torch.int8, **z) for _ in range(layers)]
+        self.rks = [torch.zeros(ring_total, H, D // group8, dtype=torch.float16, **z) for _ in range(layers)]
+        self.rvs = [torch.zeros(ring_total, H, D // group8, dtype=torch.float16, **z) for _ in range(layers)]
+        self.sm_k = self.sm_v = self.sm_k_inv = self.sm_v_inv = None   # identity smoothing
+        self.ring_total = ring_total
+        self.max_seqs, self.max_pages = max_seqs, max_pages
+        self.page_table = torch.full((max_seqs, max_pages), -1, dtype=torch.int32, **z)
+        self.ring_base = torch.zeros(max_seqs, dtype=torch.int64, **z)
+        self.ring_len = torch.ones(max_seqs, dtype=torch.int32, **z)
+        self.ring_start = torch.zeros(max_seqs, dtype=torch.int64, **z)
+        self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, **z)
+        self.alloc = PageAllocator(n_pages, page_seed)
+        self._ring_used = 0
+        # host mirror
+        self.h_len: List[int] = []
+        self.h_ring: List[tuple] = []       # (base, len, start)
+        self.h_pages: List[List[int]] = []
+
+    # -- sequences
+    @property
+    def n_seqs(self) -> int:
+        return len(self.h_len)
+
+    def add_seq(self, ring_len: int, ring_start: int = 0, shared_pages: Sequence[int] = ()) -> int:
+        """New sequence with its own ring of ring_len rows (a power of two).  Positions below ring_start come from
+        shared_pages (physical INT4 pages already holding a common prefix; paged-prefix reuse)."""
+        assert ring_len > 0 and ring_len & (ring_len - 1) == 0, "ring_len must be a power of two"
+        assert len(shared_pages) * PAGE >= ring_start and ring_start % PAGE == 0
+        s = self.n_seqs
+        assert s < self.max_seqs
+        if self._ring_used + ring_len > self.ring_total:
+            raise RuntimeError("ring rows exhausted")
+        base = self._ring_used
+        self._ring_used += ring_len
+        self.h_len.append(ring_start)
+        self.h_ring.append((base, ring_len, ring_start))
+        self.h_pages.append(list(shared_pages))
+        self.ring_base[s] = base
+        self.ring_len[s] = ring_len
+        self.ring_start[s] = ring_start
+        self.seq_lens[s] = ring_start
+        if shared_pages:
+            self.page_table[s, :len(shared_pages)] = torch.tensor(list(shared_pages), dtype=torch.int32)
+        return s
+
+    def hot_start(self, s: int) -> int:
+        base, R, start = self.h_ring[s]
+        return max(start, self.h_len[s] - R)
+
+    # -- write path
+    def plan_append(self, seqs: Sequence[int], counts: Sequence[int]) -> AppendPlan:
+        """Positions of the next counts[i] tokens of seqs[i]; pages the evictions of this append enter for the first
+        time are popped from the allocator and written into the device page table (one small launch)."""
+        sid, pos, upd_s, upd_l, upd_p = [], [], [], [], []
+        for s, n in zip(seqs, counts):
+            base, R, start = self.h_ring[s]
+            assert 0 <= n <= R, f"{n} tokens in one append exceed the ring of {R}"
+            L0 = self.h_len[s]
+            for p in range(L0, L0 + n):
+                e = p - R
+                if e >= start and e % PAGE == 0:
+                    lp = e // PAGE
+                    assert lp == len(self.h_pages[s]), "page table out of order"
+                    if lp >= self.max_pages:
+                        raise RuntimeError("page table row full")
+                    phys = self.alloc.pop()
+                    self.h_pages[s].append(phys)
+                    upd_s.append(s)
+                    upd_l.append(lp)
+                    upd_p.append(phys)
+            sid.extend([s] * n)
+            pos.extend(range(L0, L0 + n))
+        dev = self.device
+        if upd_s:
+            upd = torch.tensor([upd_s, upd_l, upd_p], dtype=torch.int32).to(dev)
+            _lib.call("kvt_page_table_update", self.page_table.data_ptr(), self.page_table.stride(0), len(upd_s),
+                      upd[0].data_ptr(), upd[1].data_ptr(), upd[2].data_ptr(), _lib.stream())
+        return AppendPlan(torch.tensor(sid, dtype=torch.int32).to(dev), torch.tensor(pos, dtype=torch.int64).to(dev),
+                          list(counts), list(seqs))
+
+    def append(self, layer: int, plan: AppendPlan, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Quantize-append the plan's tokens (k, v: [N, H, D] bf16/fp16/fp32) into layer `layer`."""
+        N = plan.n
+        assert k.shape == (N, self.H, self.D) and v.shape == k.shape and k.stride(2) == 1 and v.stride(2) == 1
+        assert k.dtype == v.dtype and k.dtype in _lib.DTYPE_CODE
+        if N == 0:
+            return
+        _lib.require_device(k, v)
+        _lib.call("kvt_append_evict", k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[k.dtype], k.stride(0), k.stride(1),
+                  v.stride(0), v.stride(1), plan.seq_ids.data_ptr(), plan.positions.data_ptr(), N, self.H, self.D,
+                  self.k4[layer].data_ptr(), self.v4[layer].data_ptr(), self.ks4[layer].data_ptr(),
+                  self.vs4[layer].data_ptr(), self.rk[layer].data_ptr(), self.rv[layer].data_ptr(),
+                  self.rks[layer].data_ptr(), self.rvs[layer].data_ptr(), self.ring_base.data_ptr(),
+                  self.ring_len.data_ptr(), self.ring_start.data_ptr(), self.page_table.data_ptr(),
+                  self.page_table.stride(0), None, None, self.group8, _lib.stream())
+
+    def commit(self, plan: AppendPlan) -> None:
+        """Advance the sequence lengths after every layer has been written."""
+        for s, n in zip(plan.seqs, plan.counts):
+            self.h_len[s] += n
+        idx = torch.tensor(plan.seqs, dtype=torch.int64)
+        add = torch.tensor(plan.counts, dtype=torch.int32)
+        self.seq_lens.index_add_(0, idx.to(self.device), add.to(self.device))
+
+    # -- byte accounting (algorithmic HBM bytes of one decode step over one layer)
+    def kv_bytes(self, seqs: Optional[Sequence[int]] = None) -> int:
+        """KV payload + scale bytes a decode step reads per layer: hot tokens x (2 D + 2 * 2 D / group8) and cold
+        tokens x (D + 2 * 2 D / 32), per KV head (K and V)."""
+        seqs = range(self.n_seqs) if seqs is None else seqs
+        hot_b = self.H * 2 * (self.D + 2 * (self.D // self.group8))
+        cold_b = self.H * 2 * (self.D // 2 + 2 * (self.D // G4))
+        tot = 0
+        for s in seqs:
+            hs = self.hot_start(s)
+            tot += (self.h_len[s] - hs) * hot_b + hs * cold_b
+        return tot
+
+
+def _choose_chunk(max_len: int, items: int, lo: int = 64, hi: int = 512) -> int:
+    """Tokens per split: enough work items to fill the chip (>= 512 blocks) but at most hi tokens each."""
+    want = max(1, 512 // max(1, items))
+    c = max(lo, min(hi, -(-max_len // want)))
+    return int(min(hi, 1 << (c - 1).bit_length()))
+
+
+def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
+                    impl: str = "ref", chunk: Optional[int] = None, max_len: Optional[int] = None,
+                    out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
+                    events: Optional[list] = None) -> torch.Tensor:
+    """Decode attention of one query token per sequence over the tiered cache of `layer`.
+
+    q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
+    every position of each sequence, K/V dequantized from the INT4 pages (positions < hot_start) and the INT8 ring.
+    events: if a list, a (start, end) pair of timing events recorded around the split-K kernel is appended.
+    """
+    S = cache.n_seqs
+    assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == cache.D and q.dtype == torch.bfloat16
+    assert q.stride(2) == 1 and q.stride(1) == cache.D
+    Hq = q.shape[1]
+    H, D = cache.H, cache.D
+    assert Hq % H == 0
+    gs = Hq // H
+    if max_len is None:
+        max_len = max(cache.h_len) if S else 0
+    if chunk is None:
+        chunk = _choose_chunk(max_len, S * H)
+    n_chunks = max(1, -(-max_len // chunk))
+    ws = workspace if workspace is not None else {}
+    need_o = S * H * n_chunks * gs * D
+    po = ws.get("part_o")
+    if po is None or po.numel() < need_o:
+        po = torch.empty(need_o, dtype=torch.float32, device=q.device)
+        pml = torch.empty(S * H * n_chunks * gs * 2, dtype=torch.float32, device=q.device)
+        ws["part_o"], ws["part_ml"] = po, pml
+    pml = ws["part_ml"]
+    if out is None:
+        out = torch.empty(S, Hq, D, dtype=out_dtype, device=q.device)
+    assert out.shape == (S, Hq, D) and out.is_contiguous()
+    scale = 1.0 / math.sqrt(D)
+    _lib.require_device(q, out)
+    if events is not None:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    if impl == "ref":
+        _lib.call("kvt_decode_ref", 0, q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8,
+                  cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
+                  cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
+                  cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), None, None, cache.ring_base.data_ptr(),
+                  cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
+                  cache.page_table.stride(0), None, 0, None, None, 0, scale, chunk, n_chunks, po.data_ptr(),
+                  pml.data_ptr(), _lib.stream())
+    else:
+        raise ValueError(f"unknown decode implementation {impl!r}")
+    if events is not None:
+        ev1.record()
+        events.append((ev0, ev1))
+    _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), S, H, Hq, D, n_chunks, chunk,
+              cache.seq_lens.data_ptr(), out.data_ptr() if out.dtype == torch.float32 else None,
+              out.data_ptr() if out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
+    return out
+
+
+def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, ring_mask,
+                      sm_k=None, sm_v=None, out_dtype=torch.float32, chunk: Optional[int] = None,
+                      max_len: Optional[int] = None) -> torch.Tensor:
+    """Decode attention over the slot-indexed (dual-write) tiered pool: position p of request b is slot
+    req_to_token[req_indices[b], p], hot when owner[slot & ring_mask] == slot (patches/kv_tiers.py:500-504).
+    q: bf16 [B, Hq, D]; seq_lens int32 [B]; req_indices int64 [B].  Returns [B, Hq, D]."""
+    B, Hq, D = q.shape
+    H = k4.shape[1]
+    assert k4.shape[2] * 2 == D and q.dtype == torch.bfloat16 and q.stride(2) == 1 and q.stride(1) == D
+    assert req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1
+    assert req_indices.dtype == torch.int64 and seq_lens.dtype == torch.int32
+    g8 = D // rks.shape[-1]
+    if max_len is None:
+        max_len = int(seq_lens.max())
+    if chunk is None:
+        chunk = _choose_chunk(max_len, B * H)
+    n_chunks = max(1, -(-max_len // chunk))
+    gs = Hq // H
+    po = torch.empty(B * H * n_chunks * gs * D, dtype=torch.float32, device=q.device)
+    pml = torch.empty(B * H * n_chunks * gs * 2, dtype=torch.float32, device=q.device)
+    out = torch.empty(B, Hq, D, dtype=out_dtype, device=q.device)
+    _lib.require_device(q, k4, owner)
+    _lib.call("kvt_decode_ref", 1, q.data_ptr(), q.stride(0), seq_lens.data_ptr(), B, H, Hq, D, g8, k4.data_ptr(),
+              v4.data_ptr(), ks4.data_ptr(), vs4.data_ptr(), rk.data_ptr(), rv.data_ptr(), rks.data_ptr(),
+              rvs.data_ptr(), _lib.ptr(sm_k), _lib.ptr(sm_v), None, None, None, None, 0, req_to_token.data_ptr(),
+              req_to_token.stride(0), req_indices.data_ptr(), owner.data_ptr(), int(ring_mask), 1.0 / math.sqrt(D),
+              chunk, n_chunks, po.data_ptr(), pml.data_ptr(), _lib.stream())
+    _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), B, H, Hq, D, n_chunks, chunk, seq_lens.data_ptr(),
+              out.data_ptr() if out_dtype == torch.float32 else None,
+              out.data_ptr() if out_dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
+    return out

@@ -1,0 +1,123 @@
+"""GPU parity of split-K decode attention over the tiered cache against the oracle (fp32 softmax over the
+bf16-dequantized rows, gemv/test_kv_paged_prefix.py:520-528).
+
+Tolerances: the reference-precision kernel dequantizes exactly like the oracle and accumulates in fp32, so it is
+held to 2e-5 max-abs; the MFMA kernel to the stated bound 2e-3 max-abs / 1e-3 mean-abs.
+"""
+import pytest
+import torch
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+H, D, HQ = 2, 256, 16
+SCALE = D ** -0.5
+
+
+def _build(lens, rings, seed=0, n_pages=None, chunk=512, starts=None):
+    """Device and oracle caches with the same appended tokens (configuration-style K with outlier channels)."""
+    from kvtier.kvt import PosTieredCache
+    gen = torch.Generator().manual_seed(seed)
+    n_pages = n_pages or sum(max(0, l - r) // 64 + 2 for l, r in zip(lens, rings))
+    ring_total = sum(rings)
+    dc = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=ring_total, max_seqs=len(lens),
+                        max_pages=max(lens) // 64 + 2, device=dev, page_seed=seed + 1)
+    oc = ref.PosTieredCache(H, D, n_pages=n_pages, ring_total=ring_total)
+    alloc = ref.PageAllocator(n_pages, seed=seed + 1)
+    base = 0
+    for r in rings:
+        dc.add_seq(r)
+        oc.add_seq(base, r)
+        base += r
+    och = ref.outlier_channels(H, D, 8, gen)
+    done = [0] * len(lens)
+    while any(d < l for d, l in zip(done, lens)):
+        seqs = [s for s in range(len(lens)) if done[s] < lens[s]]
+        cnt = [min(chunk, rings[s], lens[s] - done[s]) for s in seqs]
+        plan = dc.plan_append(seqs, cnt)
+        ks, vs = [], []
+        for s, n in zip(seqs, cnt):
+            xk, xv = ref.make_kv(n, H, D, gen, och)
+            oc.plan_pages(s, n, alloc)
+            oc.append(s, xk, xv)
+            ks.append(xk); vs.append(xv)
+        dc.append(0, plan, torch.cat(ks).to(dev), torch.cat(vs).to(dev))
+        dc.commit(plan)
+        for s, n in zip(seqs, cnt):
+            done[s] += n
+    q = ref.make_q(HQ, D, gen, n=len(lens))
+    return dc, oc, q
+
+
+def _oracle_out(oc, q):
+    outs = []
+    for s in range(q.shape[0]):
+        kk, vv = oc.rows(s)
+        outs.append(ref.attention_rows(q[s], kk, vv, SCALE))
+    return torch.stack(outs)
+
+
+@pytest.mark.parametrize("impl,tol", [("ref", 2e-5)])
+def test_decode_pos_rings(kvt_pkg, impl, tol):
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([3000, 700, 130, 64], [1024, 512, 256, 128], seed=1)
+    torch.cuda.synchronize()
+    out = kvt_decode_attn(dc, 0, q.to(dev), impl=impl).cpu()
+    exp = _oracle_out(oc, q)
+    err = (out - exp).abs()
+    assert float(err.max()) < tol and float(err.mean()) < tol / 2, (float(err.max()), float(err.mean()))
+
+
+def test_decode_pos_single_and_empty(kvt_pkg):
+    """A single-token context returns exactly its V row; an empty context is NaN (0/0)."""
+    from kvtier.kvt import PosTieredCache, kvt_decode_attn
+    dc, oc, q = _build([1, 5], [64, 64], seed=2)
+    out = kvt_decode_attn(dc, 0, q.to(dev), impl="ref").cpu()
+    kk, vv = oc.rows(0)
+    assert torch.equal(out[0, :8], vv[0, 0].float().expand(8, D)) and torch.equal(out[0, 8:], vv[0, 1].float().expand(8, D))
+    empty = PosTieredCache(1, H, D, n_pages=2, ring_total=64, max_seqs=1, max_pages=2, device=dev)
+    empty.add_seq(64)
+    o = kvt_decode_attn(empty, 0, q[:1].to(dev), impl="ref", max_len=1)
+    assert torch.isnan(o).all()
+
+
+def test_decode_slot_rings_config0(kvt_pkg):
+    """The CPU-plumbing configuration on the GPU: 4,096 tokens appended one at a time through the dual-write path
+    (R = 512, per-(token, head) INT8, identity slots), then one decode step; codes bit-exact, output vs oracle."""
+    from kvtier import sparse_attn as sa
+    from kvtier.kvt import decode_attn_slots
+    gen = torch.Generator().manual_seed(0)
+    N, R = 4096, 512
+    och = ref.outlier_channels(H, D, 8, gen)
+    xk, xv = ref.make_kv(N, H, D, gen, och)
+    q = ref.make_q(HQ, D, gen)
+    k4 = torch.zeros(N, H, D // 2, dtype=torch.uint8, device=dev); v4 = torch.zeros_like(k4)
+    ks4 = torch.zeros(N, H, 8, dtype=torch.float16, device=dev); vs4 = torch.zeros_like(ks4)
+    rk = torch.zeros(R, H, D, dtype=torch.int8, device=dev); rv = torch.zeros_like(rk)
+    rks = torch.zeros(R, H, 1, dtype=torch.float16, device=dev); rvs = torch.zeros_like(rks)
+    owner = torch.full((R,), -1, dtype=torch.int32, device=dev)
+    ones = torch.ones(H, D, dtype=torch.float16, device=dev)
+    xk_d, xv_d = xk.to(dev), xv.to(dev)
+    locs = torch.arange(N, dtype=torch.int32, device=dev)
+    for t in range(N):
+        sa.quant_store_kv_tiered(xk_d[t:t + 1], xv_d[t:t + 1], locs[t:t + 1], k4, v4, ks4, vs4, rk, rv, rks, rvs, owner,
+                                 ones, ones, R - 1)
+    torch.cuda.synchronize()
+    e = [torch.zeros(N, H, D // 2, dtype=torch.uint8), torch.zeros(N, H, D // 2, dtype=torch.uint8),
+         torch.zeros(N, H, 8, dtype=torch.float16), torch.zeros(N, H, 8, dtype=torch.float16),
+         torch.zeros(R, H, D, dtype=torch.int8), torch.zeros(R, H, D, dtype=torch.int8),
+         torch.zeros(R, H, 1, dtype=torch.float16), torch.zeros(R, H, 1, dtype=torch.float16),
+         torch.full((R,), -1, dtype=torch.int32)]
+    for a in range(0, N, R):
+        ref.quant_store_tiered(xk[a:a + R], xv[a:a + R], torch.arange(a, a + R), *e, None, None, R - 1, group8=256)
+    got = [t.cpu() for t in (k4, v4, ks4, vs4, rk, rv, rks, rvs, owner)]
+    for i in range(9):
+        assert torch.equal(got[i], e[i]), i
+    rtt = torch.arange(N, dtype=torch.int32, device=dev)[None]
+    out = decode_attn_slots(q.to(dev), torch.tensor([N], dtype=torch.int32, device=dev), rtt,
+                            torch.zeros(1, dtype=torch.int64, device=dev), k4, v4, ks4, vs4, rk, rv, rks, rvs, owner,
+                            R - 1).cpu()
+    kk, vv = ref.dequant_slots_tiered(torch.arange(N), *e, R - 1, group8=256)
+    exp = ref.attention_rows(q[0], kk, vv, SCALE)
+    assert float((out[0] - exp).abs().max()) < 2e-5
