@@ -74,7 +74,7 @@ def pack4(q: torch.Tensor) -> torch.Tensor:
 def unpack4(p: torch.Tensor) -> torch.Tensor:
     """uint8 [..., D // 2] -> int32 [..., D] (gemv/test_kv_int4.py:49-52)."""
     b = p.to(torch.int32)
-    return torch.stack([(b & 15) - 8, (b >> 4) - 8], dim=-1).reshape(*p.shape[:-1], -1)
+    return torch.stack([(b & 15) - 8, (b >> 4) - 8], dim=-1).reshape(*p.shape[:-1], 2 * p.shape[-1])
 
 
 def quant4(x: torch.Tensor, sm_inv: Optional[torch.Tensor] = None):
