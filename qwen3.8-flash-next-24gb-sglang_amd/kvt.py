@@ -197,10 +197,19 @@ class PosTieredCache:
 
 
 def _choose_chunk(max_len: int, items: int, lo: int = 64, hi: int = 512) -> int:
-    """Tokens per split: enough work items to fill the chip (>= 512 blocks) but at most hi tokens each."""
+    """Tokens per split for the reference-precision kernel: enough work items to fill the chip (>= 512 blocks),
+    at most hi tokens each."""
     want = max(1, 512 // max(1, items))
     c = max(lo, min(hi, -(-max_len // want)))
     return int(min(hi, 1 << (c - 1).bit_length()))
+
+
+def _choose_chunk_mfma(max_len: int, items: int, blocks: int = 512) -> int:
+    """Tokens per split of the MFMA kernel: a multiple of 128 (4 wavefronts x 32-token tiles), sized so that
+    about `blocks` work items cover the longest context (2 blocks per CU on 256 CUs), at most 4096."""
+    c = -(-max_len * max(1, items) // blocks)
+    c = -(-c // 128) * 128
+    return int(min(4096, max(128, c)))
 
 
 def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
@@ -223,7 +232,7 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     if max_len is None:
         max_len = max(cache.h_len) if S else 0
     if chunk is None:
-        chunk = _choose_chunk(max_len, S * H)
+        chunk = _choose_chunk_mfma(max_len, S * H) if impl == "mfma" else _choose_chunk(max_len, S * H)
     n_chunks = max(1, -(-max_len // chunk))
     ws = workspace if workspace is not None else {}
     need_o = S * H * n_chunks * gs * D
@@ -250,6 +259,13 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
                   cache.page_table.stride(0), None, 0, None, None, 0, scale, chunk, n_chunks, po.data_ptr(),
                   pml.data_ptr(), _lib.stream())
+    elif impl == "mfma":
+        _lib.call("kvt_decode_mfma", q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8,
+                  cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
+                  cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
+                  cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
+                  cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
+                  cache.page_table.stride(0), scale, chunk, n_chunks, po.data_ptr(), pml.data_ptr(), _lib.stream())
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
