@@ -1,21 +1,24 @@
 // Split-K GQA decode attention over the position-indexed tiered cache on gfx950 matrix cores.
 //
-// Work item = (sequence, KV head, split of `chunk` positions); 4 wavefronts per block, each owning a quarter of
-// the split, which it walks in sub-chunks of 128 positions: cold positions (< hot_start) read INT4-G32 pages through
-// the page table, hot positions the INT8 ring row (position mod R).
+// Work item = (sequence, KV head, split of `chunk` positions); 4 wavefronts per block, each owning a quarter of the
+// split, which it walks in sub-chunks of 128 positions: cold positions (< hot_start) read INT4-G32 pages through the
+// page table, hot positions the INT8 ring row (position mod R).  GQA groups of up to 8 q heads per KV head.
 //
 // QK^T on v_mfma_f32_16x16x32_f16, one instruction per 16 tokens x 32 channels (= one INT4 scale group):
-//   A = K codes as exact fp16 integers (16 tokens x 32 channels); B = Q (32 channels x 16 columns, the GQA group's
-//   q heads, zero beyond the group).  The fp16 codes come from the magic-number conversion
-//   (0x6400 | nibble) = 1024 + nibble, minus 1032 (for the high nibble: (1024 + 16 n) / 16 - 72); channels appear in
-//   the order [0,4,1,5,2,6,3,7] of each 8, and Q is loaded in the same order (a contraction is order-free).
-//   The per-(token, group) fp16 scale is folded into the fp32 group result: score += s_g(t) * D_g.
-// Softmax: scores sit in the MFMA D layout (lane = q head, 4 tokens of each 16-token tile); that layout is exactly
-//   the A operand of P.V (lane = q head, 8 tokens), so P needs no transpose.  exp2 with the log2(e) factor folded
-//   into the score scale; the running max is rescaled only when it grows (wave-uniform test).
-// P.V on the same instruction: A = P (fp16), B = V dequantized to fp16 (code * scale, exact code conversion then one
-//   packed multiply by the per-(token, group) scale pair), 16 instructions per 32 tokens, fp32 accumulators.
-// The four wavefronts merge their (max, sum, o) in LDS; one fp32 partial per work item goes to kvt_decode_combine.
+//   A = K codes as exact fp16 integers (row = token), B = Q (32 channels x 16 columns: the group's q heads in
+//   columns 0-7 and again in 8-15).  Codes come from the magic-number conversion (0x6400 | nibble) = 1024 + nibble,
+//   minus 1032 (high nibble: (1024 + 16 n) / 16 - 72), channels in the order [0,4,1,5,2,6,3,7] of each 8 with Q
+//   loaded in the same order.  The per-(token, group) fp16 scale is folded into the fp32 group result:
+//   score += s_g(t) * D_g.
+// Softmax: scores stay in the D layout (lane = q head, 4 tokens of each 16-token tile), which is the A operand
+//   layout of P.V, so P needs no transpose.  exp2 with log2(e) folded into the score scale; the running max is
+//   rescaled only when it grows (wave-uniform test).
+// P.V, block-diagonal: a 16 x 16 accumulator tile holds 8 heads x 16 dims in rows 0-7 and the same 8 heads x 16
+//   other dims in rows 8-15.  Because columns 8-15 of Q duplicate 0-7, lane (row m >= 8) holds P of head m - 8;
+//   A_X = (m < 8 ? own P : 0) with B = V(own tokens, dims A) and A_Y = (m >= 8 ? P of lane ^ 32 : 0) with
+//   B = V(tokens of lane ^ 32, dims B) accumulate into the same tile: 32 accumulator registers for 256 dims.
+//   V is dequantized to fp16 (exact code conversion, then one packed multiply by the per-(token, group) scale pair).
+// The four wavefronts merge (max, sum, o) in LDS; one fp32 partial per work item goes to kvt_decode_combine.
 //
 // Numerics versus the oracle (bf16(code * scale) rows, fp32 softmax): K enters exactly (integer codes, fp32 scale
 // fold); V as fp16(code * scale) (finer than the oracle's bf16 rounding); P as fp16; fp32 accumulation.  V entries
@@ -31,6 +34,7 @@ namespace {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kSub = 128;      // positions per wave sub-chunk (8 QK tiles of 16, 4 PV tiles of 32)
@@ -57,14 +61,23 @@ KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f1
 
 KVT_DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+KVT_DEV h8 as_h8(u4v u) { return __builtin_bit_cast(h8, u); }
+KVT_DEV u4v as_u4(h8 h) { return __builtin_bit_cast(u4v, h); }
+
+// (a & m) | o in one VOP3 instruction (the compiler otherwise splits it in two around the literal constants).
+KVT_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
+  return r;
+}
 
 // 8 INT4 codes (one dword, channels c0..c7 = nibbles 0..7) -> fp16 (c - 8) in the order [c0,c4,c1,c5,c2,c6,c3,c7].
-KVT_DEV h8 int4_codes_to_h8(uint32_t w) {
+KVT_DEV h8 int4_codes_to_h8(uint32_t w, uint32_t mlo, uint32_t mhi, uint32_t magic) {
   const uint32_t w8 = w >> 8;
-  const h2 lo0 = as_h2((w & 0x000F000Fu) | 0x64006400u);   // 1024 + (c0, c4)
-  const h2 hi0 = as_h2((w & 0x00F000F0u) | 0x64006400u);   // 1024 + 16 (c1, c5)
-  const h2 lo1 = as_h2((w8 & 0x000F000Fu) | 0x64006400u);  // 1024 + (c2, c6)
-  const h2 hi1 = as_h2((w8 & 0x00F000F0u) | 0x64006400u);  // 1024 + 16 (c3, c7)
+  const h2 lo0 = as_h2(and_or(w, mlo, magic));    // 1024 + (c0, c4)
+  const h2 hi0 = as_h2(and_or(w, mhi, magic));    // 1024 + 16 (c1, c5)
+  const h2 lo1 = as_h2(and_or(w8, mlo, magic));   // 1024 + (c2, c6)
+  const h2 hi1 = as_h2(and_or(w8, mhi, magic));   // 1024 + 16 (c3, c7)
   const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
   const h2 sc = {(_Float16)0.0625f, (_Float16)0.0625f};
   const h2 off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -83,16 +96,6 @@ KVT_DEV h8 int8_codes_to_h8(uint32_t w0, uint32_t w1) {
   return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
-// Row of position p of sequence b (cold: INT4 pool row through the page table; hot: ring row).
-template <bool HOT>
-KVT_DEV int64_t pos_row(const PosArgs& A, int b, int64_t p, int64_t rbase, int64_t rmask) {
-  if constexpr (HOT) {
-    return rbase + (p & rmask);
-  } else {
-    return (int64_t)A.page_table[b * A.pt_stride + (p >> 6)] * kPage + (p & (kPage - 1));
-  }
-}
-
 struct WaveLds {
   int32_t rows[kSub];
   uint16_t sk[kSub][8];   // K scales, [token][group]
@@ -101,13 +104,13 @@ struct WaveLds {
 
 struct Lds {
   WaveLds w[kWaves];
-  float m[kWaves][16];
-  float l[kWaves][16];
-  float o[16][kD];
+  float m[kWaves][8];
+  float l[kWaves][8];
+  float o[8][kD];
 };
 
-// Q of this lane (q head n = lane % 16, channel block kb = lane / 16) as 8 MFMA B operands, one per 32-channel
-// step: INT4 order [0,4,1,5,2,6,3,7] (PERM) or natural (INT8).  Zero beyond the GQA group.
+// Q (q head n % 8 of the group, channel block kb) as 8 MFMA B operands, one per 32-channel step: INT4 order
+// [0,4,1,5,2,6,3,7] (PERM) or natural (INT8).  Zero for heads beyond the group.
 template <bool PERM>
 KVT_DEV void load_q(const uint16_t* qrow, bool valid, int kb, h8 qop[8]) {
   constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
@@ -121,23 +124,39 @@ KVT_DEV void load_q(const uint16_t* qrow, bool valid, int kb, h8 qop[8]) {
   }
 }
 
+KVT_DEV void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // One sub-chunk (up to kSub positions starting at p0, n valid) of one segment type.
 template <bool HOT, int G8>
 KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_t p0, int n, int64_t rbase,
-                       int64_t rmask, const h8 qop[8], float cscale, f4 acc[16], float& m_run, float& l_run) {
+                       int64_t rmask, const h8 qop[8], float cscale, f4 acc[8], float& m_run, float& l_run) {
   const int lane = threadIdx.x & 63;
   const int n16 = lane & 15, kb = lane >> 4;
   constexpr int NG8 = kD / G8;
+  constexpr uint32_t kRowStride4 = kD / 2;   // INT4 bytes per (row, head)
+  const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  wave_sync();
   // ---- stage rows and scales of the sub-chunk (2 positions per lane)
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int t = lane + 64 * i;
     const bool ok = t < n;
-    const int64_t row = pos_row<HOT>(A, b, p0 + (ok ? t : 0), rbase, rmask);
-    L.rows[t] = (int32_t)row;
+    const int64_t p = p0 + (ok ? t : 0);
+    int32_t row;
+    if constexpr (HOT) {
+      row = (int32_t)(rbase + (p & rmask));
+    } else {
+      row = A.page_table[b * A.pt_stride + (p >> 6)] * kPage + (int32_t)(p & (kPage - 1));
+    }
+    L.rows[t] = row;
+    const uint32_t srow = (uint32_t)row * (uint32_t)H + (uint32_t)h;
     if constexpr (!HOT) {
-      const uint4 ks = *reinterpret_cast<const uint4*>(A.ks4 + (row * H + h) * 8);
-      uint4 vs = *reinterpret_cast<const uint4*>(A.vs4 + (row * H + h) * 8);
+      const uint4 ks = *reinterpret_cast<const uint4*>(A.ks4 + srow * 8u);
+      uint4 vs = *reinterpret_cast<const uint4*>(A.vs4 + srow * 8u);
       if (!ok) vs = make_uint4(0, 0, 0, 0);
       *reinterpret_cast<uint4*>(&L.sk[t][0]) = ks;
       const uint32_t v[4] = {vs.x, vs.y, vs.z, vs.w};
@@ -149,30 +168,27 @@ KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_
     } else {
 #pragma unroll
       for (int g = 0; g < NG8; ++g) {
-        L.sk[t][g] = A.rks[(row * H + h) * NG8 + g];
-        L.sv[g][t] = ok ? A.rvs[(row * H + h) * NG8 + g] : (uint16_t)0;
+        L.sk[t][g] = A.rks[srow * NG8 + g];
+        L.sv[g][t] = ok ? A.rvs[srow * NG8 + g] : (uint16_t)0;
       }
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  wave_sync();
 
-  // ---- QK^T: 8 tiles of 16 tokens; lane holds scores of q head n16 for tokens 16 nt + 4 kb + r
+  // ---- QK^T: 8 tiles of 16 tokens; lane holds scores of q head n16 % 8 for tokens 16 nt + 4 kb + r
   float s[8][4];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    const int trow = 16 * nt + n16;  // token of this lane's A-operand row
-    const int64_t row = L.rows[trow];
+    const uint32_t row = (uint32_t)L.rows[16 * nt + n16];   // token of this lane's A-operand row
     f4 sc = {0.f, 0.f, 0.f, 0.f};
     if constexpr (!HOT) {
-      const uint32_t* kp = reinterpret_cast<const uint32_t*>(A.k4 + (row * H + h) * (kD / 2)) + kb;
+      const uint32_t* kp = reinterpret_cast<const uint32_t*>(A.k4 + (row * (uint32_t)H + h) * kRowStride4) + kb;
       uint32_t w[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) w[g] = kp[4 * g];
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
-        const f4 d = mfma(int4_codes_to_h8(w[g]), qop[g], f4{0.f, 0.f, 0.f, 0.f});
+        const f4 d = mfma(int4_codes_to_h8(w[g], mlo, mhi, magic), qop[g], f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float sg = f16_bits_to_f32(L.sk[16 * nt + 4 * kb + r][g]);
@@ -180,7 +196,7 @@ KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_
         }
       }
     } else {
-      const uint2* kp = reinterpret_cast<const uint2*>(A.rk + (row * H + h) * kD) + kb;
+      const uint2* kp = reinterpret_cast<const uint2*>(A.rk + (row * (uint32_t)H + h) * (uint32_t)kD) + kb;
       uint2 w[8];
 #pragma unroll
       for (int st = 0; st < 8; ++st) w[st] = kp[4 * st];
@@ -200,10 +216,12 @@ KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_
         }
       }
     }
+    if (n == kSub) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = 16 * nt + 4 * kb + r;
-      s[nt][r] = t < n ? sc[r] * cscale : -INFINITY;
+      for (int r = 0; r < 4; ++r) s[nt][r] = sc[r] * cscale;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
     }
   }
 
@@ -217,14 +235,14 @@ KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_
   mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
   const float m_new = fmaxf(m_run, mloc);
   if (__any(m_new > m_run)) {
-    const float alpha = exp2f(m_run - m_new);   // 0 on the first sub-chunk (m_run = -inf)
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // 0 on the first sub-chunk (m_run = -inf)
     l_run *= alpha;
-    // acc rows are q heads 4 kb + i: fetch each head's alpha from its owner lane (head column)
+    // accumulator rows are q heads (4 kb + i) % 8: fetch each row's alpha from a lane of that head
     float arow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);
+    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, (4 * kb + i) & 7, 64);
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[j][i] *= arow[i];
   }
@@ -234,93 +252,118 @@ KVT_DEV void sub_chunk(const PosArgs& A, WaveLds& L, int b, int H, int h, int64_
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      s[nt][r] = exp2f(s[nt][r] - m_new);
+      s[nt][r] = __builtin_amdgcn_exp2f(s[nt][r] - m_new);
       psum += s[nt][r];
     }
   l_run += psum;
 
-  // ---- P.V: 4 tiles of 32 tokens; k slot e of lane (kb) = token 32 pt + (e < 4 ? 4 kb + e : 16 + 4 kb + e - 4)
+  // ---- P.V: 4 tiles of 32 tokens; k slot e of lane block kb = token 32 pt + (e < 4 ? 4 kb + e : 16 + 4 kb + e - 4)
+  const int kbp = kb ^ 2;                 // block of the partner lane (lane ^ 32)
+  const bool lowrow = n16 < 8;
+  const int cblk_a = n16, cblk_b = n16 + 16;   // 8-dim blocks: dims A = 8 n16 + e, dims B = 8 (n16 + 16) + e
 #pragma unroll
   for (int pt = 0; pt < 4; ++pt) {
-    const h8 pa = {(_Float16)s[2 * pt][0],     (_Float16)s[2 * pt][1],     (_Float16)s[2 * pt][2],
-                   (_Float16)s[2 * pt][3],     (_Float16)s[2 * pt + 1][0], (_Float16)s[2 * pt + 1][1],
-                   (_Float16)s[2 * pt + 1][2], (_Float16)s[2 * pt + 1][3]};
-    int tok[8];
-    int64_t rows[8];
+    const h8 pown = {(_Float16)s[2 * pt][0],     (_Float16)s[2 * pt][1],     (_Float16)s[2 * pt][2],
+                     (_Float16)s[2 * pt][3],     (_Float16)s[2 * pt + 1][0], (_Float16)s[2 * pt + 1][1],
+                     (_Float16)s[2 * pt + 1][2], (_Float16)s[2 * pt + 1][3]};
+    const u4v po = as_u4(pown);
+    u4v pp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pp[i] = (uint32_t)__shfl_xor((int)po[i], 32, 64);
+    const u4v zero = {0u, 0u, 0u, 0u};
+    const h8 ax = as_h8(lowrow ? po : zero);
+    const h8 ay = as_h8(lowrow ? zero : pp);
+    int tok_o[8], tok_p[8];
+    uint32_t row_o[8], row_p[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      tok[e] = 32 * pt + (e < 4 ? 4 * kb + e : 16 + 4 * kb + e - 4);
-      rows[e] = L.rows[tok[e]];
+      const int te = e < 4 ? e : 12 + e;    // 0..3, 16..19
+      tok_o[e] = 32 * pt + 4 * kb + te;
+      tok_p[e] = 32 * pt + 4 * kbp + te;
+      row_o[e] = (uint32_t)L.rows[tok_o[e]];
+      row_p[e] = (uint32_t)L.rows[tok_p[e]];
     }
+    if constexpr (!HOT) {
+      const int ga = cblk_a >> 2, gb = cblk_b >> 2;   // INT4 scale group of each dim block
+      uint32_t wo[8], wp[8];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int cblk = n16 + 16 * half;     // this lane's 8-dim block: dims 8 cblk .. 8 cblk + 7
-      if constexpr (!HOT) {
-        const int g = cblk >> 2;            // INT4 scale group of those dims
-        uint32_t w[8];
+      for (int e = 0; e < 8; ++e) {
+        wo[e] = reinterpret_cast<const uint32_t*>(A.v4 + (row_o[e] * (uint32_t)H + h) * kRowStride4)[cblk_a];
+        wp[e] = reinterpret_cast<const uint32_t*>(A.v4 + (row_p[e] * (uint32_t)H + h) * kRowStride4)[cblk_b];
+      }
+      h2 so[4], sp[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          w[e] = reinterpret_cast<const uint32_t*>(A.v4 + (rows[e] * H + h) * (kD / 2))[cblk];
-        h2 spair[4];
+      for (int pr = 0; pr < 4; ++pr) {
+        so[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[ga][tok_o[2 * pr]]));
+        sp[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[gb][tok_p[2 * pr]]));
+      }
+      const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+      const h2 sc16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+      const h2 off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
 #pragma unroll
-        for (int pr = 0; pr < 4; ++pr)
-          spair[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[g][tok[2 * pr]]));
-        const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-        const h2 sc16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-        const h2 off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
+      for (int byte = 0; byte < 4; ++byte) {
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
+        h8 olo, ohi, plo, phi;
 #pragma unroll
-        for (int byte = 0; byte < 4; ++byte) {
-          h8 blo, bhi;
-#pragma unroll
-          for (int pr = 0; pr < 4; ++pr) {
-            const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
-            const uint32_t x = __builtin_amdgcn_perm(w[2 * pr + 1], w[2 * pr], sel);  // [b(t0), 0, b(t1), 0]
-            const h2 lo = (as_h2((x & 0x000F000Fu) | 0x64006400u) + off) * spair[pr];
-            const h2 hi = (as_h2((x & 0x00F000F0u) | 0x64006400u) * sc16 + off2) * spair[pr];
-            blo[2 * pr] = lo.x;
-            blo[2 * pr + 1] = lo.y;
-            bhi[2 * pr] = hi.x;
-            bhi[2 * pr + 1] = hi.y;
-          }
-          acc[8 * half + 2 * byte] = mfma(pa, blo, acc[8 * half + 2 * byte]);
-          acc[8 * half + 2 * byte + 1] = mfma(pa, bhi, acc[8 * half + 2 * byte + 1]);
+        for (int pr = 0; pr < 4; ++pr) {
+          const uint32_t xo = __builtin_amdgcn_perm(wo[2 * pr + 1], wo[2 * pr], sel);  // [b(t0), 0, b(t1), 0]
+          const uint32_t xp = __builtin_amdgcn_perm(wp[2 * pr + 1], wp[2 * pr], sel);
+          const h2 lo_o = (as_h2(and_or(xo, mlo, magic)) + off) * so[pr];
+          const h2 hi_o = (as_h2(and_or(xo, mhi, magic)) * sc16 + off2) * so[pr];
+          const h2 lo_p = (as_h2(and_or(xp, mlo, magic)) + off) * sp[pr];
+          const h2 hi_p = (as_h2(and_or(xp, mhi, magic)) * sc16 + off2) * sp[pr];
+          olo[2 * pr] = lo_o.x; olo[2 * pr + 1] = lo_o.y;
+          ohi[2 * pr] = hi_o.x; ohi[2 * pr + 1] = hi_o.y;
+          plo[2 * pr] = lo_p.x; plo[2 * pr + 1] = lo_p.y;
+          phi[2 * pr] = hi_p.x; phi[2 * pr + 1] = hi_p.y;
         }
-      } else {
-        const int g = (8 * cblk) / G8;      // INT8 scale group of those dims
-        uint2 w[8];
+        acc[2 * byte] = mfma(ax, olo, acc[2 * byte]);
+        acc[2 * byte] = mfma(ay, plo, acc[2 * byte]);
+        acc[2 * byte + 1] = mfma(ax, ohi, acc[2 * byte + 1]);
+        acc[2 * byte + 1] = mfma(ay, phi, acc[2 * byte + 1]);
+      }
+    } else {
+      const int ga = (8 * cblk_a) / G8, gb = (8 * cblk_b) / G8;   // INT8 scale groups of the dim blocks
+      uint2 wo[8], wp[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          w[e] = reinterpret_cast<const uint2*>(A.rv + (rows[e] * H + h) * kD)[cblk];
-          w[e].x ^= 0x80808080u;
-          w[e].y ^= 0x80808080u;
+      for (int e = 0; e < 8; ++e) {
+        wo[e] = reinterpret_cast<const uint2*>(A.rv + (row_o[e] * (uint32_t)H + h) * (uint32_t)kD)[cblk_a];
+        wp[e] = reinterpret_cast<const uint2*>(A.rv + (row_p[e] * (uint32_t)H + h) * (uint32_t)kD)[cblk_b];
+        wo[e].x ^= 0x80808080u; wo[e].y ^= 0x80808080u;
+        wp[e].x ^= 0x80808080u; wp[e].y ^= 0x80808080u;
+      }
+      h2 so[4], sp[4];
+#pragma unroll
+      for (int pr = 0; pr < 4; ++pr) {
+        so[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[ga][tok_o[2 * pr]]));
+        sp[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[gb][tok_p[2 * pr]]));
+      }
+      const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t bsel = (uint32_t)(q & 3);
+        const uint32_t sel = 0x0C000C00u | ((4 + bsel) << 16) | bsel;
+        h8 bo, bp;
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          const uint32_t xo = __builtin_amdgcn_perm(q < 4 ? wo[2 * pr + 1].x : wo[2 * pr + 1].y,
+                                                    q < 4 ? wo[2 * pr].x : wo[2 * pr].y, sel);
+          const uint32_t xp = __builtin_amdgcn_perm(q < 4 ? wp[2 * pr + 1].x : wp[2 * pr + 1].y,
+                                                    q < 4 ? wp[2 * pr].x : wp[2 * pr].y, sel);
+          const h2 vo = (as_h2(xo | magic) + off) * so[pr];
+          const h2 vp = (as_h2(xp | magic) + off) * sp[pr];
+          bo[2 * pr] = vo.x; bo[2 * pr + 1] = vo.y;
+          bp[2 * pr] = vp.x; bp[2 * pr + 1] = vp.y;
         }
-        h2 spair[4];
-#pragma unroll
-        for (int pr = 0; pr < 4; ++pr)
-          spair[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&L.sv[g][tok[2 * pr]]));
-        const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          h8 bv;
-#pragma unroll
-          for (int pr = 0; pr < 4; ++pr) {
-            const uint32_t a0 = q < 4 ? w[2 * pr].x : w[2 * pr].y;
-            const uint32_t a1 = q < 4 ? w[2 * pr + 1].x : w[2 * pr + 1].y;
-            const uint32_t bsel = (uint32_t)(q & 3);
-            const uint32_t x = __builtin_amdgcn_perm(a1, a0, 0x0C000C00u | ((4 + bsel) << 16) | bsel);
-            const h2 v = (as_h2(x | 0x64006400u) + off) * spair[pr];
-            bv[2 * pr] = v.x;
-            bv[2 * pr + 1] = v.y;
-          }
-          acc[8 * half + q] = mfma(pa, bv, acc[8 * half + q]);
-        }
+        acc[q] = mfma(ax, bo, acc[q]);
+        acc[q] = mfma(ay, bp, acc[q]);
       }
     }
   }
 }
 
 template <int G8>
-__global__ void __launch_bounds__(256) decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b,
                                                           const int32_t* seq_lens, int H, int gs, int chunk,
                                                           int n_chunks, float scale, float* part_o, float* part_ml) {
   __shared__ Lds lds;
@@ -338,12 +381,13 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(PosArgs A, const uint1
   const int64_t w0 = (int64_t)c * chunk + (int64_t)wave * cw;
   const int64_t w1 = min(w0 + cw, L);
   const float cscale = scale * kLog2e;
-  const uint16_t* qrow = q + b * q_stride_b + (int64_t)(h * gs + min(n16, gs - 1)) * kD;
-  const bool qvalid = n16 < gs;
+  const int hq = n16 & 7;
+  const bool qvalid = hq < gs;
+  const uint16_t* qrow = q + b * q_stride_b + (int64_t)(h * gs + (qvalid ? hq : 0)) * kD;
 
-  f4 acc[16];
+  f4 acc[8];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < 8; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   h8 qop[8];
 
@@ -364,36 +408,35 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(PosArgs A, const uint1
                           acc, m_run, l_run);
   }
 
-  // ---- merge the four wavefronts
+  // ---- merge the four wavefronts (heads 0-7 of the group; lanes n16 >= 8 duplicate n16 - 8)
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
-  if (kb == 0) {
+  if (kb == 0 && n16 < 8) {
     lds.m[wave][n16] = m_run;
     lds.l[wave][n16] = l_run;
   }
   __syncthreads();
-  // per acc row (q head 4 kb + i) the wave's weight exp2(m_wave - M)
   float wrow[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int hq = 4 * kb + i;
-    float M = lds.m[0][hq];
+    const int hr = (4 * kb + i) & 7;
+    float M = lds.m[0][hr];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds.m[w][hq]);
-    const float mw = lds.m[wave][hq];
-    wrow[i] = mw == -INFINITY ? 0.f : exp2f(mw - M);
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds.m[w][hr]);
+    const float mw = lds.m[wave][hr];
+    wrow[i] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
   }
   for (int w = 0; w < kWaves; ++w) {
     if (wave == w) {
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int dim = 8 * (n16 + 16 * (j >> 3)) + (j & 7);
+      for (int j = 0; j < 8; ++j) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int hq = 4 * kb + i;
+          const int r = 4 * kb + i;
+          const int dim = 8 * (n16 + (r >= 8 ? 16 : 0)) + j;
           const float v = acc[j][i] * wrow[i];
-          if (w == 0) lds.o[hq][dim] = v;
-          else lds.o[hq][dim] += v;
+          if (w == 0) lds.o[r & 7][dim] = v;
+          else lds.o[r & 7][dim] += v;
         }
       }
     }
@@ -401,8 +444,8 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(PosArgs A, const uint1
   }
   const int tid = threadIdx.x;
   for (int idx = tid; idx < gs * kD; idx += 256) {
-    const int hq = idx / kD, d = idx - hq * kD;
-    part_o[(item * gs + hq) * kD + d] = lds.o[hq][d];
+    const int hh = idx / kD, d = idx - hh * kD;
+    part_o[(item * gs + hh) * kD + d] = lds.o[hh][d];
   }
   if (tid < gs) {
     float M = lds.m[0][tid];
@@ -410,7 +453,7 @@ __global__ void __launch_bounds__(256) decode_mfma_kernel(PosArgs A, const uint1
     float l = 0.f;
     for (int w = 0; w < kWaves; ++w) {
       const float mw = lds.m[w][tid];
-      l += mw == -INFINITY ? 0.f : exp2f(mw - M) * lds.l[w][tid];
+      l += mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M) * lds.l[w][tid];
     }
     part_ml[(item * gs + tid) * 2 + 0] = M == -INFINITY ? -INFINITY : M / kLog2e;   // natural-log units
     part_ml[(item * gs + tid) * 2 + 1] = l;
@@ -428,7 +471,7 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                     int n_chunks, void* part_o, void* part_ml, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD) return KVT_EINVAL;
   const int gs = Hq / H;
-  if (gs > 16 || chunk <= 0 || chunk % (kWaves * 32) != 0 || n_chunks <= 0) return KVT_EINVAL;
+  if (gs > 8 || chunk <= 0 || chunk % (kWaves * 32) != 0 || n_chunks <= 0) return KVT_EINVAL;
   PosArgs A{(const uint8_t*)k4,         (const uint8_t*)v4,        (const uint16_t*)ks4,     (const uint16_t*)vs4,
             (const int8_t*)rk,          (const int8_t*)rv,         (const uint16_t*)rks,     (const uint16_t*)rvs,
             (const int64_t*)ring_base,  (const int32_t*)ring_len,  (const int64_t*)ring_start,

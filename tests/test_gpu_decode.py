@@ -194,3 +194,24 @@ def test_decode_slot_rings_config0(kvt_pkg):
     kk, vv = ref.dequant_slots_tiered(torch.arange(N), *e, R - 1, group8=256)
     exp = ref.attention_rows(q[0], kk, vv, SCALE)
     assert float((out[0] - exp).abs().max()) < 2e-5
+
+
+def test_decode_graph_replay(kvt_pkg):
+    """The decode step (split-K + combine, both layers) captured in a HIP graph: every replay, with eager work and
+    synchronizations in between, equals the eager result bit for bit."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([2500, 900], [1024, 512], seed=7)
+    qd = q.to(dev)
+    ws = {}
+    eager = kvt_decode_attn(dc, 0, qd, impl="mfma", workspace=ws).clone()
+    out = torch.empty_like(eager)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kvt_decode_attn(dc, 0, qd, out=out, impl="mfma", workspace=ws)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        _ = (qd.float() * 2).sum()          # unrelated eager work between replays
+        torch.cuda.synchronize()
