@@ -265,7 +265,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                   cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
                   cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
-                  cache.page_table.stride(0), scale, chunk, n_chunks, po.data_ptr(), pml.data_ptr(), _lib.stream())
+                  cache.page_table.stride(0), cache.k4[layer].shape[0], scale, chunk, n_chunks, po.data_ptr(),
+                  pml.data_ptr(), _lib.stream())
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
