@@ -132,8 +132,10 @@ def main():
     for _ in range(args.steps):
         step(kev)
     torch.cuda.synchronize()
-    kern_ms = [a.elapsed_time(b) for a, b in kev]
+    kern_ms = [a.elapsed_time(b) for a, b, _ in kev]
+    comb_ms = [b.elapsed_time(c) for _, b, c in kev]
     kern_avg_s = sum(kern_ms) / len(kern_ms) / 1e3
+    comb_avg_us = sum(comb_ms) / len(comb_ms) * 1e3
     bytes_layer = cache.kv_bytes()
     bytes_step = bytes_layer * LAYERS
     value = bytes_step / (ms_step / 1e3) / 1e9
@@ -177,6 +179,7 @@ def main():
             "traffic": traffic,
             "kernel": "decode split-K (per layer launch)",
             "kernel_avg_us": round(kern_avg_s * 1e6, 2),
+            "combine_avg_us": round(comb_avg_us, 2),
         },
         "cpu_baseline": cpu,
     }

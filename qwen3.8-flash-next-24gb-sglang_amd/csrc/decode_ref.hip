@@ -172,43 +172,71 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 }
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
-// grid (D / 64, Hq, batch), 256 threads: thread (d = tid % 64, part = tid / 64) folds splits c = part (mod 4) for
-// one output channel; the four parts meet in LDS.  An empty context gives 0/0 = NaN
-// (gemv/test_kv_paged_prefix.py:524-526).
-__global__ void __launch_bounds__(256) decode_combine_kernel(const float* part_o, const float* part_ml, int H, int gs,
-                                                             int D, int n_chunks, int64_t chunk,
-                                                             const int32_t* seq_lens, float* out_f32,
-                                                             uint16_t* out_bf16, int64_t out_stride_b) {
-  __shared__ float red[4][3][64];
-  __shared__ float mred[4];
+// grid (D / 64, Hq, batch), 1024 threads: thread (d = tid % 64, part = tid / 64) folds splits c = part (mod 16) for
+// one output channel, four independent loads in flight; the 16 parts meet in LDS.  An empty context gives
+// 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
+constexpr int kCombParts = 16;
+
+__global__ void __launch_bounds__(64 * kCombParts) decode_combine_kernel(const float* part_o, const float* part_ml,
+                                                                         int H, int gs, int D, int n_chunks,
+                                                                         int64_t chunk, const int32_t* seq_lens,
+                                                                         float* out_f32, uint16_t* out_bf16,
+                                                                         int64_t out_stride_b) {
+  __shared__ float red[kCombParts][2][64];
+  __shared__ float mred[kCombParts];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
   const int tid = threadIdx.x, dl = tid & 63, part = tid >> 6;
   const int d = blockIdx.x * 64 + dl;
   const int64_t L = seq_lens[b];
-  const int used = (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk);
+  // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
+  const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk) : n_chunks;
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
-  // M = max over the used splits (each wave scans a quarter, then LDS)
+  // M = max over the used splits (each wave scans 1/16, then LDS)
   float M = -INFINITY;
-  for (int c = (tid & 63) + 64 * part; c < used; c += 256) M = fmaxf(M, part_ml[((base + c) * gs + j) * 2]);
+  for (int c = tid; c < used; c += 64 * kCombParts) M = fmaxf(M, part_ml[((base + c) * gs + j) * 2]);
   M = group_max<64>(M);
   if (dl == 0) mred[part] = M;
   __syncthreads();
-  M = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+  M = mred[0];
+#pragma unroll
+  for (int p = 1; p < kCombParts; ++p) M = fmaxf(M, mred[p]);
   float num = 0.0f, den = 0.0f;
-  for (int c = part; c < used; c += 4) {
-    const float* ml = part_ml + ((base + c) * gs + j) * 2;
-    const float w = expf(ml[0] - M);
-    num = fmaf(w, part_o[((base + c) * gs + j) * D + d], num);
-    den = fmaf(w, ml[1], den);
+  int c = part;
+  for (; c + 3 * kCombParts < used; c += 4 * kCombParts) {
+    float mv[4], lv[4], ov[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t it = (base + c + u * kCombParts) * gs + j;
+      mv[u] = part_ml[it * 2];
+      lv[u] = part_ml[it * 2 + 1];
+      ov[u] = part_o[it * D + d];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float w = expf(mv[u] - M);
+      num = fmaf(w, ov[u], num);
+      den = fmaf(w, lv[u], den);
+    }
+  }
+  for (; c < used; c += kCombParts) {
+    const int64_t it = (base + c) * gs + j;
+    const float w = expf(part_ml[it * 2] - M);
+    num = fmaf(w, part_o[it * D + d], num);
+    den = fmaf(w, part_ml[it * 2 + 1], den);
   }
   red[part][0][dl] = num;
   red[part][1][dl] = den;
   __syncthreads();
   if (part == 0) {
-    num = red[0][0][dl] + red[1][0][dl] + red[2][0][dl] + red[3][0][dl];
-    den = red[0][1][dl] + red[1][1][dl] + red[2][1][dl] + red[3][1][dl];
+    num = 0.0f;
+    den = 0.0f;
+#pragma unroll
+    for (int p = 0; p < kCombParts; ++p) {
+      num += red[p][0][dl];
+      den += red[p][1][dl];
+    }
     const float o = num / den;
     const int64_t oi = b * out_stride_b + (int64_t)hq * D + d;
     if (out_f32) out_f32[oi] = o;
@@ -262,8 +290,9 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
                        int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
                        void* stream) {
-  if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk <= 0 || D % 64 != 0) return KVT_EINVAL;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / 64), (unsigned)Hq, (unsigned)batch), dim3(256), 0,
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % 64 != 0) return KVT_EINVAL;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / 64), (unsigned)Hq, (unsigned)batch),
+                     dim3(64 * kCombParts), 0,
                      (hipStream_t)stream,
                      (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
                      (const int32_t*)seq_lens, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b);

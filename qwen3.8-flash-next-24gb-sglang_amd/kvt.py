@@ -204,23 +204,23 @@ def _choose_chunk(max_len: int, items: int, lo: int = 64, hi: int = 512) -> int:
     return int(min(hi, 1 << (c - 1).bit_length()))
 
 
-def _choose_chunk_mfma(max_len: int, items: int, blocks: int = 512) -> int:
-    """Tokens per split of the MFMA kernel: a multiple of 128 (4 wavefronts x 32-token tiles), sized so that
-    about `blocks` work items cover the longest context (2 blocks per CU on 256 CUs), at most 4096."""
-    c = -(-max_len * max(1, items) // blocks)
-    c = -(-c // 128) * 128
-    return int(min(4096, max(128, c)))
+def _choose_splits_mfma(max_len: int, items: int, blocks: int = 512) -> int:
+    """Splits per (sequence, KV head) of the MFMA kernel: about `blocks` blocks in all (2 per CU on 256 CUs), each
+    wavefront (4 per split) with at least 64 positions."""
+    n = -(-blocks // max(1, items))
+    return int(max(1, min(n, -(-max_len // 256))))
 
 
 def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
                     impl: str = "ref", chunk: Optional[int] = None, max_len: Optional[int] = None,
                     out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
-                    events: Optional[list] = None) -> torch.Tensor:
+                    events: Optional[list] = None, splits: Optional[int] = None) -> torch.Tensor:
     """Decode attention of one query token per sequence over the tiered cache of `layer`.
 
     q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
     every position of each sequence, K/V dequantized from the INT4 pages (positions < hot_start) and the INT8 ring.
-    events: if a list, a (start, end) pair of timing events recorded around the split-K kernel is appended.
+    impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per (sequence, KV head).
+    events: if a list, timing events (start, after the split-K kernel, after the combine) are appended.
     """
     S = cache.n_seqs
     assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == cache.D and q.dtype == torch.bfloat16
@@ -231,9 +231,13 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     gs = Hq // H
     if max_len is None:
         max_len = max(cache.h_len) if S else 0
-    if chunk is None:
-        chunk = _choose_chunk_mfma(max_len, S * H) if impl == "mfma" else _choose_chunk(max_len, S * H)
-    n_chunks = max(1, -(-max_len // chunk))
+    if impl == "mfma":
+        n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)
+        chunk = 0   # every split holds a partial
+    else:
+        if chunk is None:
+            chunk = _choose_chunk(max_len, S * H)
+        n_chunks = max(1, -(-max_len // chunk))
     ws = workspace if workspace is not None else {}
     need_o = S * H * n_chunks * gs * D
     po = ws.get("part_o")
@@ -260,21 +264,26 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                   cache.page_table.stride(0), None, 0, None, None, 0, scale, chunk, n_chunks, po.data_ptr(),
                   pml.data_ptr(), _lib.stream())
     elif impl == "mfma":
+        if cache.rk[layer].numel() >= 2 ** 31:
+            raise ValueError("kvt_decode_mfma: ring buffers beyond 2^31 bytes per layer are not supported")
         _lib.call("kvt_decode_mfma", q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8,
                   cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
                   cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
                   cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
-                  cache.page_table.stride(0), cache.k4[layer].shape[0], scale, chunk, n_chunks, po.data_ptr(),
+                  cache.page_table.stride(0), cache.k4[layer].shape[0], scale, n_chunks, po.data_ptr(),
                   pml.data_ptr(), _lib.stream())
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
         ev1.record()
-        events.append((ev0, ev1))
     _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), S, H, Hq, D, n_chunks, chunk,
               cache.seq_lens.data_ptr(), out.data_ptr() if out.dtype == torch.float32 else None,
               out.data_ptr() if out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
+    if events is not None:
+        ev2 = torch.cuda.Event(enable_timing=True)
+        ev2.record()
+        events.append((ev0, ev1, ev2))
     return out
 
 

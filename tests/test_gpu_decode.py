@@ -73,14 +73,25 @@ def test_decode_pos_rings(kvt_pkg, impl, tol, mtol):
     assert float(err.max()) < tol and float(err.mean()) < mtol, (float(err.max()), float(err.mean()))
 
 
-@pytest.mark.parametrize("chunk", [128, 512, 1024, 2048])
-def test_decode_mfma_chunking(kvt_pkg, chunk):
-    """The MFMA kernel at several split sizes (one to many sub-chunks per wavefront) against the oracle."""
+@pytest.mark.parametrize("splits", [1, 3, 17, 64])
+def test_decode_mfma_splits(kvt_pkg, splits):
+    """The MFMA kernel at several split counts (one to many tiles and ring sub-chunks per wavefront, wavefront
+    ranges that straddle the paged / ring boundary, idle wavefronts) against the oracle."""
     from kvtier.kvt import kvt_decode_attn
     dc, oc, q = _build([5000, 2100], [2048, 1024], seed=3)
-    out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma", chunk=chunk).cpu()
+    out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma", splits=splits).cpu()
     err = (out - _oracle_out(oc, q)).abs()
-    assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (chunk, float(err.max()), float(err.mean()))
+    assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (splits, float(err.max()), float(err.mean()))
+
+
+def test_decode_mfma_page_windows(kvt_pkg):
+    """One split over 40,000 positions: each wavefront walks about 9,000 paged positions, i.e. several 64-page
+    windows of page ids."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([40000], [1024], seed=5, chunk=1024)
+    out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma", splits=1).cpu()
+    err = (out - _oracle_out(oc, q)).abs()
+    assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (float(err.max()), float(err.mean()))
 
 
 def test_decode_mfma_closed_forms(kvt_pkg):
