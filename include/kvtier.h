@@ -121,7 +121,7 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 /* Split-K GQA decode attention on the matrix cores (v_mfma_f32_16x16x32_f16) over position rings + page tables
  * (the mode-0 layout of kvt_decode_ref): QK^T with exact fp16 integer codes and the per-group scales folded in
  * fp32, P.V with fp16 P and fp16 code*scale values, fp32 accumulation.  Each (sequence, KV head) gets n_splits
- * partials (4 wavefront ranges each, of equal cost: a ring position weighs 7/4 of a paged one), in the layout of
+ * partials (4 wavefront ranges each, of equal cost), in the layout of
  * kvt_decode_ref; merge them with kvt_decode_combine(chunk = 0).  Hq / H <= 8, D = 256; pool_rows = rows of the
  * INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 < 2^31, else KVT_ERANGE).  No reference counterpart:
  * it replaces the compact gather + FA2 pair (flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for

@@ -2,7 +2,8 @@
 //
 // Work split: every (sequence, KV head) has n_splits blocks of 4 wavefronts.  The position range [0, L) is cut into
 // 4 * n_splits consecutive wavefront ranges of equal cost, where a ring position (INT8, 2 x 256 code bytes) costs
-// kHotCost4 / 4 of a paged position (INT4, 2 x 128 code bytes): the waves holding the ring finish with the others.
+// kHotCost4 / 4 of a paged position (INT4, 2 x 128 code bytes; the ring tile takes about the same time per position
+// as the paged tile): the waves holding the ring finish with the others.
 // Range boundaries inside the paged part are multiples of 32.  GQA groups of up to 8 q heads per KV head.
 //   Cold positions (< hot_start, INT4-G32 pages through the page table) stream in 32-token tiles: a 32-aligned tile
 //   lies in one 64-token page, i.e. 32 consecutive pool rows.  Each wavefront double-buffers its tiles in LDS with
@@ -50,7 +51,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 4;
 constexpr int kD = 256;
-constexpr int kHotCost4 = 7;    // cost of a ring position; a paged position costs 4
+constexpr int kHotCost4 = 4;    // cost of a ring position; a paged position costs 4 (measured: equal time)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct PosArgs {

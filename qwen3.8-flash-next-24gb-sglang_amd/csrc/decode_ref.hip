@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
 // grid (D / 64, Hq, batch), 1024 threads: thread (d = tid % 64, part = tid / 64) folds splits c = part (mod 16) for
-// one output channel, four independent loads in flight; the 16 parts meet in LDS.  An empty context gives
+// one output channel, sixteen independent loads in flight; the 16 parts meet in LDS.  An empty context gives
 // 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
 constexpr int kCombParts = 16;
 
@@ -204,17 +204,17 @@ __global__ void __launch_bounds__(64 * kCombParts) decode_combine_kernel(const f
   for (int p = 1; p < kCombParts; ++p) M = fmaxf(M, mred[p]);
   float num = 0.0f, den = 0.0f;
   int c = part;
-  for (; c + 3 * kCombParts < used; c += 4 * kCombParts) {
-    float mv[4], lv[4], ov[4];
+  for (; c + 15 * kCombParts < used; c += 16 * kCombParts) {   // 16 independent loads of each kind in flight
+    float mv[16], lv[16], ov[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 16; ++u) {
       const int64_t it = (base + c + u * kCombParts) * gs + j;
       mv[u] = part_ml[it * 2];
       lv[u] = part_ml[it * 2 + 1];
       ov[u] = part_o[it * D + d];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 16; ++u) {
       const float w = expf(mv[u] - M);
       num = fmaf(w, ov[u], num);
       den = fmaf(w, lv[u], den);
