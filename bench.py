@@ -86,6 +86,69 @@ def cpu_baseline(cache, q, layer: int = 0):
                        f"({nbytes} KV bytes, {dt:.2f} s)")
 
 
+CAL_BYTES = 256 * 1024 * 1024   # the calibration copy: 256 MiB read + 256 MiB written
+
+
+def pmc_sample(impl: str) -> None:
+    """The workload run under `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE): 12 eager decode layers (split-K +
+    combine) after a warm-up, then one device copy of CAL_BYTES whose counter reading calibrates the counter."""
+    import kvtier  # noqa: F401
+    from kvtier.kvt import kvt_decode_attn
+    cache, q = build_cache()
+    ws = {}
+    out = torch.empty(1, HQ, D, dtype=torch.float32, device="cuda")
+    for layer in range(LAYERS):
+        kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws)
+    torch.cuda.synchronize()
+    for layer in range(LAYERS):
+        kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws)
+    torch.cuda.synchronize()
+    src = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_sample": impl, "kv_bytes_per_layer": cache.kv_bytes(), "cal_bytes": CAL_BYTES}))
+
+
+def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, impl: str) -> None:
+    """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel from two rocprofv3 --pmc counter
+    CSVs, scaled by the ratio of the calibration copy's known bytes to its counter reading."""
+    import csv
+
+    def per_kernel(path, counter):
+        acc = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return acc
+
+    lines = []
+    res = {"impl": impl}
+    for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
+        acc = per_kernel(path, counter)
+        dec = [v for k, v in acc.items() if "decode_mfma_kernel" in k or "decode_ref_kernel" in k]
+        cal = [v for k, v in acc.items() if "copy" in k.lower() and max(v) * 1024 > CAL_BYTES / 4]
+        assert dec and cal, (counter, list(acc))
+        dec_v = [x for v in dec for x in v]
+        cal_v = max(cal, key=max)
+        cal_kib = max(cal_v)
+        factor = CAL_BYTES / (cal_kib * 1024)
+        dec_kib = sum(dec_v) / len(dec_v)
+        res[key] = {"counter_kib_per_dispatch": round(dec_kib, 1), "calibration_copy_kib": round(cal_kib, 1),
+                    "factor": round(factor, 4), "bytes_per_launch": round(dec_kib * 1024 * factor)}
+        lines.append(f"{counter}: decode kernel {dec_kib:.1f} KiB/dispatch over {len(dec_v)} dispatches; copy of "
+                     f"{CAL_BYTES} B {key}s {cal_kib:.1f} KiB -> factor {factor:.4f} -> {dec_kib * 1024 * factor:.0f} B")
+    res["hbm_bytes_per_launch"] = res["read"]["bytes_per_launch"] + res["write"]["bytes_per_launch"]
+    with open(out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    with open(out_txt, "a") as f:  # appended under the commands already written at the top of the file
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(res))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -93,7 +156,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--impl", default=os.environ.get("KVT_DECODE_IMPL", "mfma"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
+                    help="summarize two rocprofv3 --pmc counter CSVs into the traffic file and exit")
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary, impl=args.impl)
+        return
+    if args.pmc_sample:
+        pmc_sample(args.impl)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is a design in "
               "DESIGN.md, not a measured path", file=sys.stderr)
