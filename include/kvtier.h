@@ -141,6 +141,22 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
                        int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
                        void* stream);
 
+/* Causal prefill attention of a chunk of queries over the position-indexed tiered cache on the matrix cores
+ * (v_mfma_f32_16x16x32_f16, K/V tiles dequantized once per 16 queries into LDS).  Sequence b's queries are rows
+ * cu_q[b] .. cu_q[b+1] of q (bf16 [total_q, Hq, D], strides sq_n / sq_h) at positions kv_lens[b] - q_len .. ;
+ * each attends to every position <= its own (patches/kv_paged_prefix.py:200), read from the cache tiers of
+ * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16
+ * [positions, H, D] rows (the reference attends to fresh bf16 K/V there).  out: bf16 or fp32 (out_f32) with the
+ * layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
+ * chunks.  Hq / H <= 8, D = 256. */
+int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                     const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
+                     const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
+                     const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
+                     const void* ring_start, const void* page_table, int64_t pt_stride, const void* k_bf16,
+                     const void* v_bf16, int64_t kb_n, int64_t kb_h, int64_t vb_n, int64_t vb_h, float scale,
+                     void* out, int out_f32, int64_t so_n, int64_t so_h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,461 @@
+// Causal prefill attention over the position-indexed tiered cache on gfx950 matrix cores.
+//
+// The queries of a chunk (positions q0 .. q0 + n - 1 of a sequence whose cache already holds the chunk) attend to
+// every key position <= their own (patches/kv_paged_prefix.py:200: visible = j + kv_len - q_len + 1).  Keys and
+// values come from the cache tiers (INT4 pages below hot_start, INT8 ring above) or, for a chunk without a prefix,
+// from the chunk's own bf16 K/V (the reference attends to fresh bf16 K/V there).
+//
+// Work item = (sequence, KV head, tile of 16 queries), 4 wavefronts, heaviest (latest) query tiles first.  The block
+// walks the keys in tiles of 32 positions.  All 256 threads dequantize a tile ONCE into LDS as fp16 (K row-major,
+// V transposed), with the next tile's codes already loaded into registers during the matrix work on the current one;
+// the four wavefronts then reuse it for their 4 queries x 8 heads = 32 rows (dequantizing per query row is what made
+// the reference's fused kernel slow, docs/KV_PAGED_PREFIX_PLAN.md:188-191).
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 K rows x 32 channels from LDS (shared by the wavefront's two
+//   16-row blocks), B = Q (rows = 2 queries x 8 heads) held in registers, pre-multiplied by scale * log2(e).  The D
+//   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
+//   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
+//   O += P V on the same instruction: B = V^T rows from LDS (two 8-byte reads per 16-dim column block).
+// Numerics: fp16 K/V = code * scale (finer than the oracle's bf16 rows), fp16 Q * scale * log2(e) and P, fp32
+// accumulation and softmax; bf16 (as the reference) or fp32 output.
+
+#include "kvt_common.h"
+
+using namespace kvt;
+
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 256;
+constexpr int kQT = 16;                 // queries per block
+constexpr int kT = 32;                  // key positions per tile
+constexpr int kKPitch = kD * 2 + 16;    // bytes per fp16 K row in LDS (padded: spreads the 16 rows over the banks)
+constexpr int kVPitch = kT * 2 + 16;    // bytes per fp16 V^T row (one dim, 32 keys)
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct KVSrc {
+  const uint8_t* k4;
+  const uint8_t* v4;
+  const uint16_t* ks4;
+  const uint16_t* vs4;
+  const int8_t* rk;
+  const int8_t* rv;
+  const uint16_t* rks;
+  const uint16_t* rvs;
+  const int64_t* ring_base;
+  const int32_t* ring_len;
+  const int64_t* ring_start;
+  const int32_t* page_table;
+  int64_t pt_stride;
+  const uint16_t* kb;   // bf16 source [positions, H, D] (non-null: keys come from here, not from the cache)
+  const uint16_t* vb;
+  int64_t kb_n, kb_h, vb_n, vb_h;
+};
+
+struct __align__(16) Lds {
+  uint8_t k[kT * kKPitch];
+  uint8_t vt[kD * kVPitch];
+};
+
+KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
+KVT_DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Where a key position's row lives: kind 0 = INT4 pool row, 1 = INT8 ring row, 2 = bf16 source row, 3 = none.
+struct RowRef {
+  int64_t row;
+  int kind;
+};
+
+template <int G8>
+KVT_DEV RowRef locate(const KVSrc& S, int b, int64_t p, int64_t key_end, int64_t hs, int64_t rbase, int64_t rmask) {
+  RowRef r;
+  if (p >= key_end) {
+    r.row = 0;
+    r.kind = 3;
+  } else if (S.kb != nullptr) {
+    r.row = p;
+    r.kind = 2;
+  } else if (p >= hs) {
+    r.row = rbase + (p & rmask);
+    r.kind = 1;
+  } else {
+    r.row = (int64_t)S.page_table[b * S.pt_stride + (p >> 6)] * kPage + (p & (kPage - 1));
+    r.kind = 0;
+  }
+  return r;
+}
+
+// Raw codes of 32 consecutive channels (K: one token) or 2 x 16 channels (V: two tokens), loaded ahead of use.
+struct RawK {
+  uint4 w[4];
+  uint16_t s;
+  int kind;
+};
+struct RawV {
+  uint4 w[2][2];
+  uint16_t s[2];
+  int kind[2];
+};
+
+// K: channels 32 dc .. 32 dc + 31 of one key row.
+template <int G8>
+KVT_DEV RawK fetch_k(const KVSrc& S, RowRef r, int H, int h, int dc) {
+  RawK x;
+  x.kind = r.kind;
+  x.s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x.w[i] = make_uint4(0, 0, 0, 0);
+  const int64_t rh = r.row * H + h;
+  if (r.kind == 0) {
+    x.w[0] = *reinterpret_cast<const uint4*>(S.k4 + rh * (kD / 2) + 16 * dc);
+    x.s = S.ks4[rh * (kD / kG4) + dc];
+  } else if (r.kind == 1) {
+    const uint4* p = reinterpret_cast<const uint4*>(S.rk + rh * kD + 32 * dc);
+    x.w[0] = p[0];
+    x.w[1] = p[1];
+    x.s = S.rks[rh * (kD / G8) + (32 * dc) / G8];
+  } else if (r.kind == 2) {
+    const uint4* p = reinterpret_cast<const uint4*>(S.kb + r.row * S.kb_n + (int64_t)h * S.kb_h + 32 * dc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.w[i] = p[i];
+  }
+  return x;
+}
+
+// V: channels 16 db .. 16 db + 15 of key rows r0, r1.
+template <int G8>
+KVT_DEV RawV fetch_v(const KVSrc& S, RowRef r0, RowRef r1, int H, int h, int db) {
+  RawV x;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const RowRef r = t == 0 ? r0 : r1;
+    x.kind[t] = r.kind;
+    x.s[t] = 0;
+    x.w[t][0] = make_uint4(0, 0, 0, 0);
+    x.w[t][1] = make_uint4(0, 0, 0, 0);
+    const int64_t rh = r.row * H + h;
+    if (r.kind == 0) {
+      const uint2 c = *reinterpret_cast<const uint2*>(S.v4 + rh * (kD / 2) + 8 * db);
+      x.w[t][0] = make_uint4(c.x, c.y, 0, 0);
+      x.s[t] = S.vs4[rh * (kD / kG4) + db / 2];
+    } else if (r.kind == 1) {
+      x.w[t][0] = *reinterpret_cast<const uint4*>(S.rv + rh * kD + 16 * db);
+      x.s[t] = S.rvs[rh * (kD / G8) + (16 * db) / G8];
+    } else if (r.kind == 2) {
+      const uint4* p = reinterpret_cast<const uint4*>(S.vb + r.row * S.vb_n + (int64_t)h * S.vb_h + 16 * db);
+      x.w[t][0] = p[0];
+      x.w[t][1] = p[1];
+    }
+  }
+  return x;
+}
+
+// 8 INT4 codes (one dword, natural channel order c0..c7) -> 4 fp16 pairs (c0,c1) .. (c6,c7) = (code - 8) * s.
+KVT_DEV void int4_pairs(uint32_t w, h2 s2, uint32_t out[4]) {
+  const h2 mul = {(_Float16)1.0f, (_Float16)0.0625f};
+  const h2 add = {(_Float16)-1032.0f, (_Float16)-72.0f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // byte i into bytes 0 and 2, then low nibble -> half 0, high nibble (<< 4) -> half 1
+    const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)i << 16) | (uint32_t)i);
+    const uint32_t m = (x & 0x00F0000Fu) | 0x64006400u;
+    out[i] = as_u32((as_h2(m) * mul + add) * s2);
+  }
+}
+
+// 4 INT8 codes (one dword) -> 2 fp16 pairs = code * s.
+KVT_DEV void int8_pairs(uint32_t w, h2 s2, uint32_t out[2]) {
+  const uint32_t u = w ^ 0x80808080u;
+  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  out[0] = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off) * s2);
+  out[1] = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off) * s2);
+}
+
+// 2 bf16 (one dword) -> 2 fp16.
+KVT_DEV uint32_t bf16x2_to_f16x2(uint32_t w) {
+  const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xffff0000u);
+  const h2 r = {(_Float16)lo, (_Float16)hi};
+  return as_u32(r);
+}
+
+// K row fragment -> LDS (fp16, natural order): 32 channels = 64 bytes.
+KVT_DEV void store_k(const RawK& x, uint8_t* dst) {
+  uint32_t o[16];
+  const h2 s2 = as_h2((uint32_t)x.s | ((uint32_t)x.s << 16));
+  if (x.kind == 0) {
+    const uint32_t w[4] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) int4_pairs(w[i], s2, o + 4 * i);
+  } else if (x.kind == 1) {
+    const uint32_t w[8] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w, x.w[1].x, x.w[1].y, x.w[1].z, x.w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) int8_pairs(w[i], s2, o + 2 * i);
+  } else if (x.kind == 2) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[4 * i + 0] = bf16x2_to_f16x2(x.w[i].x);
+      o[4 * i + 1] = bf16x2_to_f16x2(x.w[i].y);
+      o[4 * i + 2] = bf16x2_to_f16x2(x.w[i].z);
+      o[4 * i + 3] = bf16x2_to_f16x2(x.w[i].w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *reinterpret_cast<uint4*>(dst + 16 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+// 16 channels of one V row -> 8 fp16 pairs (natural order).
+KVT_DEV void v_row16(const uint4 w[2], uint16_t s, int kind, uint32_t o[8]) {
+  const h2 s2 = as_h2((uint32_t)s | ((uint32_t)s << 16));
+  if (kind == 0) {
+    int4_pairs(w[0].x, s2, o);
+    int4_pairs(w[0].y, s2, o + 4);
+  } else if (kind == 1) {
+    const uint32_t c[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) int8_pairs(c[i], s2, o + 2 * i);
+  } else if (kind == 2) {
+    const uint32_t c[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = bf16x2_to_f16x2(c[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = 0;
+  }
+}
+
+// Two keys x 16 channels -> V^T rows (dim 16 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
+KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
+  uint32_t a[8], b[8];
+  v_row16(x.w[0], x.s[0], x.kind[0], a);
+  v_row16(x.w[1], x.s[1], x.kind[1], b);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
+    const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
+    *reinterpret_cast<uint32_t*>(vt + (16 * db + 2 * i) * kVPitch + 4 * tp) = lo;
+    *reinterpret_cast<uint32_t*>(vt + (16 * db + 2 * i + 1) * kVPitch + 4 * tp) = hi;
+  }
+}
+
+template <int G8>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                    const int32_t* kv_lens, int H, int gs, int n_qtiles, float scale, void* out, int out_f32,
+                    int64_t so_n, int64_t so_h) {
+  __shared__ Lds lds;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n16 = lane & 15, kb = lane >> 4;
+  const int qt = n_qtiles - 1 - (int)blockIdx.x;   // latest (heaviest) query tiles first
+  const int b = blockIdx.y / H;
+  const int h = blockIdx.y - b * H;
+  const int64_t qs = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b]
+                                   : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b];
+  const int64_t qe = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b + 1]
+                                   : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b + 1];
+  const int64_t q_len = qe - qs;
+  const int64_t L = kv_lens[b];
+  const int64_t q_pos0 = L - q_len;   // position of the chunk's first query
+  const int64_t qt0 = (int64_t)qt * kQT;
+  if (qt0 >= q_len) return;
+  const int64_t key_end = min(L, q_pos0 + min(q_len, qt0 + kQT));   // keys visible to the tile's last query
+  int64_t hs = 0, rbase = 0, rmask = 0;
+  if (S.kb == nullptr) {
+    const int64_t R = S.ring_len[b];
+    hs = min(max(max(S.ring_start[b], L - R), (int64_t)0), L);
+    rbase = S.ring_base[b];
+    rmask = R - 1;
+  }
+
+  // ---- Q operands: rows j of block rb = query qt0 + 4 wave + 2 rb + (j >> 3), head j & 7
+  h8 qop[2][8];
+  int64_t qpos[2];   // position of this lane's query row (as the S^T column), per row block
+  const float qmul = scale * kLog2e;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int64_t qi = qt0 + 4 * wave + 2 * rb + (n16 >> 3);
+    const int hq = n16 & 7;
+    const bool ok = qi < q_len && hq < gs;
+    qpos[rb] = q_pos0 + qi;
+    const uint16_t* qr = q + (qs + (ok ? qi : 0)) * sq_n + (int64_t)(h * gs + (ok ? hq : 0)) * sq_h;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = bf16_to_f32(qr[32 * s + 8 * kb + e]) * qmul;
+        qop[rb][s][e] = (_Float16)(ok ? x : 0.0f);
+      }
+    }
+  }
+
+  f4 acc[2][16];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int c = 0; c < 16; ++c) acc[rb][c] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+
+  // dequant roles: K row tk = tid >> 3, channels 32 (tid & 7) ..; V keys 2 tp, 2 tp + 1 (tp = tid & 15),
+  // channels 16 db .. (db = tid >> 4)
+  const int tk = tid >> 3, dc = tid & 7;
+  const int tp = tid & 15, db = tid >> 4;
+  const int ntiles = (int)((key_end + kT - 1) / kT);
+  RawK rk_next = fetch_k<G8>(S, locate<G8>(S, b, tk, key_end, hs, rbase, rmask), H, h, dc);
+  RawV rv_next = fetch_v<G8>(S, locate<G8>(S, b, 2 * tp, key_end, hs, rbase, rmask),
+                             locate<G8>(S, b, 2 * tp + 1, key_end, hs, rbase, rmask), H, h, db);
+  for (int it = 0; it < ntiles; ++it) {
+    const int64_t t0 = (int64_t)it * kT;
+    __syncthreads();   // the previous tile's fragments are consumed
+    store_k(rk_next, lds.k + tk * kKPitch + 64 * dc);
+    store_v(rv_next, lds.vt, db, tp);
+    __syncthreads();
+    if (it + 1 < ntiles) {   // next tile's codes travel during this tile's matrix work
+      const int64_t t1 = t0 + kT;
+      rk_next = fetch_k<G8>(S, locate<G8>(S, b, t1 + tk, key_end, hs, rbase, rmask), H, h, dc);
+      rv_next = fetch_v<G8>(S, locate<G8>(S, b, t1 + 2 * tp, key_end, hs, rbase, rmask),
+                            locate<G8>(S, b, t1 + 2 * tp + 1, key_end, hs, rbase, rmask), H, h, db);
+    }
+    // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16
+    float s[2][2][4];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+      const uint8_t* krow = lds.k + (16 * nt + n16) * kKPitch + 16 * kb;
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        const h8 a = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(krow + 64 * st));
+        d0 = mfma(a, qop[0][st], d0);
+        d1 = mfma(a, qop[1][st], d1);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t kp = t0 + 16 * nt + 4 * kb + r;
+        s[0][nt][r] = (kp <= qpos[0] && kp < key_end) ? d0[r] : -INFINITY;
+        s[1][nt][r] = (kp <= qpos[1] && kp < key_end) ? d1[r] : -INFINITY;
+      }
+    }
+    // ---- online softmax per row block; P as the A operand of P.V
+    h8 pa[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[rb][nt][r]);
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float m_new = fmaxf(m_run[rb], mloc);
+      // rows with no visible key yet keep m = -inf and contribute nothing
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      if (__any(m_new > m_run[rb])) {
+        const float alpha = m_run[rb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_use);
+        l_run[rb] *= alpha;
+        float arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[rb][c][i] *= arow[i];
+      }
+      m_run[rb] = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          s[rb][nt][r] = __builtin_amdgcn_exp2f(s[rb][nt][r] - m_use);
+          psum += s[rb][nt][r];
+        }
+      l_run[rb] += psum;
+      pa[rb] = h8{(_Float16)s[rb][0][0], (_Float16)s[rb][0][1], (_Float16)s[rb][0][2], (_Float16)s[rb][0][3],
+                  (_Float16)s[rb][1][0], (_Float16)s[rb][1][1], (_Float16)s[rb][1][2], (_Float16)s[rb][1][3]};
+    }
+    // ---- O += P V: B = V^T row (dim 16 c + n16), keys {4 kb .. +3, 16 + 4 kb .. +3}
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const uint8_t* vrow = lds.vt + (16 * c + n16) * kVPitch + 8 * kb;
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 32);
+      const h8 bv = __builtin_bit_cast(h8, u4v{lo.x, lo.y, hi.x, hi.y});
+      acc[0][c] = mfma(pa[0], bv, acc[0][c]);
+      acc[1][c] = mfma(pa[1], bv, acc[1][c]);
+    }
+  }
+
+  // ---- normalize and store: accumulator row 4 kb + i of block rb = query qt0 + 4 wave + 2 rb + (kb >> 1),
+  // head 4 (kb & 1) + i; column n16 of block c = dim 16 c + n16
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    float l = l_run[rb];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t qi = qt0 + 4 * wave + 2 * rb + (kb >> 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float lr = __shfl(l, 4 * kb + i, 64);
+      const int hq = 4 * (kb & 1) + i;
+      if (qi < q_len && hq < gs) {
+        const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
+        if (out_f32) {
+          float* orow = reinterpret_cast<float*>(out) + o0;
+#pragma unroll
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[rb][c][i] / lr;
+        } else {
+          uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
+#pragma unroll
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[rb][c][i] / lr);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                     const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
+                     const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
+                     const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
+                     const void* ring_start, const void* page_table, int64_t pt_stride, const void* k_bf16,
+                     const void* v_bf16, int64_t kb_n, int64_t kb_h, int64_t vb_n, int64_t vb_h, float scale,
+                     void* out, int out_f32, int64_t so_n, int64_t so_h, void* stream) {
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || Hq / H > 8 || max_q < 0) return KVT_EINVAL;
+  if ((k_bf16 == nullptr) != (v_bf16 == nullptr)) return KVT_EINVAL;
+  if (max_q == 0) return KVT_OK;
+  KVSrc S{(const uint8_t*)k4,        (const uint8_t*)v4,       (const uint16_t*)ks4,    (const uint16_t*)vs4,
+          (const int8_t*)rk,         (const int8_t*)rv,        (const uint16_t*)rks,    (const uint16_t*)rvs,
+          (const int64_t*)ring_base, (const int32_t*)ring_len, (const int64_t*)ring_start,
+          (const int32_t*)page_table, pt_stride,               (const uint16_t*)k_bf16, (const uint16_t*)v_bf16,
+          kb_n, kb_h, vb_n, vb_h};
+  const int n_qtiles = (max_q + kQT - 1) / kQT;
+  const dim3 grid((unsigned)n_qtiles, (unsigned)(batch * H));
+  hipStream_t st = (hipStream_t)stream;
+  if (group8 == 64) {
+    hipLaunchKernelGGL(prefill_mfma_kernel<64>, grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,
+                       cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n,
+                       so_h);
+  } else if (group8 == 256) {
+    hipLaunchKernelGGL(prefill_mfma_kernel<256>, grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,
+                       cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n,
+                       so_h);
+  } else {
+    return KVT_EINVAL;
+  }
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
+}
+
+}  // extern "C"

@@ -318,3 +318,51 @@ def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, 
               out.data_ptr() if out_dtype == torch.float32 else None,
               out.data_ptr() if out_dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
     return out
+
+
+def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: torch.Tensor,
+                     kv_lens: Optional[torch.Tensor] = None, max_q: Optional[int] = None,
+                     k_src: Optional[torch.Tensor] = None, v_src: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Causal prefill attention of the chunk queries q (bf16 [total_q, Hq, D]; sequence b = cache sequence b owns
+    rows cu_q[b] .. cu_q[b+1]) over the tiered cache of `layer`, which must already hold the chunk: the queries sit
+    at positions kv_lens[b] - q_len .. kv_lens[b] - 1 (kv_lens defaults to the cache lengths) and each attends to
+    every position up to its own (patches/kv_paged_prefix.py:200).  k_src / v_src (bf16 [positions, H, D], batch 1):
+    read keys from these rows instead, as the reference does for a chunk without a prefix.  Returns out
+    ([total_q, Hq, D], bf16 like the reference or fp32)."""
+    assert q.dim() == 3 and q.dtype == torch.bfloat16 and q.stride(2) == 1 and q.shape[2] == cache.D
+    assert cu_q.dtype in (torch.int32, torch.int64) and cu_q.is_contiguous() and cu_q.is_cuda
+    batch = cu_q.shape[0] - 1
+    H, D = cache.H, cache.D
+    Hq = q.shape[1]
+    assert Hq % H == 0 and Hq // H <= 8
+    if kv_lens is None:
+        kv_lens = cache.seq_lens[:batch]
+    assert kv_lens.dtype == torch.int32 and kv_lens.is_cuda and kv_lens.numel() >= batch
+    if max_q is None:
+        max_q = int((cu_q[1:] - cu_q[:-1]).max()) if batch else 0
+    if out is None:
+        out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
+    assert out.shape == q.shape and out.dtype in (torch.bfloat16, torch.float32) and out.stride(2) == 1
+    if (k_src is None) != (v_src is None):
+        raise ValueError("k_src and v_src go together")
+    if k_src is not None:
+        assert batch == 1 and k_src.dtype == torch.bfloat16 and v_src.dtype == torch.bfloat16
+        assert k_src.stride(2) == 1 and v_src.stride(2) == 1 and k_src.shape[1:] == (H, D) == v_src.shape[1:]
+        if min(k_src.shape[0], v_src.shape[0]) < int(kv_lens[0]):
+            raise ValueError("k_src / v_src hold fewer rows than the context length")
+    _lib.require_device(q, out, k_src, v_src)
+    if batch == 0 or max_q == 0:
+        return out
+    _lib.call("kvt_prefill_attn", q.data_ptr(), q.stride(0), q.stride(1), cu_q.data_ptr(),
+              int(cu_q.dtype == torch.int64), kv_lens.data_ptr(), batch, max_q, H, Hq, D, cache.group8,
+              cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
+              cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
+              cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
+              cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
+              cache.page_table.stride(0), _lib.ptr(k_src), _lib.ptr(v_src),
+              k_src.stride(0) if k_src is not None else 0, k_src.stride(1) if k_src is not None else 0,
+              v_src.stride(0) if v_src is not None else 0, v_src.stride(1) if v_src is not None else 0,
+              1.0 / math.sqrt(D), out.data_ptr(), int(out.dtype == torch.float32), out.stride(0), out.stride(1),
+              _lib.stream())
+    return out

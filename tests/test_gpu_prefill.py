@@ -1,0 +1,129 @@
+"""GPU parity of the causal prefill kernel (kvt_prefill_attn) against the oracle.
+
+Chunked prefill as the reference serves it (patches/kv_paged_prefix.py:200, docs/KV_PAGED_PREFIX_PLAN.md:21-23): the
+first chunk attends to its own fresh bf16 K/V; every later chunk is first appended to the cache (the ring's oldest
+rows requantized into INT4 pages) and then attends to all positions up to its own, read back from the tiers.  The
+oracle is fp32 softmax attention over the oracle cache's bf16-dequantized rows (gemv/test_kv_paged_prefix.py:506-531).
+Tolerance: 2e-3 max-abs / 1e-3 mean-abs on fp32 outputs (fp16 K/V/Q/P on the matrix cores, fp32 accumulation); the
+bf16 output is the fp32 output rounded to nearest even, bit for bit.
+"""
+import pytest
+import torch
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+H, D, HQ = 2, 256, 16
+SCALE = D ** -0.5
+
+
+def _chunked(lens_chunks, ring, seed, group8=64, n_pages=64):
+    """Append chunks to a device and an oracle cache (one sequence); yield (start, n, xk, xv, dc, oc) after each
+    chunk's append."""
+    from kvtier.kvt import PosTieredCache
+    gen = torch.Generator().manual_seed(seed)
+    och = ref.outlier_channels(H, D, 8, gen)
+    dc = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=ring, max_seqs=1, max_pages=n_pages, device=dev,
+                        page_seed=seed, group8=group8)
+    oc = ref.PosTieredCache(H, D, n_pages=n_pages, ring_total=ring, group8=group8)
+    alloc = ref.PageAllocator(n_pages, seed=seed)
+    dc.add_seq(ring)
+    oc.add_seq(0, ring)
+    a = 0
+    for n in lens_chunks:
+        xk, xv = ref.make_kv(n, H, D, gen, och)
+        done = 0
+        while done < n:   # one append never exceeds the ring
+            m = min(ring, n - done)
+            plan = dc.plan_append([0], [m])
+            dc.append(0, plan, xk[done:done + m].to(dev), xv[done:done + m].to(dev))
+            dc.commit(plan)
+            oc.plan_pages(0, m, alloc)
+            oc.append(0, xk[done:done + m], xv[done:done + m])
+            done += m
+        yield a, n, xk, xv, dc, oc, gen
+        a += n
+
+
+def _oracle_chunk(q, a, kk, vv):
+    """Causal attention of queries at positions a .. a + n - 1 over rows kk / vv [>= a + n, H, D]."""
+    return torch.stack([ref.attention_rows(q[j], kk[:a + j + 1], vv[:a + j + 1], SCALE) for j in range(q.shape[0])])
+
+
+@pytest.mark.parametrize("group8", [64, 256])
+def test_prefill_chunks_vs_oracle(kvt_pkg, group8):
+    """4 chunks of 96 queries, ring 128: chunk 0 from bf16, chunks 1-3 from the tiers (positions below hot_start in
+    INT4 pages after evict-requant); ragged last query tile (96 = 6 x 16)."""
+    from kvtier.kvt import kvt_prefill_attn
+    for a, n, xk, xv, dc, oc, gen in _chunked([96, 96, 96, 80], 128, seed=11, group8=group8):
+        q = ref.make_q(HQ, D, gen, n=n)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        if a == 0:
+            k_src, v_src = xk.to(dev), xv.to(dev)
+            out = kvt_prefill_attn(dc, 0, q.to(dev), cu, k_src=k_src, v_src=v_src, out_dtype=torch.float32)
+            outb = kvt_prefill_attn(dc, 0, q.to(dev), cu, k_src=k_src, v_src=v_src)
+            exp = _oracle_chunk(q, 0, xk, xv)
+        else:
+            out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32)
+            outb = kvt_prefill_attn(dc, 0, q.to(dev), cu)
+            kk, vv = oc.rows(0)
+            exp = _oracle_chunk(q, a, kk, vv)
+        out = out.cpu()
+        err = (out - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (a, float(err.max()), float(err.mean()))
+        assert torch.equal(outb.cpu(), out.to(torch.bfloat16)), ("bf16 output != rounded fp32 output", a)
+
+
+def test_prefill_first_query_closed_form(kvt_pkg):
+    """Query 0 of a chunk without a prefix sees only key 0: the output is exactly that V row (P = 1), for every q
+    head of each KV head."""
+    from kvtier.kvt import kvt_prefill_attn
+    for a, n, xk, xv, dc, oc, gen in _chunked([40], 64, seed=12):
+        q = ref.make_q(HQ, D, gen, n=n)
+        cu = torch.tensor([0, n], dtype=torch.int64, device=dev)
+        out = kvt_prefill_attn(dc, 0, q.to(dev), cu, k_src=xk.to(dev), v_src=xv.to(dev),
+                               out_dtype=torch.float32).cpu()
+        for hq in range(HQ):
+            assert torch.equal(out[0, hq], xv[0, hq // 8].float()), hq
+
+
+def test_prefill_two_sequences_cache(kvt_pkg):
+    """Two sequences with their own rings and interleaved pages, chunks of 50 and 33 queries (int64 cu_q)."""
+    from kvtier.kvt import PosTieredCache, kvt_prefill_attn
+    gen = torch.Generator().manual_seed(13)
+    och = ref.outlier_channels(H, D, 8, gen)
+    rings = [64, 128]
+    dc = PosTieredCache(1, H, D, n_pages=32, ring_total=sum(rings), max_seqs=2, max_pages=16, device=dev,
+                        page_seed=3)
+    oc = ref.PosTieredCache(H, D, n_pages=32, ring_total=sum(rings))
+    alloc = ref.PageAllocator(32, seed=3)
+    base = 0
+    for r in rings:
+        dc.add_seq(r)
+        oc.add_seq(base, r)
+        base += r
+    # history: 300 and 190 positions, then the chunk (50, 33) appended
+    for total in ([60, 60], [60, 60], [60, 60], [60, 10], [60, 0], [50, 33]):
+        seqs = [s for s in range(2) if total[s] > 0]
+        cnt = [total[s] for s in seqs]
+        plan = dc.plan_append(seqs, cnt)
+        ks, vs = [], []
+        for s, m in zip(seqs, cnt):
+            xk, xv = ref.make_kv(m, H, D, gen, och)
+            oc.plan_pages(s, m, alloc)
+            oc.append(s, xk, xv)
+            ks.append(xk)
+            vs.append(xv)
+        dc.append(0, plan, torch.cat(ks).to(dev), torch.cat(vs).to(dev))
+        dc.commit(plan)
+    nq = [50, 33]
+    q = ref.make_q(HQ, D, gen, n=sum(nq))
+    cu = torch.tensor([0, 50, 83], dtype=torch.int64, device=dev)
+    out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32).cpu()
+    for s, (q0, q1) in enumerate(((0, 50), (50, 83))):
+        kk, vv = oc.rows(s)
+        L = kk.shape[0]
+        exp = _oracle_chunk(q[q0:q1], L - (q1 - q0), kk, vv)
+        err = (out[q0:q1] - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (s, float(err.max()), float(err.mean()))
