@@ -149,6 +149,172 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
     print(json.dumps(res))
 
 
+def _layer_kv(n: int, layer: int, seed: int):
+    """Seeded synthetic K (8 of 256 channels per head x8) and V for one layer, bf16 on the GPU."""
+    gc = torch.Generator().manual_seed(seed * 1000 + layer)
+    mul = torch.ones(H, D)
+    for h in range(H):
+        mul[h, torch.randperm(D, generator=gc)[:8]] = 8.0
+    g = torch.Generator(device="cuda").manual_seed(seed * 1000 + layer)
+    k = (torch.randn(n, H, D, device="cuda", generator=g) * mul.to("cuda")).to(torch.bfloat16)
+    v = torch.randn(n, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    return k, v
+
+
+def prefill_workload(args) -> dict:
+    """Chunked prefill of a 10,001-token prompt, 12 layers, chunks of 2,048: per chunk the quantize-append of every
+    layer (the ring's oldest rows requantized into INT4 pages once it is full), then causal prefill attention of
+    every layer (the first chunk over its fresh bf16 K/V, later ones over the tiers).  Timed: whole prompt;
+    prefill kernels also timed alone (HIP events) for the matrix-core rate."""
+    import kvtier  # noqa: F401
+    from kvtier.kvt import PosTieredCache, kvt_prefill_attn
+    N, CH = 10_001, 2048
+    n_pages = (N - RING) // PAGE + 2
+    kv = [_layer_kv(N, layer, seed=3) for layer in range(LAYERS)]
+    gq = torch.Generator(device="cuda").manual_seed(303)
+    qs = [(torch.randn(N, HQ, D, device="cuda", generator=gq) / 16).to(torch.bfloat16) for _ in range(LAYERS)]
+    chunks = [(a, min(CH, N - a)) for a in range(0, N, CH)]
+    cus = {n: torch.tensor([0, n], dtype=torch.int32, device="cuda") for _, n in chunks}
+    outs = [torch.empty(CH, HQ, D, dtype=torch.bfloat16, device="cuda") for _ in range(LAYERS)]
+
+    def run(events=None):
+        cache = PosTieredCache(LAYERS, H, D, n_pages=n_pages, ring_total=RING, max_seqs=1, max_pages=n_pages + 1,
+                               device="cuda", page_seed=0)
+        cache.add_seq(RING)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for a, n in chunks:
+            plan = cache.plan_append([0], [n])
+            for layer in range(LAYERS):
+                cache.append(layer, plan, kv[layer][0][a:a + n], kv[layer][1][a:a + n])
+            cache.commit(plan)
+            for layer in range(LAYERS):
+                if events is not None:
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                src = dict(k_src=kv[layer][0][:n], v_src=kv[layer][1][:n]) if a == 0 else {}
+                kvt_prefill_attn(cache, layer, qs[layer][a:a + n], cus[n], max_q=n, out=outs[layer][:n], **src)
+                if events is not None:
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e1.record()
+                    events.append((e0, e1))
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    for _ in range(args.warmup):
+        run()
+    times, ev = [], []
+    for _ in range(args.steps):
+        times.append(run(ev))
+    torch.cuda.synchronize()
+    t_prompt = min(times)
+    t_prefill = sum(a.elapsed_time(b) for a, b in ev) / 1e3 / args.steps
+    flops = 4.0 * HQ * D * (N * (N + 1) // 2) * LAYERS
+    return {
+        "metric": "chunked prefill 10,001 tokens x 12 layers: ms per prompt (append + evict + causal prefill)",
+        "value": round(t_prompt * 1e3, 3), "unit": "ms", "higher_is_better": False, "steps": args.steps,
+        "warmup": args.warmup, "dtype": "f16-mfma/f32", "data": "synthetic",
+        "config": {"workload": "10,001-token prompt, chunks of 2048, 12 layers, 16 Q / 2 KV heads, D 256, ring 8192 "
+                               "(1,809 positions evicted to INT4 pages in the last chunk)"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / t_prefill / 1e12, 2), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(flops / t_prefill / 2.5e15, 4), "traffic": None,
+                     "kernel": "prefill (causal, all chunks and layers)", "kernel_ms": round(t_prefill * 1e3, 3),
+                     "flops": flops},
+    }
+
+
+def decode_steps_workload(args, ragged: bool) -> dict:
+    """ragged = False: one layer, 10,001-token context (ring 8192 + 1,809 paged positions), 1,000 steps of
+    append-one-token + decode.  ragged = True: 8 sequences with log-uniform lengths in [1024, 65536] (seeded), 12
+    layers, two sequences sharing a 4,096-token prefix in common pages, 256 iterations of one decode step per
+    sequence (append + decode of every layer).  Reports us per step (wall, host planning included) and the KV GB/s of
+    the decode launches."""
+    import kvtier  # noqa: F401
+    from kvtier.kvt import PosTieredCache, kvt_decode_attn
+    layers = LAYERS if ragged else 1
+    if ragged:
+        gl = torch.Generator().manual_seed(4)
+        lens = [int(math.exp(math.log(1024) + (math.log(65536) - math.log(1024)) * float(u)))
+                for u in torch.rand(8, generator=gl)]
+        lens[0], lens[1] = max(lens[0], 4096 + 1024), max(lens[1], 4096 + 1024)   # the two prefix sharers
+        steps = 256
+    else:
+        lens = [10_001]
+        steps = 1000
+    S = len(lens)
+    rings = [min(RING, 1 << (max(1, L) - 1).bit_length()) for L in lens]
+    shared = 4096 if ragged else 0
+    n_pages = sum(max(0, L + steps - r) // PAGE + 2 for L, r in zip(lens, rings)) + shared // PAGE
+    max_pages = max(lens) // PAGE + steps // PAGE + 4
+    cache = PosTieredCache(layers, H, D, n_pages=n_pages, ring_total=sum(rings), max_seqs=S, max_pages=max_pages,
+                           device="cuda", page_seed=5)
+    # the shared prefix: 64 pages taken from the allocator and written once with the INT4 writer (positions 0..4095),
+    # then referenced by sequences 0 and 1 through their page tables (ring_start = 4096)
+    seqs = []
+    if shared:
+        from kvtier import sparse_attn
+        shared_pages = [cache.alloc.pop() for _ in range(shared // PAGE)]
+        rows = (torch.tensor(shared_pages, device="cuda")[:, None] * PAGE
+                + torch.arange(PAGE, device="cuda")[None, :]).reshape(-1)
+        ones = torch.ones(H, D, dtype=torch.float16, device="cuda")
+        for layer in range(layers):
+            k, v = _layer_kv(shared, layer, seed=40)
+            sparse_attn.quant_store_kv_int4(k, v, rows, cache.k4[layer], cache.v4[layer], cache.ks4[layer],
+                                            cache.vs4[layer], ones, ones)
+    for i, (L, r) in enumerate(zip(lens, rings)):
+        if shared and i < 2:
+            seqs.append(cache.add_seq(r, ring_start=shared, shared_pages=shared_pages))
+        else:
+            seqs.append(cache.add_seq(r))
+    done = [shared if (shared and i < 2) else 0 for i in range(S)]
+    while any(d < L for d, L in zip(done, lens)):
+        act = [i for i in range(S) if done[i] < lens[i]]
+        cnt = [min(rings[i], lens[i] - done[i]) for i in act]
+        plan = cache.plan_append([seqs[i] for i in act], cnt)
+        for layer in range(layers):
+            k, v = _layer_kv(sum(cnt), layer, seed=7 + done[act[0]])
+            cache.append(layer, plan, k, v)
+        cache.commit(plan)
+        for i, n in zip(act, cnt):
+            done[i] += n
+    n_all = cache.n_seqs
+    gq = torch.Generator(device="cuda").manual_seed(9)
+    q = (torch.randn(layers, n_all, HQ, D, device="cuda", generator=gq) / 16).to(torch.bfloat16)
+    knew, vnew = _layer_kv(S, 0, seed=11)
+    ws = {}
+    out = torch.empty(n_all, HQ, D, dtype=torch.float32, device="cuda")
+    ev = []
+
+    def step(events=None):
+        plan = cache.plan_append(seqs, [1] * S)
+        for layer in range(layers):
+            cache.append(layer, plan, knew, vnew)
+        cache.commit(plan)
+        for layer in range(layers):
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, events=events)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    kv_bytes = cache.kv_bytes(seqs) * layers
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(ev)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    dec_s = sum(a.elapsed_time(c) for a, _, c in ev) / 1e3 / steps
+    name = ("ragged decode: 8 sequences, 12 layers, shared 4,096-token prefix, 256 iterations" if ragged
+            else "decode with append: 10,001-token context, 1 layer, 1,000 steps")
+    return {
+        "metric": name + ": us per step", "value": round(wall * 1e6, 1), "unit": "us", "higher_is_better": False,
+        "steps": steps, "warmup": args.warmup, "dtype": "f16-mfma/f32", "data": "synthetic",
+        "config": {"workload": name, "lens": lens, "rings": rings, "impl": args.impl},
+        "decode_us_per_step": round(dec_s * 1e6, 1),
+        "decode_kv_GBps": round(kv_bytes / dec_s / 1e9, 1),
+        "kv_bytes_per_step": kv_bytes,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +322,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--impl", default=os.environ.get("KVT_DECODE_IMPL", "mfma"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged"],
+                    help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
                     help="summarize two rocprofv3 --pmc counter CSVs into the traffic file and exit")
@@ -170,6 +338,13 @@ def main():
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is a design in "
               "DESIGN.md, not a measured path", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "decode262k":
+        fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
+              "ragged": lambda a: decode_steps_workload(a, True)}[args.workload]
+        line = fn(args)
+        line["n_gpus"] = 1
+        print(json.dumps(line))
+        return
     import kvtier  # noqa: F401
     from kvtier.kvt import kvt_decode_attn
 
