@@ -49,6 +49,7 @@ def _build(lens, rings, seed=0, n_pages=None, chunk=512, starts=None):
         for s, n in zip(seqs, cnt):
             done[s] += n
     q = ref.make_q(HQ, D, gen, n=len(lens))
+    oc.alloc = alloc   # the oracle's page allocator, for callers that keep appending
     return dc, oc, q
 
 
@@ -226,3 +227,87 @@ def test_decode_graph_replay(kvt_pkg):
         assert torch.equal(out, eager), f"replay {i}"
         _ = (qd.float() * 2).sum()          # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_decode_steps_with_append(kvt_pkg):
+    """Decode with append (the 1,000-step configuration at a reduced size): 500 positions, ring 128, then 40 steps of
+    append-one-token (each evicting the oldest ring row into INT4 pages) + MFMA decode; every step's output against the
+    oracle, codes and page table bit-exact at the end."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([500], [128], seed=21)
+    gen = torch.Generator().manual_seed(22)
+    och = ref.outlier_channels(H, D, 8, gen)
+    alloc = oc.alloc
+    ws = {}
+    for step in range(40):
+        xk, xv = ref.make_kv(1, H, D, gen, och)
+        plan = dc.plan_append([0], [1])
+        dc.append(0, plan, xk.to(dev), xv.to(dev))
+        dc.commit(plan)
+        oc.plan_pages(0, 1, alloc)
+        oc.append(0, xk, xv)
+        qs = ref.make_q(HQ, D, gen)
+        out = kvt_decode_attn(dc, 0, qs.to(dev), impl="mfma", workspace=ws).cpu()
+        err = (out - _oracle_out(oc, qs)).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (step, float(err.max()))
+    for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
+        assert torch.equal(getattr(dc, name)[0].cpu(), getattr(oc, name)), name
+    assert torch.equal(dc.page_table.cpu()[0, :len(oc.seqs[0].pages)], torch.tensor(oc.seqs[0].pages, dtype=torch.int32))
+
+
+def test_decode_ragged_shared_prefix(kvt_pkg):
+    """Ragged batch (the 8-sequence configuration at a reduced size): 4 sequences of different lengths and rings;
+    sequences 0 and 1 share a 128-position prefix held in two common INT4 pages (paged-prefix reuse); 6 iterations of
+    one append + one batched MFMA decode step per sequence, each against the oracle."""
+    from kvtier import sparse_attn as sa
+    from kvtier.kvt import PosTieredCache, kvt_decode_attn
+    gen = torch.Generator().manual_seed(23)
+    och = ref.outlier_channels(H, D, 8, gen)
+    lens, rings = [700, 420, 90, 1500], [256, 128, 128, 512]
+    n_pages = 64
+    dc = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=sum(rings), max_seqs=4, max_pages=40, device=dev,
+                        page_seed=6)
+    oc = ref.PosTieredCache(H, D, n_pages=n_pages, ring_total=sum(rings))
+    alloc = ref.PageAllocator(n_pages, seed=6)
+    shared = [dc.alloc.pop(), dc.alloc.pop()]
+    assert shared == [alloc.pop(), alloc.pop()]
+    pk, pv = ref.make_kv(128, H, D, gen, och)
+    rows = torch.tensor([p * 64 + i for p in shared for i in range(64)])
+    ones = torch.ones(H, D, dtype=torch.float16)
+    sa.quant_store_kv_int4(pk.to(dev), pv.to(dev), rows.to(dev), dc.k4[0], dc.v4[0], dc.ks4[0], dc.vs4[0],
+                           ones.to(dev), ones.to(dev))
+    ref.quant_store_int4(pk, pv, rows, oc.k4, oc.v4, oc.ks4, oc.vs4, ones, ones)
+    base = 0
+    for s, r in enumerate(rings):
+        start, pages = (128, shared) if s < 2 else (0, ())
+        dc.add_seq(r, ring_start=start, shared_pages=pages)
+        oc.add_seq(base, r, ring_start=start, shared_pages=pages)
+        base += r
+    done = [128, 128, 0, 0]
+    while any(d < l for d, l in zip(done, lens)):
+        seqs = [s for s in range(4) if done[s] < lens[s]]
+        cnt = [min(rings[s], lens[s] - done[s]) for s in seqs]
+        plan = dc.plan_append(seqs, cnt)
+        ks, vs = [], []
+        for s, m in zip(seqs, cnt):
+            xk, xv = ref.make_kv(m, H, D, gen, och)
+            oc.plan_pages(s, m, alloc)
+            oc.append(s, xk, xv)
+            ks.append(xk)
+            vs.append(xv)
+        dc.append(0, plan, torch.cat(ks).to(dev), torch.cat(vs).to(dev))
+        dc.commit(plan)
+        for s, m in zip(seqs, cnt):
+            done[s] += m
+    for it in range(6):
+        xk, xv = ref.make_kv(4, H, D, gen, och)
+        plan = dc.plan_append([0, 1, 2, 3], [1, 1, 1, 1])
+        dc.append(0, plan, xk.to(dev), xv.to(dev))
+        dc.commit(plan)
+        for s in range(4):
+            oc.plan_pages(s, 1, alloc)
+            oc.append(s, xk[s:s + 1], xv[s:s + 1])
+        qs = ref.make_q(HQ, D, gen, n=4)
+        out = kvt_decode_attn(dc, 0, qs.to(dev), impl="mfma").cpu()
+        err = (out - _oracle_out(oc, qs)).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (it, float(err.max()), float(err.mean()))
