@@ -275,6 +275,8 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
   const int lane = threadIdx.x & 63;
   const int n16 = lane & 15, kb = lane >> 4;
   const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  // QK^T per 16-token half, software-pipelined over the groups: the MFMA of group g + 1 is in flight while the
+  // result of group g is folded with its scales (the fold no longer waits on the matrix core)
   float s[2][4];
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
@@ -282,24 +284,27 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
     uint32_t w[8];
 #pragma unroll
     for (int g = 0; g < 8; ++g) w[g] = lds_code_dword(st.k, t, g, kb);
-    // bias term -sum_g s_g(t) bias_g (scaled by 2^-bexp in the MFMA, restored here)
-    const h8 srow = as_h8(*reinterpret_cast<const u4v*>(&st.ks[t][0]));
-    const f4 bsum = mfma(srow, kbias, f4{0.f, 0.f, 0.f, 0.f});
-    f4 sc;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = ldexpf(bsum[r], bexp);
     uint4 ksr[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) ksr[r] = *reinterpret_cast<const uint4*>(&st.ks[16 * nt + 4 * kb + r][0]);
+    // bias term -sum_g s_g(t) bias_g (scaled by 2^-bexp in the MFMA, restored here)
+    const h8 srow = as_h8(*reinterpret_cast<const u4v*>(&st.ks[t][0]));
+    const f4 bsum = mfma(srow, kbias, f4{0.f, 0.f, 0.f, 0.f});
+    f4 dp = mfma(int4_codes_raw(w[0], mlo, mhi, magic), qop[0], f4{0.f, 0.f, 0.f, 0.f});
+    f4 sc;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = ldexpf(bsum[r], bexp);
 #pragma unroll
     for (int g = 0; g < 8; ++g) {
-      const f4 d = mfma(int4_codes_raw(w[g], mlo, mhi, magic), qop[g], f4{0.f, 0.f, 0.f, 0.f});
+      f4 dn = dp;
+      if (g + 1 < 8) dn = mfma(int4_codes_raw(w[g + 1], mlo, mhi, magic), qop[g + 1], f4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t pairw = g < 2 ? ksr[r].x : g < 4 ? ksr[r].y : g < 6 ? ksr[r].z : ksr[r].w;
         const float sg = f16_bits_to_f32((uint16_t)((g & 1) ? (pairw >> 16) : (pairw & 0xffffu)));
-        sc[r] = fmaf(sg, d[r], sc[r]);
+        sc[r] = fmaf(sg, dp[r], sc[r]);
       }
+      dp = dn;
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
@@ -380,9 +385,9 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
       plo[2 * pr] = lo_p.x; plo[2 * pr + 1] = lo_p.y;
       phi[2 * pr] = hi_p.x; phi[2 * pr + 1] = hi_p.y;
     }
-    acc[2 * byte] = mfma(ax, olo, acc[2 * byte]);
-    acc[2 * byte] = mfma(ay, plo, acc[2 * byte]);
+    acc[2 * byte] = mfma(ax, olo, acc[2 * byte]);            // alternate accumulators: no back-to-back chain
     acc[2 * byte + 1] = mfma(ax, ohi, acc[2 * byte + 1]);
+    acc[2 * byte] = mfma(ay, plo, acc[2 * byte]);
     acc[2 * byte + 1] = mfma(ay, phi, acc[2 * byte + 1]);
   }
 }

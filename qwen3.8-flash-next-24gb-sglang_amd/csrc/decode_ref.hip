@@ -172,71 +172,60 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 }
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
-// grid (D / 64, Hq, batch), 1024 threads: thread (d = tid % 64, part = tid / 64) folds splits c = part (mod 16) for
-// one output channel, sixteen independent loads in flight; the 16 parts meet in LDS.  An empty context gives
-// 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
+// grid (D / 16, Hq, batch), 256 threads: thread (d = 16 blockIdx.x + tid % 16, part = tid / 16) loads splits
+// c = part (mod 16) of one output channel, all loads in flight at once, and merges them in one pass with a running
+// max (m, num, den) <- (max(m, m_c), num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')); the 16
+// parts merge the same way through LDS.  One block per CU-sized piece spreads the merge over the whole chip.
+// An empty context gives 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
 constexpr int kCombParts = 16;
+constexpr int kCombDims = 16;
+constexpr int kCombUnroll = 16;   // splits per thread and round
 
-__global__ void __launch_bounds__(64 * kCombParts) decode_combine_kernel(const float* part_o, const float* part_ml,
-                                                                         int H, int gs, int D, int n_chunks,
-                                                                         int64_t chunk, const int32_t* seq_lens,
-                                                                         float* out_f32, uint16_t* out_bf16,
-                                                                         int64_t out_stride_b) {
-  __shared__ float red[kCombParts][2][64];
-  __shared__ float mred[kCombParts];
+// Partial maxima are in natural-log units; the weights use the hardware exp2 on log2-scaled differences (<= 0).
+KVT_DEV void merge_into(float& m, float& num, float& den, float mc, float oc, float lc) {
+  constexpr float kL2e = 1.4426950408889634f;
+  const float mn = fmaxf(m, mc);
+  if (mn == -INFINITY) return;   // both empty
+  const float a = __builtin_amdgcn_exp2f((m - mn) * kL2e), c = __builtin_amdgcn_exp2f((mc - mn) * kL2e);
+  num = num * a + oc * c;
+  den = den * a + lc * c;
+  m = mn;
+}
+
+__global__ void __launch_bounds__(kCombDims * kCombParts) decode_combine_kernel(
+    const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
+    const int32_t* seq_lens, float* out_f32, uint16_t* out_bf16, int64_t out_stride_b) {
+  __shared__ float red[kCombParts][3][kCombDims];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
-  const int tid = threadIdx.x, dl = tid & 63, part = tid >> 6;
-  const int d = blockIdx.x * 64 + dl;
+  const int tid = threadIdx.x, dl = tid % kCombDims, part = tid / kCombDims;
+  const int d = blockIdx.x * kCombDims + dl;
   const int64_t L = seq_lens[b];
   // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
   const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk) : n_chunks;
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
-  // M = max over the used splits (each wave scans 1/16, then LDS)
-  float M = -INFINITY;
-  for (int c = tid; c < used; c += 64 * kCombParts) M = fmaxf(M, part_ml[((base + c) * gs + j) * 2]);
-  M = group_max<64>(M);
-  if (dl == 0) mred[part] = M;
-  __syncthreads();
-  M = mred[0];
+  float m = -INFINITY, num = 0.0f, den = 0.0f;
+  for (int c0 = part; c0 < used; c0 += kCombUnroll * kCombParts) {
+    float mv[kCombUnroll], lv[kCombUnroll], ov[kCombUnroll];
 #pragma unroll
-  for (int p = 1; p < kCombParts; ++p) M = fmaxf(M, mred[p]);
-  float num = 0.0f, den = 0.0f;
-  int c = part;
-  for (; c + 15 * kCombParts < used; c += 16 * kCombParts) {   // 16 independent loads of each kind in flight
-    float mv[16], lv[16], ov[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int64_t it = (base + c + u * kCombParts) * gs + j;
-      mv[u] = part_ml[it * 2];
+    for (int u = 0; u < kCombUnroll; ++u) {
+      const int c = c0 + u * kCombParts;
+      const int64_t it = (base + (c < used ? c : 0)) * gs + j;
+      mv[u] = c < used ? part_ml[it * 2] : -INFINITY;
       lv[u] = part_ml[it * 2 + 1];
       ov[u] = part_o[it * D + d];
     }
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float w = expf(mv[u] - M);
-      num = fmaf(w, ov[u], num);
-      den = fmaf(w, lv[u], den);
-    }
+    for (int u = 0; u < kCombUnroll; ++u) merge_into(m, num, den, mv[u], ov[u], lv[u]);
   }
-  for (; c < used; c += kCombParts) {
-    const int64_t it = (base + c) * gs + j;
-    const float w = expf(part_ml[it * 2] - M);
-    num = fmaf(w, part_o[it * D + d], num);
-    den = fmaf(w, part_ml[it * 2 + 1], den);
-  }
-  red[part][0][dl] = num;
-  red[part][1][dl] = den;
+  red[part][0][dl] = m;
+  red[part][1][dl] = num;
+  red[part][2][dl] = den;
   __syncthreads();
   if (part == 0) {
-    num = 0.0f;
-    den = 0.0f;
 #pragma unroll
-    for (int p = 0; p < kCombParts; ++p) {
-      num += red[p][0][dl];
-      den += red[p][1][dl];
-    }
+    for (int p = 1; p < kCombParts; ++p) merge_into(m, num, den, red[p][0][dl], red[p][1][dl], red[p][2][dl]);
     const float o = num / den;
     const int64_t oi = b * out_stride_b + (int64_t)hq * D + d;
     if (out_f32) out_f32[oi] = o;
@@ -290,9 +279,9 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
                        int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
                        void* stream) {
-  if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % 64 != 0) return KVT_EINVAL;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / 64), (unsigned)Hq, (unsigned)batch),
-                     dim3(64 * kCombParts), 0,
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % kCombDims != 0) return KVT_EINVAL;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch),
+                     dim3(kCombDims * kCombParts), 0,
                      (hipStream_t)stream,
                      (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
                      (const int32_t*)seq_lens, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b);
