@@ -148,14 +148,16 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
  * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16
  * [positions, H, D] rows (the reference attends to fresh bf16 K/V there).  out: bf16 or fp32 (out_f32) with the
  * layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
- * chunks.  Hq / H <= 8, D = 256. */
+ * chunks.  Hq / H <= 8, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
+ * offsets are 32-bit, else KVT_ERANGE). */
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
                      const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
                      const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
-                     const void* ring_start, const void* page_table, int64_t pt_stride, const void* k_bf16,
-                     const void* v_bf16, int64_t kb_n, int64_t kb_h, int64_t vb_n, int64_t vb_h, float scale,
-                     void* out, int out_f32, int64_t so_n, int64_t so_h, void* stream);
+                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
+                     const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
+                     int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
+                     void* stream);
 
 #ifdef __cplusplus
 }

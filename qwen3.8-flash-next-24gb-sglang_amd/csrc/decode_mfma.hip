@@ -149,15 +149,12 @@ KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
   return r;
 }
 
-// 16 bytes per lane from rsrc + voffset into lds + 16 * lane (M0 = LDS base).  Written as inline assembly so that
-// the compiler does not treat every later LDS read as dependent on it: completion is tracked explicitly with
-// wait_vmcnt by the caller.
+// 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
+// statement, so the compiler sets it.  Inline assembly rather than the builtin so that the compiler does not treat
+// every later LDS read as dependent on the copy: completion is tracked explicitly with wait_vmcnt by the caller.
 KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(base), "v"(voffset), "s"(rsrc)
-               : "memory", "m0");
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base) : "memory");
 }
 
 // s_waitcnt vmcnt(<= n) leaving the other counters alone (gfx9 encoding).
@@ -206,8 +203,7 @@ KVT_DEV void load_q_int4(const uint16_t* qrow, bool valid, int kb, h8 qop[8], h8
       qop[g][e] = hq;
       part = fmaf(odd ? 1152.0f : 1032.0f, (float)hq, part);
     }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
+    part = sum_xor16_32(part);
     bias[g] = part;
   }
   float amax = 0.0f;
@@ -228,12 +224,38 @@ struct ColdCtx {
   uint32_t rowbytes;            // H * 128
   uint32_t hoff;                // h * 128
   int H, h;
+  uint32_t coff[4];             // this lane's code byte offset in copy j of a full tile, relative to row0 * rowbytes
+  uint32_t soff;                // this lane's scale byte offset (lanes < 32), relative to row0 * H * 16
 };
+
+// Per-lane parts of the copy offsets of a full 32-token tile (computed once per wavefront).
+KVT_DEV void cold_lane_offsets(ColdCtx& C) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = 8 * j + (lane >> 3);
+    C.coff[j] = (uint32_t)t * C.rowbytes + C.hoff + 16u * (uint32_t)((lane & 7) ^ (t & 7));
+  }
+  C.soff = ((uint32_t)(lane & 31) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
+}
 
 // Issue the direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`:
 // exactly 10 vector-memory instructions per wavefront (the vmcnt accounting of cold_step relies on it).
 KVT_DEV void cold_issue(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
   const int lane = threadIdx.x & 63;
+  if (n == 32) {   // full tile: one add per copy
+    const uint32_t cb = row0 * C.rowbytes, sb = row0 * (uint32_t)C.H * 16u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
+      copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
+    }
+    if (lane < 32) {
+      copy16_to_lds(C.rks4, &st.ks[0][0], sb + C.soff);
+      copy16_to_lds(C.rvs4, &st.vsn[0][0], sb + C.soff);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = 8 * j + (lane >> 3);
@@ -306,14 +328,18 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
       }
       dp = dn;
     }
+    if (n == 32) {   // full tile: no mask
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
+      for (int r = 0; r < 4; ++r) s[nt][r] = sc[r] * cscale;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
+    }
   }
   // online softmax over the tile
   float mloc = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  mloc = max_xor16_32(mloc);
   const float m_new = fmaxf(m_run, mloc);
   if (__any(m_new > m_run)) {
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -344,7 +370,7 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
   const u4v po = as_u4(pown);
   u4v pp;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) pp[i] = (uint32_t)__shfl_xor((int)po[i], 32, 64);
+  for (int i = 0; i < 4; ++i) pp[i] = xor32_u32(po[i]);
   const u4v zero = {0u, 0u, 0u, 0u};
   const h8 ax = as_h8(lowrow ? po : zero);
   const h8 ay = as_h8(lowrow ? zero : pp);
@@ -531,8 +557,7 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
   for (int r = 0; r < 4; ++r) s[r] = (4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
   // ---- online softmax over the tile
   float mloc = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  mloc = max_xor16_32(mloc);
   const float m_new = fmaxf(m_run, mloc);
   if (__any(m_new > m_run)) {
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -559,8 +584,8 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
   const h4 pown = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
   const uint2 po = __builtin_bit_cast(uint2, pown);
   uint2 pp;
-  pp.x = (uint32_t)__shfl_xor((int)po.x, 32, 64);
-  pp.y = (uint32_t)__shfl_xor((int)po.y, 32, 64);
+  pp.x = xor32_u32(po.x);
+  pp.y = xor32_u32(po.y);
   const uint2 zero = {0u, 0u};
   const h4 ax = __builtin_bit_cast(h4, lowrow ? po : zero);
   const h4 ay = __builtin_bit_cast(h4, lowrow ? zero : pp);
@@ -684,7 +709,8 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
     load_q_int4(qrow, qvalid, kb, qop, kbias, bexp);
     ColdCtx C{buffer_rsrc(A.k4, pool_rows * (uint32_t)H * 128u), buffer_rsrc(A.v4, pool_rows * (uint32_t)H * 128u),
               buffer_rsrc(A.ks4, pool_rows * (uint32_t)H * 16u), buffer_rsrc(A.vs4, pool_rows * (uint32_t)H * 16u),
-              (uint32_t)H * 128u, (uint32_t)h * 128u, H, h};
+              (uint32_t)H * 128u, (uint32_t)h * 128u, H, h, {0u, 0u, 0u, 0u}, 0u};
+    cold_lane_offsets(C);
     cold_segment(A, C, lds.w[wave], b, w0, ce, qop, kbias, bexp, cscale, acc, m_run, l_run);
   }
   // hot segment [max(w0, hs), w1) from the INT8 ring
@@ -702,8 +728,7 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   }
 
   // ---- merge the four wavefronts (heads 0-7 of the group; lanes n16 >= 8 duplicate n16 - 8)
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  l_run = sum_xor16_32(l_run);
   __syncthreads();                        // every wavefront is done with its staging area
   if (kb == 0 && n16 < 8) {
     lds.merge.m[wave][n16] = m_run;

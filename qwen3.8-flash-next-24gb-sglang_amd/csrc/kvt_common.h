@@ -53,6 +53,27 @@ KVT_DEV float group_max(float v) {
   return v;
 }
 
+// Cross-lane steps on the VALU (v_permlane16_swap / v_permlane32_swap, gfx950) instead of LDS permutes.  With both
+// operands equal, the two results at lane l are the values of lanes l and l ^ 16 (resp. l ^ 32), in an order that
+// depends on l: a max or a sum of the two is the pairwise reduction.  All 64 lanes must be active.
+KVT_DEV float max_xor16_32(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+KVT_DEV float sum_xor16_32(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// The value of lane l ^ 32.
+KVT_DEV uint32_t xor32_u32(uint32_t v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+
 // Stored scale of a group with absmax a: fp16(min(a > 0 ? a / qmax : 1, 65504))
 // (patches/kv_tiers.py:337, :367).  Returns the fp16 bits.
 KVT_DEV uint16_t group_scale(float a, float qmax) {

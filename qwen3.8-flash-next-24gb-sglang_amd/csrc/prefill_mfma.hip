@@ -36,6 +36,12 @@ constexpr int kKPitch = kD * 2 + 16;    // bytes per fp16 K row in LDS (padded: 
 constexpr int kVPitch = kT * 2 + 16;    // bytes per fp16 V^T row (one dim, 32 keys)
 constexpr float kLog2e = 1.4426950408889634f;
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOOB = 0x80000000u;     // byte offset beyond every buffer: the load returns zeros
+constexpr int kMaxLdsPages = 8192;         // page ids staged in LDS: paged key ranges up to 524,288 positions
+
 struct KVSrc {
   const uint8_t* k4;
   const uint8_t* v4;
@@ -50,105 +56,109 @@ struct KVSrc {
   const int64_t* ring_start;
   const int32_t* page_table;
   int64_t pt_stride;
-  const uint16_t* kb;   // bf16 source [positions, H, D] (non-null: keys come from here, not from the cache)
+  uint32_t pool_rows;
+  const uint16_t* kb;   // bf16 source [positions, H, D] (the BF16 kernel variant reads keys from here)
   const uint16_t* vb;
-  int64_t kb_n, kb_h, vb_n, vb_h;
+  int64_t kb_n, kb_h, vb_n, vb_h, kb_rows;
 };
 
 struct __align__(16) Lds {
   uint8_t k[kT * kKPitch];
   uint8_t vt[kD * kVPitch];
+  int32_t pages[kMaxLdsPages];
 };
 
 KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 KVT_DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
 
-// Where a key position's row lives: kind 0 = INT4 pool row, 1 = INT8 ring row, 2 = bf16 source row, 3 = none.
-struct RowRef {
-  int64_t row;
-  int kind;
-};
-
-template <int G8>
-KVT_DEV RowRef locate(const KVSrc& S, int b, int64_t p, int64_t key_end, int64_t hs, int64_t rbase, int64_t rmask) {
-  RowRef r;
-  if (p >= key_end) {
-    r.row = 0;
-    r.kind = 3;
-  } else if (S.kb != nullptr) {
-    r.row = p;
-    r.kind = 2;
-  } else if (p >= hs) {
-    r.row = rbase + (p & rmask);
-    r.kind = 1;
-  } else {
-    r.row = (int64_t)S.page_table[b * S.pt_stride + (p >> 6)] * kPage + (p & (kPage - 1));
-    r.kind = 0;
-  }
-  return r;
+KVT_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
+KVT_DEV uint4 ld128(Rsrc r, uint32_t off) {
+  const v4i x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4((uint32_t)x.x, (uint32_t)x.y, (uint32_t)x.z, (uint32_t)x.w);
+}
+KVT_DEV uint2 ld64(Rsrc r, uint32_t off) {
+  const v2i x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2((uint32_t)x.x, (uint32_t)x.y);
+}
+KVT_DEV uint32_t ld16(Rsrc r, uint32_t off) { return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0); }
 
-// Raw codes of 32 consecutive channels (K: one token) or 2 x 16 channels (V: two tokens), loaded ahead of use.
+// This block's view of the key source: buffer resources over the INT4 pool, the sequence's ring rows and the bf16
+// source, the tier boundary and the key range.  Every key fetch issues the loads of both tiers unconditionally
+// (the other tier's at an offset beyond its buffer, which returns zeros): no branch, so the loads of the next tile
+// stay in flight across the matrix work of the current one.
+struct Tier {
+  Rsrc k4, v4, ks4, vs4, rk, rv, rks, rvs, kb, vb;
+  int64_t hs, rmask, key_end;
+  int64_t kb_n, kb_h, vb_n, vb_h;
+  int H, h;
+};
+
+// Raw K of one key row, channels 32 dc .. 32 dc + 31: INT4 (a, s4) or INT8 (b, c, s8); bf16 source: a, b, c, d.
 struct RawK {
-  uint4 w[4];
-  uint16_t s;
-  int kind;
+  uint4 a, b, c, d;
+  uint32_t s4, s8;
+  int hot;
 };
+// Raw V of two key rows, channels 16 db .. 16 db + 15 each: INT4 (c4, s4) or INT8 (a, s8); bf16 source: a, bb.
 struct RawV {
-  uint4 w[2][2];
-  uint16_t s[2];
-  int kind[2];
+  uint4 a[2], bb[2];
+  uint2 c4[2];
+  uint32_t s4[2], s8[2];
+  int hot[2];
 };
 
-// K: channels 32 dc .. 32 dc + 31 of one key row.
-template <int G8>
-KVT_DEV RawK fetch_k(const KVSrc& S, RowRef r, int H, int h, int dc) {
+template <int G8, bool BF16>
+KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int64_t p, int dc) {
   RawK x;
-  x.kind = r.kind;
-  x.s = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x.w[i] = make_uint4(0, 0, 0, 0);
-  const int64_t rh = r.row * H + h;
-  if (r.kind == 0) {
-    x.w[0] = *reinterpret_cast<const uint4*>(S.k4 + rh * (kD / 2) + 16 * dc);
-    x.s = S.ks4[rh * (kD / kG4) + dc];
-  } else if (r.kind == 1) {
-    const uint4* p = reinterpret_cast<const uint4*>(S.rk + rh * kD + 32 * dc);
-    x.w[0] = p[0];
-    x.w[1] = p[1];
-    x.s = S.rks[rh * (kD / G8) + (32 * dc) / G8];
-  } else if (r.kind == 2) {
-    const uint4* p = reinterpret_cast<const uint4*>(S.kb + r.row * S.kb_n + (int64_t)h * S.kb_h + 32 * dc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x.w[i] = p[i];
+  p = min(p, T.key_end - 1);   // keys past the end: valid rows, masked in the scores
+  if constexpr (BF16) {
+    const uint32_t off = (uint32_t)((p * T.kb_n + (int64_t)T.h * T.kb_h + 32 * dc) * 2);
+    x.a = ld128(T.kb, off);
+    x.b = ld128(T.kb, off + 16);
+    x.c = ld128(T.kb, off + 32);
+    x.d = ld128(T.kb, off + 48);
+    x.hot = 2;
+  } else {
+    constexpr int NG8 = kD / G8;
+    const bool hot = p >= T.hs;
+    const int64_t pg = hot ? 0 : min(p >> 6, (int64_t)kMaxLdsPages - 1);
+    const uint32_t rh4 = (uint32_t)(((int64_t)lpages[pg] * kPage + (p & (kPage - 1))) * T.H + T.h);
+    const uint32_t rh8 = (uint32_t)((p & T.rmask) * T.H + T.h);
+    x.a = ld128(T.k4, hot ? kOOB : rh4 * 128u + 16u * dc);
+    x.s4 = ld16(T.ks4, hot ? kOOB : (rh4 * 8u + dc) * 2u);
+    x.b = ld128(T.rk, hot ? rh8 * 256u + 32u * dc : kOOB);
+    x.c = ld128(T.rk, hot ? rh8 * 256u + 32u * dc + 16u : kOOB);
+    x.s8 = ld16(T.rks, hot ? (rh8 * NG8 + (32u * dc) / G8) * 2u : kOOB);
+    x.hot = hot ? 1 : 0;
   }
   return x;
 }
 
-// V: channels 16 db .. 16 db + 15 of key rows r0, r1.
-template <int G8>
-KVT_DEV RawV fetch_v(const KVSrc& S, RowRef r0, RowRef r1, int H, int h, int db) {
+template <int G8, bool BF16>
+KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int64_t p0, int db) {
   RawV x;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const RowRef r = t == 0 ? r0 : r1;
-    x.kind[t] = r.kind;
-    x.s[t] = 0;
-    x.w[t][0] = make_uint4(0, 0, 0, 0);
-    x.w[t][1] = make_uint4(0, 0, 0, 0);
-    const int64_t rh = r.row * H + h;
-    if (r.kind == 0) {
-      const uint2 c = *reinterpret_cast<const uint2*>(S.v4 + rh * (kD / 2) + 8 * db);
-      x.w[t][0] = make_uint4(c.x, c.y, 0, 0);
-      x.s[t] = S.vs4[rh * (kD / kG4) + db / 2];
-    } else if (r.kind == 1) {
-      x.w[t][0] = *reinterpret_cast<const uint4*>(S.rv + rh * kD + 16 * db);
-      x.s[t] = S.rvs[rh * (kD / G8) + (16 * db) / G8];
-    } else if (r.kind == 2) {
-      const uint4* p = reinterpret_cast<const uint4*>(S.vb + r.row * S.vb_n + (int64_t)h * S.vb_h + 16 * db);
-      x.w[t][0] = p[0];
-      x.w[t][1] = p[1];
+    const int64_t p = min(p0 + t, T.key_end - 1);
+    if constexpr (BF16) {
+      const uint32_t off = (uint32_t)((p * T.vb_n + (int64_t)T.h * T.vb_h + 16 * db) * 2);
+      x.a[t] = ld128(T.vb, off);
+      x.bb[t] = ld128(T.vb, off + 16);
+      x.hot[t] = 2;
+    } else {
+      constexpr int NG8 = kD / G8;
+      const bool hot = p >= T.hs;
+      const int64_t pg = hot ? 0 : min(p >> 6, (int64_t)kMaxLdsPages - 1);
+      const uint32_t rh4 = (uint32_t)(((int64_t)lpages[pg] * kPage + (p & (kPage - 1))) * T.H + T.h);
+      const uint32_t rh8 = (uint32_t)((p & T.rmask) * T.H + T.h);
+      x.c4[t] = ld64(T.v4, hot ? kOOB : rh4 * 128u + 8u * db);
+      x.s4[t] = ld16(T.vs4, hot ? kOOB : (rh4 * 8u + db / 2) * 2u);
+      x.a[t] = ld128(T.rv, hot ? rh8 * 256u + 16u * db : kOOB);
+      x.s8[t] = ld16(T.rvs, hot ? (rh8 * NG8 + (16u * db) / G8) * 2u : kOOB);
+      x.hot[t] = hot ? 1 : 0;
     }
   }
   return x;
@@ -182,29 +192,24 @@ KVT_DEV uint32_t bf16x2_to_f16x2(uint32_t w) {
   return as_u32(r);
 }
 
+KVT_DEV h2 splat(uint32_t s) { return as_h2((s & 0xffffu) | ((s & 0xffffu) << 16)); }
+
 // K row fragment -> LDS (fp16, natural order): 32 channels = 64 bytes.
 KVT_DEV void store_k(const RawK& x, uint8_t* dst) {
   uint32_t o[16];
-  const h2 s2 = as_h2((uint32_t)x.s | ((uint32_t)x.s << 16));
-  if (x.kind == 0) {
-    const uint32_t w[4] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w};
+  if (x.hot == 2) {
+    const uint32_t w[16] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w,
+                            x.c.x, x.c.y, x.c.z, x.c.w, x.d.x, x.d.y, x.d.z, x.d.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) int4_pairs(w[i], s2, o + 4 * i);
-  } else if (x.kind == 1) {
-    const uint32_t w[8] = {x.w[0].x, x.w[0].y, x.w[0].z, x.w[0].w, x.w[1].x, x.w[1].y, x.w[1].z, x.w[1].w};
+    for (int i = 0; i < 16; ++i) o[i] = bf16x2_to_f16x2(w[i]);
+  } else if (x.hot == 1) {
+    const uint32_t w[8] = {x.b.x, x.b.y, x.b.z, x.b.w, x.c.x, x.c.y, x.c.z, x.c.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) int8_pairs(w[i], s2, o + 2 * i);
-  } else if (x.kind == 2) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o[4 * i + 0] = bf16x2_to_f16x2(x.w[i].x);
-      o[4 * i + 1] = bf16x2_to_f16x2(x.w[i].y);
-      o[4 * i + 2] = bf16x2_to_f16x2(x.w[i].z);
-      o[4 * i + 3] = bf16x2_to_f16x2(x.w[i].w);
-    }
+    for (int i = 0; i < 8; ++i) int8_pairs(w[i], splat(x.s8), o + 2 * i);
   } else {
+    const uint32_t w[4] = {x.a.x, x.a.y, x.a.z, x.a.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = 0;
+    for (int i = 0; i < 4; ++i) int4_pairs(w[i], splat(x.s4), o + 4 * i);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -212,30 +217,26 @@ KVT_DEV void store_k(const RawK& x, uint8_t* dst) {
 }
 
 // 16 channels of one V row -> 8 fp16 pairs (natural order).
-KVT_DEV void v_row16(const uint4 w[2], uint16_t s, int kind, uint32_t o[8]) {
-  const h2 s2 = as_h2((uint32_t)s | ((uint32_t)s << 16));
-  if (kind == 0) {
-    int4_pairs(w[0].x, s2, o);
-    int4_pairs(w[0].y, s2, o + 4);
-  } else if (kind == 1) {
-    const uint32_t c[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) int8_pairs(c[i], s2, o + 2 * i);
-  } else if (kind == 2) {
-    const uint32_t c[8] = {w[0].x, w[0].y, w[0].z, w[0].w, w[1].x, w[1].y, w[1].z, w[1].w};
+KVT_DEV void v_row16(const RawV& x, int t, uint32_t o[8]) {
+  if (x.hot[t] == 2) {
+    const uint32_t c[8] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w, x.bb[t].x, x.bb[t].y, x.bb[t].z, x.bb[t].w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = bf16x2_to_f16x2(c[i]);
-  } else {
+  } else if (x.hot[t] == 1) {
+    const uint32_t c[4] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = 0;
+    for (int i = 0; i < 4; ++i) int8_pairs(c[i], splat(x.s8[t]), o + 2 * i);
+  } else {
+    int4_pairs(x.c4[t].x, splat(x.s4[t]), o);
+    int4_pairs(x.c4[t].y, splat(x.s4[t]), o + 4);
   }
 }
 
 // Two keys x 16 channels -> V^T rows (dim 16 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
 KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   uint32_t a[8], b[8];
-  v_row16(x.w[0], x.s[0], x.kind[0], a);
-  v_row16(x.w[1], x.s[1], x.kind[1], b);
+  v_row16(x, 0, a);
+  v_row16(x, 1, b);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
@@ -245,7 +246,7 @@ KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   }
 }
 
-template <int G8>
+template <int G8, bool BF16>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                     const int32_t* kv_lens, int H, int gs, int n_qtiles, float scale, void* out, int out_f32,
@@ -268,13 +269,41 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   const int64_t qt0 = (int64_t)qt * kQT;
   if (qt0 >= q_len) return;
   const int64_t key_end = min(L, q_pos0 + min(q_len, qt0 + kQT));   // keys visible to the tile's last query
-  int64_t hs = 0, rbase = 0, rmask = 0;
-  if (S.kb == nullptr) {
+  constexpr uint32_t NG8 = kD / G8;
+  Tier T;
+  T.H = H;
+  T.h = h;
+  T.key_end = key_end;
+  T.kb_n = S.kb_n;
+  T.kb_h = S.kb_h;
+  T.vb_n = S.vb_n;
+  T.vb_h = S.vb_h;
+  if constexpr (BF16) {
+    const uint32_t kbytes = (uint32_t)(((S.kb_rows - 1) * S.kb_n + (int64_t)(H - 1) * S.kb_h + kD) * 2);
+    const uint32_t vbytes = (uint32_t)(((S.kb_rows - 1) * S.vb_n + (int64_t)(H - 1) * S.vb_h + kD) * 2);
+    T.kb = make_rsrc(S.kb, kbytes);
+    T.vb = make_rsrc(S.vb, vbytes);
+    T.hs = 0;
+    T.rmask = 0;
+  } else {
     const int64_t R = S.ring_len[b];
-    hs = min(max(max(S.ring_start[b], L - R), (int64_t)0), L);
-    rbase = S.ring_base[b];
-    rmask = R - 1;
+    const int64_t rbase = S.ring_base[b];
+    T.hs = min(max(max(S.ring_start[b], L - R), (int64_t)0), L);
+    T.rmask = R - 1;
+    T.k4 = make_rsrc(S.k4, S.pool_rows * (uint32_t)H * 128u);
+    T.v4 = make_rsrc(S.v4, S.pool_rows * (uint32_t)H * 128u);
+    T.ks4 = make_rsrc(S.ks4, S.pool_rows * (uint32_t)H * 16u);
+    T.vs4 = make_rsrc(S.vs4, S.pool_rows * (uint32_t)H * 16u);
+    T.rk = make_rsrc(S.rk + rbase * H * kD, (uint32_t)R * (uint32_t)H * kD);
+    T.rv = make_rsrc(S.rv + rbase * H * kD, (uint32_t)R * (uint32_t)H * kD);
+    T.rks = make_rsrc(S.rks + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
+    T.rvs = make_rsrc(S.rvs + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
+    // page ids of the paged key range, once per block
+    const int64_t npg = min((min(T.hs, key_end) + kPage - 1) / kPage, (int64_t)kMaxLdsPages);
+    for (int64_t i = tid; i < npg; i += 256) lds.pages[i] = S.page_table[b * S.pt_stride + i];
+    if (tid == 0 && npg == 0) lds.pages[0] = 0;
   }
+  __syncthreads();
 
   // ---- Q operands: rows j of block rb = query qt0 + 4 wave + 2 rb + (j >> 3), head j & 7
   h8 qop[2][8];
@@ -309,9 +338,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   const int tk = tid >> 3, dc = tid & 7;
   const int tp = tid & 15, db = tid >> 4;
   const int ntiles = (int)((key_end + kT - 1) / kT);
-  RawK rk_next = fetch_k<G8>(S, locate<G8>(S, b, tk, key_end, hs, rbase, rmask), H, h, dc);
-  RawV rv_next = fetch_v<G8>(S, locate<G8>(S, b, 2 * tp, key_end, hs, rbase, rmask),
-                             locate<G8>(S, b, 2 * tp + 1, key_end, hs, rbase, rmask), H, h, db);
+  RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
+  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
   for (int it = 0; it < ntiles; ++it) {
     const int64_t t0 = (int64_t)it * kT;
     __syncthreads();   // the previous tile's fragments are consumed
@@ -320,9 +348,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     __syncthreads();
     if (it + 1 < ntiles) {   // next tile's codes travel during this tile's matrix work
       const int64_t t1 = t0 + kT;
-      rk_next = fetch_k<G8>(S, locate<G8>(S, b, t1 + tk, key_end, hs, rbase, rmask), H, h, dc);
-      rv_next = fetch_v<G8>(S, locate<G8>(S, b, t1 + 2 * tp, key_end, hs, rbase, rmask),
-                            locate<G8>(S, b, t1 + 2 * tp + 1, key_end, hs, rbase, rmask), H, h, db);
+      rk_next = fetch_k<G8, BF16>(T, lds.pages, t1 + tk, dc);
+      rv_next = fetch_v<G8, BF16>(T, lds.pages, t1 + 2 * tp, db);
     }
     // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16
     float s[2][2][4];
@@ -352,13 +379,12 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[rb][nt][r]);
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      mloc = max_xor16_32(mloc);
+      // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
+      // by more than 8 (log2 units), so P = 2^(s - m) <= 256 stays well inside fp16
       const float m_new = fmaxf(m_run[rb], mloc);
-      // rows with no visible key yet keep m = -inf and contribute nothing
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      if (__any(m_new > m_run[rb])) {
-        const float alpha = m_run[rb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_use);
+      if (__any(m_new > m_run[rb] + 8.0f)) {
+        const float alpha = m_run[rb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_new);
         l_run[rb] *= alpha;
         float arow[4];
 #pragma unroll
@@ -367,8 +393,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         for (int c = 0; c < 16; ++c)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[rb][c][i] *= arow[i];
+        m_run[rb] = m_new;
       }
-      m_run[rb] = m_new;
+      // rows with no visible key yet keep m = -inf and contribute nothing
+      const float m_use = m_run[rb] == -INFINITY ? 0.f : m_run[rb];
       float psum = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
@@ -397,9 +425,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   // head 4 (kb & 1) + i; column n16 of block c = dim 16 c + n16
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
-    float l = l_run[rb];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = sum_xor16_32(l_run[rb]);
     const int64_t qi = qt0 + 4 * wave + 2 * rb + (kb >> 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -429,31 +455,40 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
                      const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
                      const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
-                     const void* ring_start, const void* page_table, int64_t pt_stride, const void* k_bf16,
-                     const void* v_bf16, int64_t kb_n, int64_t kb_h, int64_t vb_n, int64_t vb_h, float scale,
-                     void* out, int out_f32, int64_t so_n, int64_t so_h, void* stream) {
+                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
+                     const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
+                     int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
+                     void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || Hq / H > 8 || max_q < 0) return KVT_EINVAL;
   if ((k_bf16 == nullptr) != (v_bf16 == nullptr)) return KVT_EINVAL;
+  const bool bf16 = k_bf16 != nullptr;
+  // 32-bit byte offsets inside each buffer
+  if (!bf16 && (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL)) return KVT_ERANGE;
+  if (bf16 && (kb_rows <= 0 || (kb_rows * kb_n + H * kb_h) * 2 > 0x7fffffffLL ||
+               (kb_rows * vb_n + H * vb_h) * 2 > 0x7fffffffLL))
+    return KVT_ERANGE;
   if (max_q == 0) return KVT_OK;
   KVSrc S{(const uint8_t*)k4,        (const uint8_t*)v4,       (const uint16_t*)ks4,    (const uint16_t*)vs4,
           (const int8_t*)rk,         (const int8_t*)rv,        (const uint16_t*)rks,    (const uint16_t*)rvs,
           (const int64_t*)ring_base, (const int32_t*)ring_len, (const int64_t*)ring_start,
-          (const int32_t*)page_table, pt_stride,               (const uint16_t*)k_bf16, (const uint16_t*)v_bf16,
-          kb_n, kb_h, vb_n, vb_h};
+          (const int32_t*)page_table, pt_stride,               (uint32_t)pool_rows,      (const uint16_t*)k_bf16,
+          (const uint16_t*)v_bf16,   kb_n, kb_h, vb_n, vb_h, kb_rows};
   const int n_qtiles = (max_q + kQT - 1) / kQT;
   const dim3 grid((unsigned)n_qtiles, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
-  if (group8 == 64) {
-    hipLaunchKernelGGL(prefill_mfma_kernel<64>, grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,
-                       cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n,
-                       so_h);
+#define KVT_PF(G, B)                                                                                              \
+  hipLaunchKernelGGL((prefill_mfma_kernel<G, B>), grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,  \
+                     cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n, so_h)
+  if (bf16) {
+    KVT_PF(64, true);
+  } else if (group8 == 64) {
+    KVT_PF(64, false);
   } else if (group8 == 256) {
-    hipLaunchKernelGGL(prefill_mfma_kernel<256>, grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,
-                       cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n,
-                       so_h);
+    KVT_PF(256, false);
   } else {
     return KVT_EINVAL;
   }
+#undef KVT_PF
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }

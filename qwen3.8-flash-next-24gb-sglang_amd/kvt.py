@@ -351,6 +351,8 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
         assert k_src.stride(2) == 1 and v_src.stride(2) == 1 and k_src.shape[1:] == (H, D) == v_src.shape[1:]
         if min(k_src.shape[0], v_src.shape[0]) < int(kv_lens[0]):
             raise ValueError("k_src / v_src hold fewer rows than the context length")
+    elif max((cache.hot_start(s) for s in range(batch)), default=0) > 8192 * 64:
+        raise ValueError("kvt_prefill_attn: paged key ranges beyond 524,288 positions are not supported")
     _lib.require_device(q, out, k_src, v_src)
     if batch == 0 or max_q == 0:
         return out
@@ -360,7 +362,8 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
               cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
               cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
               cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
-              cache.page_table.stride(0), _lib.ptr(k_src), _lib.ptr(v_src),
+              cache.page_table.stride(0), cache.k4[layer].shape[0], _lib.ptr(k_src), _lib.ptr(v_src),
+              min(k_src.shape[0], v_src.shape[0]) if k_src is not None else 0,
               k_src.stride(0) if k_src is not None else 0, k_src.stride(1) if k_src is not None else 0,
               v_src.stride(0) if v_src is not None else 0, v_src.stride(1) if v_src is not None else 0,
               1.0 / math.sqrt(D), out.data_ptr(), int(out.dtype == torch.float32), out.stride(0), out.stride(1),
