@@ -120,26 +120,30 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 
 /* Split-K GQA decode attention on the matrix cores (v_mfma_f32_16x16x32_f16) over position rings + page tables
  * (the mode-0 layout of kvt_decode_ref): QK^T with exact fp16 integer codes and the per-group scales folded in
- * fp32, P.V with fp16 P and fp16 code*scale values, fp32 accumulation.  Each (sequence, KV head) gets n_splits
- * partials (4 wavefront ranges each, of equal cost), in the layout of
- * kvt_decode_ref; merge them with kvt_decode_combine(chunk = 0).  Hq / H <= 8, D = 256; pool_rows = rows of the
- * INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 < 2^31, else KVT_ERANGE).  No reference counterpart:
- * it replaces the compact gather + FA2 pair (flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for
- * dense decode. */
+ * fp32, P.V with fp16 P and fp16 code*scale values, fp32 accumulation.  Each split holds 4 wavefront ranges of
+ * equal cost.  split_map NULL: every (sequence, KV head) gets n_splits splits; otherwise split_map (int32
+ * [n_map][3] = {sequence, split index, splits of that sequence}) lists the splits (per-sequence counts for ragged
+ * batches) and n_splits is the partial slot stride per (sequence, head).  Partials in the layout of kvt_decode_ref;
+ * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 8, D = 256; pool_rows = rows of the INT4
+ * pool (byte offsets are 32-bit: pool_rows * H * D / 2 < 2^31, else KVT_ERANGE).  No reference counterpart: it
+ * replaces the compact gather + FA2 pair (flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense
+ * decode. */
 int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
-                    float scale, int n_splits, void* part_o, void* part_ml, void* stream);
+                    float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
+                    void* stream);
 
 /* Merge the split-K partials: out[b, hq, :] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c (fp32 and/or bf16
  * output, either may be NULL; batch stride out_stride_b elements).  chunk > 0: split c covers positions
- * [c chunk, (c + 1) chunk) and splits beyond the length are skipped; chunk = 0: all n_chunks splits hold partials
- * (an empty one carries m = -inf).  An empty context yields NaN (0/0), as the
- * reference's chunk kernel (gemv/test_kv_paged_prefix.py:524-526). */
+ * [c chunk, (c + 1) chunk) and splits beyond the length are skipped; chunk = 0: the first split_counts[b] of the
+ * n_chunks slots of sequence b hold partials (all n_chunks if split_counts is NULL; an empty one carries
+ * m = -inf).  An empty context yields NaN (0/0), as the reference's chunk kernel
+ * (gemv/test_kv_paged_prefix.py:524-526). */
 int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
-                       int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
-                       void* stream);
+                       int64_t chunk, const void* seq_lens, const void* split_counts, void* out_f32, void* out_bf16,
+                       int64_t out_stride_b, void* stream);
 
 /* Causal prefill attention of a chunk of queries over the position-indexed tiered cache on the matrix cores
  * (v_mfma_f32_16x16x32_f16, K/V tiles dequantized once per 16 queries into LDS).  Sequence b's queries are rows

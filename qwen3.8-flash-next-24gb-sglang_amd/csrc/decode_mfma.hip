@@ -665,21 +665,33 @@ KVT_DEV void hot_segment(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, c
 template <int G8>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32_t* seq_lens, int H, int gs,
-                   int n_splits, float scale, float* part_o, float* part_ml, uint32_t pool_rows) {
+                   int n_splits, const int32_t* split_map, float scale, float* part_o, float* part_ml,
+                   uint32_t pool_rows) {
   __shared__ Lds lds;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar addressing of the page table
   const int n16 = lane & 15, kb = lane >> 4;
-  const int c = blockIdx.x;
-  const int b = blockIdx.y / H;
-  const int h = blockIdx.y - b * H;
-  const int64_t item = ((int64_t)b * H + h) * n_splits + c;
+  // split c of n_b for sequence b: uniform (grid.x = n_splits, grid.y = batch x H) or from the split map
+  // (grid.x = total splits, grid.y = H; entry = {b, c, n_b})
+  int b, c, h, n_b;
+  if (split_map != nullptr) {
+    b = split_map[3 * blockIdx.x];
+    c = split_map[3 * blockIdx.x + 1];
+    n_b = split_map[3 * blockIdx.x + 2];
+    h = blockIdx.y;
+  } else {
+    c = blockIdx.x;
+    b = blockIdx.y / H;
+    h = blockIdx.y - b * H;
+    n_b = n_splits;
+  }
+  const int64_t item = ((int64_t)b * H + h) * n_splits + c;   // partial slots: n_splits per (sequence, head)
   const int64_t L = seq_lens[b];
   const int64_t R = A.ring_len[b];
   const int64_t rbase = A.ring_base[b];
   const int64_t hs = min(max(max(A.ring_start[b], L - R), (int64_t)0), L);   // first ring position
   // this wavefront's positions [w0, w1): equal shares of the cost 4 hs + kHotCost4 (L - hs)
-  const int64_t n_w = (int64_t)n_splits * kWaves;
+  const int64_t n_w = (int64_t)n_b * kWaves;
   const int64_t wg = (int64_t)c * kWaves + wave;
   const int64_t cost = 4 * hs + kHotCost4 * (L - hs);
   auto bound = [&](int64_t w) -> int64_t {
@@ -789,24 +801,28 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
-                    float scale, int n_splits, void* part_o, void* part_ml, void* stream) {
+                    float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
+                    void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD) return KVT_EINVAL;
   if (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL) return KVT_ERANGE;   // 32-bit byte offsets
   const int gs = Hq / H;
-  if (gs > 8 || n_splits <= 0) return KVT_EINVAL;
+  if (gs > 8 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
   PosArgs A{(const uint8_t*)k4,         (const uint8_t*)v4,        (const uint16_t*)ks4,     (const uint16_t*)vs4,
             (const int8_t*)rk,          (const int8_t*)rv,         (const uint16_t*)rks,     (const uint16_t*)rvs,
             (const int64_t*)ring_base,  (const int32_t*)ring_len,  (const int64_t*)ring_start,
             (const int32_t*)page_table, pt_stride};
-  const dim3 grid((unsigned)n_splits, (unsigned)(batch * H));
+  const dim3 grid = split_map != nullptr ? dim3((unsigned)n_map, (unsigned)H)
+                                         : dim3((unsigned)n_splits, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
   if (group8 == 64) {
     hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(256), 0, st, A, (const uint16_t*)q, q_stride_b,
-                       (const int32_t*)seq_lens, H, gs, n_splits, scale, (float*)part_o, (float*)part_ml,
+                       (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
+                       (float*)part_o, (float*)part_ml,
                        (uint32_t)pool_rows);
   } else if (group8 == 256) {
     hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(256), 0, st, A, (const uint16_t*)q, q_stride_b,
-                       (const int32_t*)seq_lens, H, gs, n_splits, scale, (float*)part_o, (float*)part_ml,
+                       (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
+                       (float*)part_o, (float*)part_ml,
                        (uint32_t)pool_rows);
   } else {
     return KVT_EINVAL;

@@ -194,7 +194,8 @@ KVT_DEV void merge_into(float& m, float& num, float& den, float mc, float oc, fl
 
 __global__ void __launch_bounds__(kCombDims * kCombParts) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
-    const int32_t* seq_lens, float* out_f32, uint16_t* out_bf16, int64_t out_stride_b) {
+    const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
+    int64_t out_stride_b) {
   __shared__ float red[kCombParts][3][kCombDims];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
@@ -203,7 +204,9 @@ __global__ void __launch_bounds__(kCombDims * kCombParts) decode_combine_kernel(
   const int d = blockIdx.x * kCombDims + dl;
   const int64_t L = seq_lens[b];
   // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
-  const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk) : n_chunks;
+  // split_counts (chunk 0): sequence b uses the first split_counts[b] slots
+  const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
+                             : (split_counts != nullptr ? split_counts[b] : n_chunks);
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
   float m = -INFINITY, num = 0.0f, den = 0.0f;
   for (int c0 = part; c0 < used; c0 += kCombUnroll * kCombParts) {
@@ -277,14 +280,15 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 }
 
 int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H, int Hq, int D, int n_chunks,
-                       int64_t chunk, const void* seq_lens, void* out_f32, void* out_bf16, int64_t out_stride_b,
-                       void* stream) {
+                       int64_t chunk, const void* seq_lens, const void* split_counts, void* out_f32, void* out_bf16,
+                       int64_t out_stride_b, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % kCombDims != 0) return KVT_EINVAL;
   hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch),
                      dim3(kCombDims * kCombParts), 0,
                      (hipStream_t)stream,
                      (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
-                     (const int32_t*)seq_lens, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b);
+                     (const int32_t*)seq_lens, (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16,
+                     out_stride_b);
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }

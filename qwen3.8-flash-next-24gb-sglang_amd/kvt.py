@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import List, Optional, Sequence
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -211,6 +211,27 @@ def _choose_splits_mfma(max_len: int, items: int, blocks: int = 512) -> int:
     return int(max(1, min(n, -(-max_len // 256))))
 
 
+def _split_counts_mfma(lens: Sequence[int], H: int, blocks: int = 512) -> List[int]:
+    """Per-sequence split counts of the MFMA kernel for a ragged batch: about `blocks` blocks in all, shared in
+    proportion to the context lengths (each sequence at least 1, each wavefront at least 64 positions)."""
+    per_head = max(1, blocks // max(1, H))
+    tot = max(1, sum(lens))
+    return [int(max(1, min(-(-L // 256), round(per_head * L / tot)))) for L in lens]
+
+
+def _split_map(counts: List[int], ws: dict, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Device split map {sequence, index, count} per split and the per-sequence counts, cached in the workspace
+    while the counts stay the same (lengths grow by one per step; the counts change rarely)."""
+    key = ("split_map", tuple(counts))
+    hit = ws.get("split_map_key")
+    if hit != key:
+        rows = [(b, c, n) for b, n in enumerate(counts) for c in range(n)]
+        ws["split_map"] = torch.tensor(rows, dtype=torch.int32).reshape(-1).to(device)
+        ws["split_counts"] = torch.tensor(counts, dtype=torch.int32).to(device)
+        ws["split_map_key"] = key
+    return ws["split_map"], ws["split_counts"]
+
+
 def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
                     impl: str = "ref", chunk: Optional[int] = None, max_len: Optional[int] = None,
                     out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
@@ -219,7 +240,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
 
     q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
     every position of each sequence, K/V dequantized from the INT4 pages (positions < hot_start) and the INT8 ring.
-    impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per (sequence, KV head).
+    impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per (sequence, KV head), or, by
+    default for more than one sequence, split counts in proportion to each sequence's length.
     events: if a list, timing events (start, after the split-K kernel, after the combine) are appended.
     """
     S = cache.n_seqs
@@ -231,14 +253,21 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     gs = Hq // H
     if max_len is None:
         max_len = max(cache.h_len) if S else 0
+    ws = workspace if workspace is not None else {}
+    split_map = split_counts = None
+    n_map = 0
     if impl == "mfma":
-        n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)
         chunk = 0   # every split holds a partial
+        if splits is None and S > 1:
+            counts = _split_counts_mfma(cache.h_len[:S], H)
+            split_map, split_counts = _split_map(counts, ws, q.device)
+            n_chunks, n_map = max(counts), sum(counts)
+        else:
+            n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)
     else:
         if chunk is None:
             chunk = _choose_chunk(max_len, S * H)
         n_chunks = max(1, -(-max_len // chunk))
-    ws = workspace if workspace is not None else {}
     need_o = S * H * n_chunks * gs * D
     po = ws.get("part_o")
     if po is None or po.numel() < need_o:
@@ -271,14 +300,14 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                   cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
                   cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
-                  cache.page_table.stride(0), cache.k4[layer].shape[0], scale, n_chunks, po.data_ptr(),
-                  pml.data_ptr(), _lib.stream())
+                  cache.page_table.stride(0), cache.k4[layer].shape[0], scale, n_chunks, _lib.ptr(split_map), n_map,
+                  po.data_ptr(), pml.data_ptr(), _lib.stream())
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
         ev1.record()
     _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), S, H, Hq, D, n_chunks, chunk,
-              cache.seq_lens.data_ptr(), out.data_ptr() if out.dtype == torch.float32 else None,
+              cache.seq_lens.data_ptr(), _lib.ptr(split_counts), out.data_ptr() if out.dtype == torch.float32 else None,
               out.data_ptr() if out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
     if events is not None:
         ev2 = torch.cuda.Event(enable_timing=True)
@@ -315,7 +344,7 @@ def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, 
               req_to_token.stride(0), req_indices.data_ptr(), owner.data_ptr(), int(ring_mask), 1.0 / math.sqrt(D),
               chunk, n_chunks, po.data_ptr(), pml.data_ptr(), _lib.stream())
     _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), B, H, Hq, D, n_chunks, chunk, seq_lens.data_ptr(),
-              out.data_ptr() if out_dtype == torch.float32 else None,
+              None, out.data_ptr() if out_dtype == torch.float32 else None,
               out.data_ptr() if out_dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
     return out
 
