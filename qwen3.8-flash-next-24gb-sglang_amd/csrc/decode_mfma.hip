@@ -239,17 +239,16 @@ KVT_DEV void cold_lane_offsets(ColdCtx& C) {
   C.soff = ((uint32_t)(lane & 31) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
 }
 
-// Issue the direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`:
-// exactly 10 vector-memory instructions per wavefront (the vmcnt accounting of cold_step relies on it).
-KVT_DEV void cold_issue(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
+// Direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`, in two parts so
+// that a wavefront does not stall on a full memory queue with the whole tile at once: cold_issue_k copies the K codes
+// and both scale rows (exactly 6 vector-memory instructions), cold_issue_v the V codes (exactly 4).  The vmcnt
+// accounting of cold_step relies on these counts.
+KVT_DEV void cold_issue_k(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
   const int lane = threadIdx.x & 63;
   if (n == 32) {   // full tile: one add per copy
     const uint32_t cb = row0 * C.rowbytes, sb = row0 * (uint32_t)C.H * 16u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
-      copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
-    }
+    for (int j = 0; j < 4; ++j) copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
     if (lane < 32) {
       copy16_to_lds(C.rks4, &st.ks[0][0], sb + C.soff);
       copy16_to_lds(C.rvs4, &st.vsn[0][0], sb + C.soff);
@@ -261,9 +260,7 @@ KVT_DEV void cold_issue(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
     const int t = 8 * j + (lane >> 3);
     const int tt = t < n ? t : n - 1;
     const uint32_t chunk = (uint32_t)((lane & 7) ^ (t & 7));
-    const uint32_t off = (row0 + tt) * C.rowbytes + C.hoff + 16u * chunk;
-    copy16_to_lds(C.rk4, st.k + 1024 * j, off);
-    copy16_to_lds(C.rv4, st.v + 1024 * j, off);
+    copy16_to_lds(C.rk4, st.k + 1024 * j, (row0 + tt) * C.rowbytes + C.hoff + 16u * chunk);
   }
   const int tl = (lane & 31) < n ? (lane & 31) : n - 1;
   const uint32_t srow = (row0 + tl) * (uint32_t)C.H + (uint32_t)C.h;
@@ -272,6 +269,31 @@ KVT_DEV void cold_issue(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
     copy16_to_lds(C.rvs4, &st.vsn[0][0], srow * 16u);
   }
 }
+
+KVT_DEV void cold_issue_v(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
+  const int lane = threadIdx.x & 63;
+  if (n == 32) {
+    const uint32_t cb = row0 * C.rowbytes;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = 8 * j + (lane >> 3);
+    const int tt = t < n ? t : n - 1;
+    const uint32_t chunk = (uint32_t)((lane & 7) ^ (t & 7));
+    copy16_to_lds(C.rv4, st.v + 1024 * j, (row0 + tt) * C.rowbytes + C.hoff + 16u * chunk);
+  }
+}
+
+// The next tile's V copies, issued from inside the current tile's computation (after QK^T).
+struct NextV {
+  const ColdCtx* C;
+  ColdStage* st;   // nullptr: no next tile
+  uint32_t row0;
+  int n;
+};
 
 // V scales of the tile into the transposed [group][token] layout (lanes 0-31 move one token each).
 KVT_DEV void cold_scatter_vs(ColdStage& st) {
@@ -293,10 +315,27 @@ KVT_DEV uint32_t lds_code_dword(const uint8_t* base, int t, int chunk, int dw) {
 
 // Attention over one staged cold tile (n valid tokens).
 KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias, int bexp, float cscale, f4 acc[8],
-                          float& m_run, float& l_run) {
+                          float& m_run, float& l_run, const NextV& nv) {
   const int lane = threadIdx.x & 63;
   const int n16 = lane & 15, kb = lane >> 4;
   const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  // V codes and scales of P.V are read first: their LDS latency overlaps the QK^T matrix work
+  const int kbp = kb ^ 2;                              // block of the partner lane (lane ^ 32)
+  const int ga = n16 >> 2, gb = 4 + (n16 >> 2);      // INT4 scale groups of dims A (8 n16 ..) and B (8 (n16+16) ..)
+  uint32_t wo[8], wp[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int te = e < 4 ? e : 12 + e;
+    wo[e] = lds_code_dword(st.v, 4 * kb + te, n16 >> 2, n16 & 3);
+    wp[e] = lds_code_dword(st.v, 4 * kbp + te, 4 + (n16 >> 2), n16 & 3);
+  }
+  h2 so[4], sp[4];
+#pragma unroll
+  for (int pr = 0; pr < 4; ++pr) {
+    const int te = (2 * pr) < 4 ? 2 * pr : 12 + 2 * pr;
+    so[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[ga][4 * kb + te]));
+    sp[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[gb][4 * kbp + te]));
+  }
   // QK^T per 16-token half, software-pipelined over the groups: the MFMA of group g + 1 is in flight while the
   // result of group g is folded with its scales (the fold no longer waits on the matrix core)
   float s[2][4];
@@ -336,6 +375,7 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
       for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
     }
   }
+  if (nv.st != nullptr) cold_issue_v(*nv.C, *nv.st, nv.row0, nv.n);
   // online softmax over the tile
   float mloc = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
@@ -363,7 +403,6 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
     }
   l_run += psum;
   // P.V (block-diagonal, see the file header)
-  const int kbp = kb ^ 2;
   const bool lowrow = n16 < 8;
   const h8 pown = {(_Float16)s[0][0], (_Float16)s[0][1], (_Float16)s[0][2], (_Float16)s[0][3],
                    (_Float16)s[1][0], (_Float16)s[1][1], (_Float16)s[1][2], (_Float16)s[1][3]};
@@ -374,23 +413,6 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
   const u4v zero = {0u, 0u, 0u, 0u};
   const h8 ax = as_h8(lowrow ? po : zero);
   const h8 ay = as_h8(lowrow ? zero : pp);
-  const int ga = n16 >> 2, gb = 4 + (n16 >> 2);      // INT4 scale groups of dims A (8 n16 ..) and B (8 (n16+16) ..)
-  uint32_t wo[8], wp[8];
-  int tok_o[8], tok_p[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int te = e < 4 ? e : 12 + e;
-    tok_o[e] = 4 * kb + te;
-    tok_p[e] = 4 * kbp + te;
-    wo[e] = lds_code_dword(st.v, tok_o[e], n16 >> 2, n16 & 3);
-    wp[e] = lds_code_dword(st.v, tok_p[e], 4 + (n16 >> 2), n16 & 3);
-  }
-  h2 so[4], sp[4];
-#pragma unroll
-  for (int pr = 0; pr < 4; ++pr) {
-    so[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[ga][tok_o[2 * pr]]));
-    sp[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[gb][tok_p[2 * pr]]));
-  }
   const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
   const h2 sc16 = {(_Float16)0.0625f, (_Float16)0.0625f};
   const h2 off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
@@ -435,15 +457,20 @@ template <int S>
 KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdTiles& T, int i, int ntiles, const h8 qop[8],
                        h8 kbias, int bexp, float cscale, f4 acc[8], float& m_run, float& l_run) {
   // (the loop issues no vector-memory instruction besides the tile copies: the vmcnt counts below are exact)
+  // in flight here, oldest first: K/scales of tile i (6), V of tile i (4), then K/scales of tile i + 1 (6)
+  NextV nv{&C, nullptr, 0u, 0};
   if (i + 1 < ntiles) {
-    cold_issue(C, W.cold[S ^ 1], T.row0(i + 1), T.n(i + 1));
-    wait_vmcnt<10>();                   // tile i's copies have landed
+    nv.st = &W.cold[S ^ 1];
+    nv.row0 = T.row0(i + 1);
+    nv.n = T.n(i + 1);
+    cold_issue_k(C, W.cold[S ^ 1], nv.row0, nv.n);
+    wait_vmcnt<6>();                    // tile i's copies have landed
   } else {
     wait_vmcnt<0>();
   }
   cold_scatter_vs(W.cold[S]);
   wave_sync();
-  cold_compute(W.cold[S], T.n(i), qop, kbias, bexp, cscale, acc, m_run, l_run);
+  cold_compute(W.cold[S], T.n(i), qop, kbias, bexp, cscale, acc, m_run, l_run, nv);   // issues tile i + 1's V
   wave_sync();
 }
 
@@ -462,7 +489,8 @@ KVT_DEV void cold_segment(const PosArgs& A, const ColdCtx& C, WaveArea& W, int b
     T.pages = lane < npg ? A.page_table[b * A.pt_stride + T.pg0 + lane] : 0;
     const int ntiles = (int)((s1 - s0 + 31) >> 5);
     wave_sync();
-    cold_issue(C, W.cold[0], T.row0(0), T.n(0));
+    cold_issue_k(C, W.cold[0], T.row0(0), T.n(0));
+    cold_issue_v(C, W.cold[0], T.row0(0), T.n(0));
     for (int i = 0; i < ntiles; i += 2) {
       cold_step<0>(C, W, T, i, ntiles, qop, kbias, bexp, cscale, acc, m_run, l_run);
       if (i + 1 < ntiles) cold_step<1>(C, W, T, i + 1, ntiles, qop, kbias, bexp, cscale, acc, m_run, l_run);
