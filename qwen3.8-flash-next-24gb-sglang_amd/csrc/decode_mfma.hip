@@ -48,6 +48,7 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;
 constexpr int kD = 256;
@@ -105,7 +106,7 @@ KVT_DEV h8 int8_codes_to_h8(uint32_t w0, uint32_t w1) {
 
 // One 32-token tile of one KV head in LDS (cold path).
 struct ColdStage {
-  uint8_t k[32 * 128];    // K codes, token-major rows; 16-B slot s of token t holds chunk s ^ (t & 7)
+  uint8_t k[32 * 128];    // K codes, token-major rows; 16-B slot s of token t holds chunk s ^ ckey(t)
   uint8_t v[32 * 128];    // V codes, same layout
   uint16_t ks[32][8];     // K scales [token][group]
   uint16_t vsn[32][8];    // V scales [token][group], as copied
@@ -174,23 +175,46 @@ KVT_DEV void wave_sync() {
   asm volatile("" ::: "memory");
 }
 
+// Channels 32 g + 8 kb .. + 7 (g = 0..7) of one q head row as fp32, natural order.  Every load is unconditional (a
+// lane whose head is beyond the group reads head 0 of the group and zeroes the values afterwards), so the loads go out
+// back to back; 16-byte loads when the rows are 16-byte aligned.
+KVT_DEV void load_q_rows(const uint16_t* qrow, bool vec16, int kb, float x[8][8]) {
+  if (vec16) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qrow + 32 * g + 8 * kb);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[g][2 * j] = __uint_as_float(w[j] << 16);
+        x[g][2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[g][e] = bf16_to_f32(qrow[32 * g + 8 * kb + e]);
+  }
+}
+
 // Q of the INT8 ring path (q head n % 8 of the group, channel block kb) as 8 MFMA B operands in natural channel
 // order; zero for heads beyond the group.
-KVT_DEV void load_q_ring(const uint16_t* qrow, bool valid, int kb, h8 qop[8]) {
+KVT_DEV void load_q_ring(const uint16_t* qrow, bool vec16, bool valid, int kb, h8 qop[8]) {
+  float x[8][8];
+  load_q_rows(qrow, vec16, kb, x);
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
+  for (int g = 0; g < 8; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = bf16_to_f32(qrow[32 * g + 8 * kb + e]);
-      qop[g][e] = (_Float16)(valid ? x : 0.0f);
-    }
-  }
+    for (int e = 0; e < 8; ++e) qop[g][e] = (_Float16)(valid ? x[g][e] : 0.0f);
 }
 
 // Q of the INT4 path in the order [0,4,1,5,2,6,3,7] with odd channels divided by 16, and the B operand of the bias
 // MFMA: lanes kb = 0 / 1 hold the leading / remainder fp16 parts of -bias_g * 2^-bexp for g = 0..7, kb >= 2 zero.
-KVT_DEV void load_q_int4(const uint16_t* qrow, bool valid, int kb, h8 qop[8], h8& kbias, int& bexp) {
+KVT_DEV void load_q_int4(const uint16_t* qrow, bool vec16, bool valid, int kb, h8 qop[8], h8& kbias, int& bexp) {
   constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+  float x[8][8];
+  load_q_rows(qrow, vec16, kb, x);
   float bias[8];
 #pragma unroll
   for (int g = 0; g < 8; ++g) {
@@ -198,8 +222,8 @@ KVT_DEV void load_q_int4(const uint16_t* qrow, bool valid, int kb, h8 qop[8], h8
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool odd = (e & 2) != 0;   // e = 2, 3, 6, 7 hold channels 1, 5, 3, 7 of the block
-      const float x = valid ? bf16_to_f32(qrow[32 * g + 8 * kb + perm[e]]) : 0.0f;
-      const _Float16 hq = (_Float16)(odd ? x * 0.0625f : x);
+      const float xv = valid ? x[g][perm[e]] : 0.0f;
+      const _Float16 hq = (_Float16)(odd ? xv * 0.0625f : xv);
       qop[g][e] = hq;
       part = fmaf(odd ? 1152.0f : 1032.0f, (float)hq, part);
     }
@@ -228,72 +252,46 @@ struct ColdCtx {
   uint32_t soff;                // this lane's scale byte offset (lanes < 32), relative to row0 * H * 16
 };
 
+// Swizzle of a paged tile in LDS: the 16-byte chunk c (one INT4 scale group) of token t (0..31) sits in slot
+// c ^ ckey(t) of the token's 128-byte row.  The QK^T reads (16 tokens 8 a + b, b < 4, one dword of one chunk) then
+// hit 8 slots twice each (2-way, the minimum for 128-byte rows), the transposed P.V reads (8 consecutive tokens of
+// one chunk, 8 bytes per lane) hit 8 distinct slots (conflict-free).
+KVT_DEV int ckey(int t) { return (t ^ ((t >> 3) << 1)) & 7; }
+
 // Per-lane parts of the copy offsets of a full 32-token tile (computed once per wavefront).
 KVT_DEV void cold_lane_offsets(ColdCtx& C) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = 8 * j + (lane >> 3);
-    C.coff[j] = (uint32_t)t * C.rowbytes + C.hoff + 16u * (uint32_t)((lane & 7) ^ (t & 7));
+    C.coff[j] = (uint32_t)t * C.rowbytes + C.hoff + 16u * (uint32_t)((lane & 7) ^ ckey(t));
   }
   C.soff = ((uint32_t)(lane & 31) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
 }
 
-// Direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`, in two parts so
-// that a wavefront does not stall on a full memory queue with the whole tile at once: cold_issue_k copies the K codes
-// and both scale rows (exactly 6 vector-memory instructions), cold_issue_v the V codes (exactly 4).  The vmcnt
-// accounting of cold_step relies on these counts.
+// Direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`, in two parts:
+// cold_issue_k copies the K codes and both scale rows (exactly 6 vector-memory instructions), cold_issue_v the V codes
+// (exactly 4).  The vmcnt accounting of the tile loop relies on these counts.  Rows beyond n are copied as they are
+// (they lie in the same page: finite codes, masked scores); the scale rows of tokens beyond n repeat row n - 1, so
+// every scale that meets a zero probability is finite.
 KVT_DEV void cold_issue_k(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
   const int lane = threadIdx.x & 63;
-  if (n == 32) {   // full tile: one add per copy
-    const uint32_t cb = row0 * C.rowbytes, sb = row0 * (uint32_t)C.H * 16u;
+  const uint32_t cb = row0 * C.rowbytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
-    if (lane < 32) {
-      copy16_to_lds(C.rks4, &st.ks[0][0], sb + C.soff);
-      copy16_to_lds(C.rvs4, &st.vsn[0][0], sb + C.soff);
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = 8 * j + (lane >> 3);
-    const int tt = t < n ? t : n - 1;
-    const uint32_t chunk = (uint32_t)((lane & 7) ^ (t & 7));
-    copy16_to_lds(C.rk4, st.k + 1024 * j, (row0 + tt) * C.rowbytes + C.hoff + 16u * chunk);
-  }
-  const int tl = (lane & 31) < n ? (lane & 31) : n - 1;
-  const uint32_t srow = (row0 + tl) * (uint32_t)C.H + (uint32_t)C.h;
+  for (int j = 0; j < 4; ++j) copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
+  const uint32_t tl = (uint32_t)min(lane & 31, n - 1);
+  const uint32_t soff = ((row0 + tl) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
   if (lane < 32) {
-    copy16_to_lds(C.rks4, &st.ks[0][0], srow * 16u);
-    copy16_to_lds(C.rvs4, &st.vsn[0][0], srow * 16u);
+    copy16_to_lds(C.rks4, &st.ks[0][0], soff);
+    copy16_to_lds(C.rvs4, &st.vsn[0][0], soff);
   }
 }
 
-KVT_DEV void cold_issue_v(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
-  const int lane = threadIdx.x & 63;
-  if (n == 32) {
-    const uint32_t cb = row0 * C.rowbytes;
+KVT_DEV void cold_issue_v(const ColdCtx& C, ColdStage& st, uint32_t row0) {
+  const uint32_t cb = row0 * C.rowbytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = 8 * j + (lane >> 3);
-    const int tt = t < n ? t : n - 1;
-    const uint32_t chunk = (uint32_t)((lane & 7) ^ (t & 7));
-    copy16_to_lds(C.rv4, st.v + 1024 * j, (row0 + tt) * C.rowbytes + C.hoff + 16u * chunk);
-  }
+  for (int j = 0; j < 4; ++j) copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
 }
-
-// The next tile's V copies, issued from inside the current tile's computation (after QK^T).
-struct NextV {
-  const ColdCtx* C;
-  ColdStage* st;   // nullptr: no next tile
-  uint32_t row0;
-  int n;
-};
 
 // V scales of the tile into the transposed [group][token] layout (lanes 0-31 move one token each).
 KVT_DEV void cold_scatter_vs(ColdStage& st) {
@@ -309,47 +307,34 @@ KVT_DEV void cold_scatter_vs(ColdStage& st) {
   }
 }
 
-KVT_DEV uint32_t lds_code_dword(const uint8_t* base, int t, int chunk, int dw) {
-  return *reinterpret_cast<const uint32_t*>(base + t * 128 + 16 * (chunk ^ (t & 7)) + 4 * dw);
-}
+// 32-bit LDS address of a pointer into the shared block, and back.
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+KVT_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
 
-// Attention over one staged cold tile (n valid tokens).
-KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias, int bexp, float cscale, f4 acc[8],
-                          float& m_run, float& l_run, const NextV& nv) {
+// QK^T of one staged tile.  Block nt (0, 1) of 16 A rows: row i is token 8 (i >> 2) + 4 nt + (i & 3), so that the
+// D layout leaves lane (n16, kb) with the scores of q head n16 % 8 for tokens 8 kb + 4 nt + r in s[4 nt + r]: the
+// lane's 8 scores are tokens 8 kb .. 8 kb + 7 in natural order, the A operand of P.V.  Scores in log2 units.
+KVT_DEV void cold_qk(const ColdStage& st, const h8 qop[8], h8 kbias, int bexp, float cscale, float s[8]) {
   const int lane = threadIdx.x & 63;
   const int n16 = lane & 15, kb = lane >> 4;
   const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
-  // V codes and scales of P.V are read first: their LDS latency overlaps the QK^T matrix work
-  const int kbp = kb ^ 2;                              // block of the partner lane (lane ^ 32)
-  const int ga = n16 >> 2, gb = 4 + (n16 >> 2);      // INT4 scale groups of dims A (8 n16 ..) and B (8 (n16+16) ..)
-  uint32_t wo[8], wp[8];
+  const int t0 = 8 * (n16 >> 2) + (n16 & 3);   // A row n16 of block 0; block 1 reads token t0 + 4 (key ^ 4)
+  // chunk g of token t0 at byte t0 * 128 + 16 (g ^ ckey(t0)); dword kb of the chunk
+  const uint32_t base = lds_off(st.k) + (uint32_t)(t0 * 128 + 16 * ckey(t0) + 4 * kb);
+  uint32_t addr[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int te = e < 4 ? e : 12 + e;
-    wo[e] = lds_code_dword(st.v, 4 * kb + te, n16 >> 2, n16 & 3);
-    wp[e] = lds_code_dword(st.v, 4 * kbp + te, 4 + (n16 >> 2), n16 & 3);
-  }
-  h2 so[4], sp[4];
-#pragma unroll
-  for (int pr = 0; pr < 4; ++pr) {
-    const int te = (2 * pr) < 4 ? 2 * pr : 12 + 2 * pr;
-    so[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[ga][4 * kb + te]));
-    sp[pr] = as_h2(*reinterpret_cast<const uint32_t*>(&st.sv[gb][4 * kbp + te]));
-  }
-  // QK^T per 16-token half, software-pipelined over the groups: the MFMA of group g + 1 is in flight while the
-  // result of group g is folded with its scales (the fold no longer waits on the matrix core)
-  float s[2][4];
+  for (int g = 0; g < 8; ++g) addr[g] = base ^ (16u * (uint32_t)g);
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
-    const int t = 16 * nt + n16;
     uint32_t w[8];
 #pragma unroll
-    for (int g = 0; g < 8; ++g) w[g] = lds_code_dword(st.k, t, g, kb);
+    for (int g = 0; g < 8; ++g) w[g] = *(const lds_u32*)(uintptr_t)(addr[g ^ (4 * nt)] + 512u * nt);
     uint4 ksr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ksr[r] = *reinterpret_cast<const uint4*>(&st.ks[16 * nt + 4 * kb + r][0]);
+    for (int r = 0; r < 4; ++r) ksr[r] = *reinterpret_cast<const uint4*>(&st.ks[8 * kb + 4 * nt + r][0]);
     // bias term -sum_g s_g(t) bias_g (scaled by 2^-bexp in the MFMA, restored here)
-    const h8 srow = as_h8(*reinterpret_cast<const u4v*>(&st.ks[t][0]));
+    const h8 srow = as_h8(*reinterpret_cast<const u4v*>(&st.ks[t0 + 4 * nt][0]));
     const f4 bsum = mfma(srow, kbias, f4{0.f, 0.f, 0.f, 0.f});
     f4 dp = mfma(int4_codes_raw(w[0], mlo, mhi, magic), qop[0], f4{0.f, 0.f, 0.f, 0.f});
     f4 sc;
@@ -367,18 +352,23 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
       }
       dp = dn;
     }
-    if (n == 32) {   // full tile: no mask
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[nt][r] = sc[r] * cscale;
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[nt][r] = (16 * nt + 4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
-    }
+    for (int r = 0; r < 4; ++r) s[4 * nt + r] = sc[r] * cscale;
   }
-  if (nv.st != nullptr) cold_issue_v(*nv.C, *nv.st, nv.row0, nv.n);
-  // online softmax over the tile
-  float mloc = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+}
+
+// Scores of tokens >= n (a partial last tile) to -inf.
+KVT_DEV void cold_mask(float s[8], int n) {
+  const int kb = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = (8 * kb + e) < n ? s[e] : -INFINITY;
+}
+
+// Online softmax over a tile's scores.  Rescales acc and l_run when the running max grows; returns P of the lane's 8
+// tokens as fp16 with tokens 2, 3, 6, 7 divided by 16 (the A operand layout of cold_pv).
+KVT_DEV u4v cold_softmax(const float s[8], f4 acc[16], float& m_run, float& l_run) {
+  const int kb = (threadIdx.x & 63) >> 4;
+  float mloc = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
   mloc = max_xor16_32(mloc);
   const float m_new = fmaxf(m_run, mloc);
   if (__any(m_new > m_run)) {
@@ -388,56 +378,58 @@ KVT_DEV void cold_compute(const ColdStage& st, int n, const h8 qop[8], h8 kbias,
 #pragma unroll
     for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, (4 * kb + i) & 7, 64);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int a = 0; a < 16; ++a)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] *= arow[i];
+      for (int i = 0; i < 4; ++i) acc[a][i] *= arow[i];
   }
   m_run = m_new;
-  float psum = 0.f;
+  float p[8], psum = 0.f;
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      s[nt][r] = __builtin_amdgcn_exp2f(s[nt][r] - m_new);
-      psum += s[nt][r];
-    }
-  l_run += psum;
-  // P.V (block-diagonal, see the file header)
-  const bool lowrow = n16 < 8;
-  const h8 pown = {(_Float16)s[0][0], (_Float16)s[0][1], (_Float16)s[0][2], (_Float16)s[0][3],
-                   (_Float16)s[1][0], (_Float16)s[1][1], (_Float16)s[1][2], (_Float16)s[1][3]};
-  const u4v po = as_u4(pown);
-  u4v pp;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pp[i] = xor32_u32(po[i]);
-  const u4v zero = {0u, 0u, 0u, 0u};
-  const h8 ax = as_h8(lowrow ? po : zero);
-  const h8 ay = as_h8(lowrow ? zero : pp);
-  const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-  const h2 sc16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const h2 off2 = {(_Float16)-72.0f, (_Float16)-72.0f};
-#pragma unroll
-  for (int byte = 0; byte < 4; ++byte) {
-    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + byte) << 16) | (uint32_t)byte;
-    h8 olo, ohi, plo, phi;
-#pragma unroll
-    for (int pr = 0; pr < 4; ++pr) {
-      const uint32_t xo = __builtin_amdgcn_perm(wo[2 * pr + 1], wo[2 * pr], sel);  // [b(t0), 0, b(t1), 0]
-      const uint32_t xp = __builtin_amdgcn_perm(wp[2 * pr + 1], wp[2 * pr], sel);
-      const h2 lo_o = (as_h2(and_or(xo, mlo, magic)) + off) * so[pr];
-      const h2 hi_o = (as_h2(and_or(xo, mhi, magic)) * sc16 + off2) * so[pr];
-      const h2 lo_p = (as_h2(and_or(xp, mlo, magic)) + off) * sp[pr];
-      const h2 hi_p = (as_h2(and_or(xp, mhi, magic)) * sc16 + off2) * sp[pr];
-      olo[2 * pr] = lo_o.x; olo[2 * pr + 1] = lo_o.y;
-      ohi[2 * pr] = hi_o.x; ohi[2 * pr + 1] = hi_o.y;
-      plo[2 * pr] = lo_p.x; plo[2 * pr + 1] = lo_p.y;
-      phi[2 * pr] = hi_p.x; phi[2 * pr + 1] = hi_p.y;
-    }
-    acc[2 * byte] = mfma(ax, olo, acc[2 * byte]);            // alternate accumulators: no back-to-back chain
-    acc[2 * byte + 1] = mfma(ax, ohi, acc[2 * byte + 1]);
-    acc[2 * byte] = mfma(ay, plo, acc[2 * byte]);
-    acc[2 * byte + 1] = mfma(ay, phi, acc[2 * byte + 1]);
+  for (int e = 0; e < 8; ++e) {
+    p[e] = __builtin_amdgcn_exp2f(s[e] - m_new);
+    psum += p[e];
   }
+  l_run += psum;
+  const h2 sc16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 p01 = {(_Float16)p[0], (_Float16)p[1]}, p23 = h2{(_Float16)p[2], (_Float16)p[3]} * sc16;
+  const h2 p45 = {(_Float16)p[4], (_Float16)p[5]}, p67 = h2{(_Float16)p[6], (_Float16)p[7]} * sc16;
+  return u4v{as_u32(p01), as_u32(p23), as_u32(p45), as_u32(p67)};
+}
+
+// P.V of one staged tile.  Per scale group g (32 channels) and half hf (16 channels 32 g + 16 hf + j):
+//   acc[2 g + hf] += A_g * B_{g,hf} + A_g * C,  A_g = P16 * s_v(t, g)  (8 heads in rows 0-7, again in 8-15),
+// where B_{g,hf} holds the raw magic values of the codes (1024 + n for tokens 0, 1, 4, 5 of the k block, 1024 + 16 n
+// for tokens 2, 3, 6, 7, whose P16 entries carry the 1/16) and C = -(1032 | 1152) removes the constant excess: the
+// products are exact in fp32 and the V scale never multiplies a code.  B comes from ds_read_b64_tr_b4, a 16 x 16
+// nibble transpose per 16 lanes: source lane k supplies 8 bytes (16 channels) of token 8 kb + pi(k & 7), half k >> 3,
+// and receives channel 32 g + 16 (word) + (k) of the 8 tokens, in the nibble order that int4_codes_raw turns into
+// natural token order (pi = 0, 2, 4, 6, 1, 3, 5, 7).
+KVT_DEV void cold_pv(const ColdStage& st, u4v p16, f4 acc[16]) {
+  const int lane = threadIdx.x & 63;
+  const int k = lane & 15, kb = lane >> 4;
+  const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  const int tv = 8 * kb + 2 * (k & 3) + ((k >> 2) & 1);
+  const uint32_t vbase = lds_off(st.v) + (uint32_t)(tv * 128 + 16 * ckey(tv) + 8 * (k >> 3));
+  const h8 bc = {(_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1152.0f, (_Float16)-1152.0f,
+                 (_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1152.0f, (_Float16)-1152.0f};
+  const h8 pa = as_h8(p16);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const v2i raw = __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_v2i*)(uintptr_t)(vbase ^ (16u * (uint32_t)g)));
+    const h8 sg = as_h8(*reinterpret_cast<const u4v*>(&st.sv[g][8 * kb]));
+    const h8 a = pa * sg;
+    acc[2 * g] = mfma(a, int4_codes_raw((uint32_t)raw.x, mlo, mhi, magic), acc[2 * g]);
+    acc[2 * g + 1] = mfma(a, int4_codes_raw((uint32_t)raw.y, mlo, mhi, magic), acc[2 * g + 1]);
+    acc[2 * g] = mfma(a, bc, acc[2 * g]);
+    acc[2 * g + 1] = mfma(a, bc, acc[2 * g + 1]);
+  }
+}
+
+// s_waitcnt lgkmcnt(0): every LDS read of this wavefront has returned.
+KVT_DEV void wait_lgkm0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
 }
 
 // Tiles of one window of a cold range: tile i covers positions c0 + 32 i .. (at most c1), all in one page.
@@ -452,32 +444,44 @@ struct ColdTiles {
   KVT_DEV int n(int i) const { return (int)min((int64_t)32, c1 - (c0 + 32 * (int64_t)i)); }
 };
 
-// Tile i of a window, staged in W.cold[S]; tile i + 1 (if any) is issued into the other stage first.
+struct ColdMath {
+  const h8* qop;
+  h8 kbias;
+  int bexp;
+  float cscale;
+};
+
+// One step of the software pipeline: P.V of tile i (stage S, P in p16) and QK^T + softmax of tile i + 1 (stage S ^ 1).
+// In flight on entry, oldest first: K/scales of tile i + 1 (6 copies), V of tile i + 1 (4).  The step issues tile
+// i + 2's K/scales into stage S (whose K and scale rows tile i no longer needs) before the math and its V after P.V.
 template <int S>
-KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdTiles& T, int i, int ntiles, const h8 qop[8],
-                       h8 kbias, int bexp, float cscale, f4 acc[8], float& m_run, float& l_run) {
-  // (the loop issues no vector-memory instruction besides the tile copies: the vmcnt counts below are exact)
-  // in flight here, oldest first: K/scales of tile i (6), V of tile i (4), then K/scales of tile i + 1 (6)
-  NextV nv{&C, nullptr, 0u, 0};
-  if (i + 1 < ntiles) {
-    nv.st = &W.cold[S ^ 1];
-    nv.row0 = T.row0(i + 1);
-    nv.n = T.n(i + 1);
-    cold_issue_k(C, W.cold[S ^ 1], nv.row0, nv.n);
-    wait_vmcnt<6>();                    // tile i's copies have landed
+KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdTiles& T, int i, int ntiles, const ColdMath& M,
+                       f4 acc[16], float& m_run, float& l_run, u4v& p16) {
+  const bool more = i + 2 < ntiles;
+  uint32_t row2 = 0;
+  if (more) {
+    row2 = T.row0(i + 2);
+    cold_issue_k(C, W.cold[S], row2, T.n(i + 2));
+    wait_vmcnt<10>();                     // K/scales of tile i + 1 have landed (and V of tile i before them)
   } else {
-    wait_vmcnt<0>();
+    wait_vmcnt<4>();
   }
-  cold_scatter_vs(W.cold[S]);
+  cold_scatter_vs(W.cold[S ^ 1]);
   wave_sync();
-  cold_compute(W.cold[S], T.n(i), qop, kbias, bexp, cscale, acc, m_run, l_run, nv);   // issues tile i + 1's V
-  wave_sync();
+  float s[8];
+  cold_pv(W.cold[S], p16, acc);           // one basic block: the two tiles' matrix and VALU work interleave
+  cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, s);
+  wait_lgkm0();                           // tile i's V reads are done before its stage takes new V copies
+  if (more) cold_issue_v(C, W.cold[S], row2);
+  const int n1 = T.n(i + 1);
+  if (n1 < 32) cold_mask(s, n1);
+  p16 = cold_softmax(s, acc, m_run, l_run);
 }
 
 // The cold range [c0, c1) of one wavefront: c0 is 32-aligned, every tile lies in one page.  Processed in windows of
-// at most 64 pages (the page ids of a window are held one per lane).
+// at most 64 pages (the page ids of a window are held one per lane), each through the two-stage pipeline.
 KVT_DEV void cold_segment(const PosArgs& A, const ColdCtx& C, WaveArea& W, int b, int64_t c0, int64_t c1,
-                          const h8 qop[8], h8 kbias, int bexp, float cscale, f4 acc[8], float& m_run, float& l_run) {
+                          const ColdMath& M, f4 acc[16], float& m_run, float& l_run) {
   const int lane = threadIdx.x & 63;
   for (int64_t s0 = c0; s0 < c1;) {
     const int64_t s1 = min(c1, ((s0 >> 6) + 64) << 6);
@@ -489,12 +493,38 @@ KVT_DEV void cold_segment(const PosArgs& A, const ColdCtx& C, WaveArea& W, int b
     T.pages = lane < npg ? A.page_table[b * A.pt_stride + T.pg0 + lane] : 0;
     const int ntiles = (int)((s1 - s0 + 31) >> 5);
     wave_sync();
-    cold_issue_k(C, W.cold[0], T.row0(0), T.n(0));
-    cold_issue_v(C, W.cold[0], T.row0(0), T.n(0));
-    for (int i = 0; i < ntiles; i += 2) {
-      cold_step<0>(C, W, T, i, ntiles, qop, kbias, bexp, cscale, acc, m_run, l_run);
-      if (i + 1 < ntiles) cold_step<1>(C, W, T, i + 1, ntiles, qop, kbias, bexp, cscale, acc, m_run, l_run);
+    // prologue: tiles 0 and 1 in flight, QK^T + softmax of tile 0
+    const uint32_t r0 = T.row0(0);
+    cold_issue_k(C, W.cold[0], r0, T.n(0));
+    cold_issue_v(C, W.cold[0], r0);
+    if (ntiles > 1) {
+      const uint32_t r1 = T.row0(1);
+      cold_issue_k(C, W.cold[1], r1, T.n(1));
+      cold_issue_v(C, W.cold[1], r1);
+      wait_vmcnt<14>();
+    } else {
+      wait_vmcnt<4>();
     }
+    cold_scatter_vs(W.cold[0]);
+    wave_sync();
+    u4v p16;
+    {
+      float s[8];
+      cold_qk(W.cold[0], M.qop, M.kbias, M.bexp, M.cscale, s);
+      const int n0 = T.n(0);
+      if (n0 < 32) cold_mask(s, n0);
+      p16 = cold_softmax(s, acc, m_run, l_run);
+    }
+    for (int i = 0; i + 1 < ntiles; i += 2) {
+      cold_step<0>(C, W, T, i, ntiles, M, acc, m_run, l_run, p16);
+      if (i + 2 < ntiles) cold_step<1>(C, W, T, i + 1, ntiles, M, acc, m_run, l_run, p16);
+    }
+    // epilogue: P.V of the last tile
+    wait_vmcnt<0>();
+    wave_sync();
+    cold_pv(W.cold[(ntiles - 1) & 1], p16, acc);
+    wait_lgkm0();
+    wave_sync();
     s0 = s1;
   }
 }
@@ -543,7 +573,7 @@ KVT_DEV uint32_t hot_scale(const uint16_t (*sc)[8], int t, int g, int sh) { retu
 
 template <int G8>
 KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n, const h8 qop[8], float cscale,
-                         f4 acc[8], float& m_run, float& l_run) {
+                         f4 acc[16], float& m_run, float& l_run) {
   constexpr int NG8 = kD / G8;
   constexpr int STEPS = G8 / 32;
   const int lane = threadIdx.x & 63;
@@ -594,9 +624,9 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
 #pragma unroll
     for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, (4 * kb + i) & 7, 64);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int a = 0; a < 16; ++a)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[j][i] *= arow[i];
+      for (int i = 0; i < 4; ++i) acc[a][i] *= arow[i];
   }
   m_run = m_new;
   float psum = 0.f;
@@ -606,65 +636,45 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
     psum += s[r];
   }
   l_run += psum;
-  // ---- P.V on 16x16x16: k = token 4 kb + i of the lane block (own) or of block kb ^ 2 (partner, lane ^ 32)
-  const int kbp = kb ^ 2;
-  const bool lowrow = n16 < 8;
+  // ---- P.V on 16x16x16 (k = tokens 4 kb .. + 3 of the lane's block), same accumulator layout as the paged tiles:
+  // acc[a] += (P * s_v(t, g(a))) * V(t, 16 a + j).  B from ds_read_b64_tr_b8: source lane 2 k8 + p supplies 8 bytes
+  // (channels 16 a + 8 p ..) of token 4 kb + (k8 & 3), block a = a0 (k8 < 4) or a0 + 4; lane j then holds channel
+  // 16 a0 + j of the 4 tokens in its low dword and channel 16 (a0 + 4) + j in its high dword (8 distinct slots per
+  // 16 lanes: conflict-free).  Codes convert exactly (b + 128 as the low byte of 1024 + u, minus 1152).
   const h4 pown = {(_Float16)s[0], (_Float16)s[1], (_Float16)s[2], (_Float16)s[3]};
-  const uint2 po = __builtin_bit_cast(uint2, pown);
-  uint2 pp;
-  pp.x = xor32_u32(po.x);
-  pp.y = xor32_u32(po.y);
-  const uint2 zero = {0u, 0u};
-  const h4 ax = __builtin_bit_cast(h4, lowrow ? po : zero);
-  const h4 ay = __builtin_bit_cast(h4, lowrow ? zero : pp);
-  // V codes: own tokens, dims 8 n16 .. + 7 (chunk n16 / 2); partner tokens, dims 8 (n16 + 16) .. + 7
-  uint2 wo[4], wp[4];
-  int sho[4], shp[4];
+  h4 pa[NG8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int to = 4 * kb + i, tp = 4 * kbp + i;
-    const int co = n16 >> 1, cp = 8 + (n16 >> 1);
-    wo[i] = *reinterpret_cast<const uint2*>(st.v + to * 256 + 16 * (co ^ to) + 8 * (n16 & 1));
-    wp[i] = *reinterpret_cast<const uint2*>(st.v + tp * 256 + 16 * (cp ^ tp) + 8 * (n16 & 1));
-    wo[i].x ^= 0x80808080u; wo[i].y ^= 0x80808080u;
-    wp[i].x ^= 0x80808080u; wp[i].y ^= 0x80808080u;
-    sho[i] = NG8 == 1 ? sh_of(to) : 0;
-    shp[i] = NG8 == 1 ? sh_of(tp) : 0;
-  }
-  const int ga = (8 * n16) / G8, gb = (8 * (n16 + 16)) / G8;
-  h2 so[2], sp[2];
+  for (int g = 0; g < NG8; ++g) {
+    h4 sg;
 #pragma unroll
-  for (int pr = 0; pr < 2; ++pr) {
-    so[pr] = as_h2(hot_scale(st.vs, 4 * kb + 2 * pr, ga, sho[2 * pr]) |
-                   (hot_scale(st.vs, 4 * kb + 2 * pr + 1, ga, sho[2 * pr + 1]) << 16));
-    sp[pr] = as_h2(hot_scale(st.vs, 4 * kbp + 2 * pr, gb, shp[2 * pr]) |
-                   (hot_scale(st.vs, 4 * kbp + 2 * pr + 1, gb, shp[2 * pr + 1]) << 16));
+    for (int e = 0; e < 4; ++e) {
+      const int t = 4 * kb + e;
+      sg[e] = __builtin_bit_cast(_Float16, (uint16_t)hot_scale(st.vs, t, g, NG8 == 1 ? sh_of(t) : 0));
+    }
+    pa[g] = pown * sg;
   }
-  const uint32_t magic = 0x64006400u;
+  const int k8 = n16 >> 1, pb = n16 & 1;
+  const int tv = 4 * kb + (k8 & 3);
+  const uint32_t vrow = lds_off(st.v) + (uint32_t)(tv * 256 + 8 * pb);
   const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t bsel = (uint32_t)(e & 3);
-    const uint32_t sel = 0x0C000C00u | ((4 + bsel) << 16) | bsel;
-    uint2 bo, bp;
-#pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
-      const uint32_t xo = __builtin_amdgcn_perm(e < 4 ? wo[2 * pr + 1].x : wo[2 * pr + 1].y,
-                                                e < 4 ? wo[2 * pr].x : wo[2 * pr].y, sel);
-      const uint32_t xp = __builtin_amdgcn_perm(e < 4 ? wp[2 * pr + 1].x : wp[2 * pr + 1].y,
-                                                e < 4 ? wp[2 * pr].x : wp[2 * pr].y, sel);
-      const uint32_t vo = as_u32((as_h2(xo | magic) + off) * so[pr]);
-      const uint32_t vp = as_u32((as_h2(xp | magic) + off) * sp[pr]);
-      if (pr == 0) { bo.x = vo; bp.x = vp; } else { bo.y = vo; bp.y = vp; }
-    }
-    acc[e] = mfma16(ax, __builtin_bit_cast(h4, bo), acc[e]);
-    acc[e] = mfma16(ay, __builtin_bit_cast(h4, bp), acc[e]);
+  for (int r = 0; r < 8; ++r) {
+    const int a0 = (r & 3) + 8 * (r >> 2);
+    const int a = k8 < 4 ? a0 : a0 + 4;
+    const v2i raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(uintptr_t)(vrow + 16u * (uint32_t)(a ^ tv)));
+    const uint32_t u0 = (uint32_t)raw.x ^ 0x80808080u, u1 = (uint32_t)raw.y ^ 0x80808080u;
+    const h2 l0 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + off;
+    const h2 h0 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + off;
+    const h2 l1 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + off;
+    const h2 h1 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + off;
+    acc[a0] = mfma16(pa[(16 * a0) / G8], h4{l0.x, l0.y, h0.x, h0.y}, acc[a0]);
+    acc[a0 + 4] = mfma16(pa[(16 * (a0 + 4)) / G8], h4{l1.x, l1.y, h1.x, h1.y}, acc[a0 + 4]);
   }
 }
 
 template <int G8, int S>
 KVT_DEV void hot_step(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, int i, int ntiles, const h8 qop[8],
-                      float cscale, f4 acc[8], float& m_run, float& l_run) {
+                      float cscale, f4 acc[16], float& m_run, float& l_run) {
   const int64_t p = p0 + 16 * (int64_t)i;
   if (i + 1 < ntiles) {
     hot_issue(C, W.hot[S ^ 1], p + 16, (int)min((int64_t)16, p1 - p - 16));
@@ -680,7 +690,7 @@ KVT_DEV void hot_step(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, int 
 // Ring positions [p0, p1) of one wavefront in 16-position tiles, double-buffered like the paged range.
 template <int G8>
 KVT_DEV void hot_segment(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, const h8 qop[8], float cscale,
-                         f4 acc[8], float& m_run, float& l_run) {
+                         f4 acc[16], float& m_run, float& l_run) {
   const int ntiles = (int)((p1 - p0 + 15) >> 4);
   wave_sync();
   hot_issue(C, W.hot[0], p0, (int)min((int64_t)16, p1 - p0));
@@ -695,7 +705,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
 decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32_t* seq_lens, int H, int gs,
                    int n_splits, const int32_t* split_map, float scale, float* part_o, float* part_ml,
                    uint32_t pool_rows) {
-  __shared__ Lds lds;
+  __shared__ __align__(128) Lds lds;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar addressing of the page table
   const int n16 = lane & 15, kb = lane >> 4;
@@ -734,10 +744,11 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   const int hq = n16 & 7;
   const bool qvalid = hq < gs;
   const uint16_t* qrow = q + b * q_stride_b + (int64_t)(h * gs + (qvalid ? hq : 0)) * kD;
+  const bool qvec16 = (((uintptr_t)q | (uintptr_t)(q_stride_b * 2)) & 15) == 0;   // uniform
 
-  f4 acc[8];
+  f4 acc[16];   // acc[a]: channels 16 a + j (lane j + 16 kb), q heads 4 kb + i in rows (kb 2, 3 repeat kb 0, 1)
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int a = 0; a < 16; ++a) acc[a] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   h8 qop[8];
 
@@ -746,17 +757,18 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   if (w0 < ce) {
     h8 kbias;
     int bexp;
-    load_q_int4(qrow, qvalid, kb, qop, kbias, bexp);
+    load_q_int4(qrow, qvec16, qvalid, kb, qop, kbias, bexp);
     ColdCtx C{buffer_rsrc(A.k4, pool_rows * (uint32_t)H * 128u), buffer_rsrc(A.v4, pool_rows * (uint32_t)H * 128u),
               buffer_rsrc(A.ks4, pool_rows * (uint32_t)H * 16u), buffer_rsrc(A.vs4, pool_rows * (uint32_t)H * 16u),
               (uint32_t)H * 128u, (uint32_t)h * 128u, H, h, {0u, 0u, 0u, 0u}, 0u};
     cold_lane_offsets(C);
-    cold_segment(A, C, lds.w[wave], b, w0, ce, qop, kbias, bexp, cscale, acc, m_run, l_run);
+    const ColdMath M{qop, kbias, bexp, cscale};
+    cold_segment(A, C, lds.w[wave], b, w0, ce, M, acc, m_run, l_run);
   }
   // hot segment [max(w0, hs), w1) from the INT8 ring
   const int64_t hp = max(w0, hs);
   if (hp < w1) {
-    load_q_ring(qrow, qvalid, kb, qop);
+    load_q_ring(qrow, qvec16, qvalid, kb, qop);
     constexpr uint32_t NG8 = kD / G8;
     const uint32_t ring_rows = (uint32_t)R;
     HotCtx C{buffer_rsrc(A.rk + rbase * H * kD, ring_rows * (uint32_t)H * kD),
@@ -775,7 +787,7 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
     lds.merge.l[wave][n16] = l_run;
   }
   __syncthreads();
-  // accumulator row 4 kb + i is q head (4 kb + i) % 8 = 4 (kb & 1) + i, dims 8 (n16 + 16 (kb >> 1)) + j
+  // accumulator row 4 kb + i is q head (4 kb + i) % 8 = 4 (kb & 1) + i; lanes kb < 2 write heads 0-7
   f4 wrow;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -787,10 +799,12 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
     wrow[i] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
   }
   float* ow = lds.merge.o[wave];
+  if (kb < 2) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int dim = 8 * (n16 + 16 * (kb >> 1)) + j;
-    *reinterpret_cast<f4*>(&ow[dim * 8 + (dim >> 3) * 4 + 4 * (kb & 1)]) = acc[j] * wrow;
+    for (int a = 0; a < 16; ++a) {
+      const int dim = 16 * a + n16;
+      *reinterpret_cast<f4*>(&ow[dim * 8 + (dim >> 3) * 4 + 4 * kb]) = acc[a] * wrow;
+    }
   }
   __syncthreads();
   {

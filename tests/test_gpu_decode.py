@@ -96,9 +96,12 @@ def test_decode_mfma_page_windows(kvt_pkg):
 
 
 def test_decode_mfma_closed_forms(kvt_pkg):
-    """Hot: a single ring position gives out == fp16(code * scale) of its V row (P = 1).  Cold: 64 identical rows in
-    a shared INT4 page (positions below ring_start) give uniform attention, out == the same fp16 row (the sum of 64
-    equal fp16 values and the division by 64 are exact in fp32)."""
+    """Hot: a single ring position gives out == code * scale of its V row in fp32 (P = 1; the scale enters the matrix
+    product through P and the fp16 x fp16 products are exact).  Cold: 64 identical rows in a shared INT4 page
+    (positions below ring_start) give uniform attention, out == code * scale of that row; the V row is k / 8 with
+    integers k in -7..7 and +-7 in every group of 32 channels, so every scale is exactly 1/8 and every partial sum of
+    the kernel (raw 1024 + n / 1024 + 16 n values times 1/8 or 1/128, the constant excess removed per tile) is a
+    small multiple of 1/8: exact in fp32."""
     from kvtier import sparse_attn as sa
     from kvtier.kvt import PosTieredCache, kvt_decode_attn
     gen = torch.Generator().manual_seed(4)
@@ -112,18 +115,22 @@ def test_decode_mfma_closed_forms(kvt_pkg):
     dc.append(0, plan, xk.to(dev), xv.to(dev))
     dc.commit(plan)
     out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma").cpu()
-    vrow = (dc.rv[0][0].cpu().float() * dc.rvs[0][0].cpu().float().repeat_interleave(64, -1)).half().float()
+    vrow = dc.rv[0][0].cpu().float() * dc.rvs[0][0].cpu().float().repeat_interleave(64, -1)
     for hq in range(HQ):
         assert torch.equal(out[0, hq], vrow[hq // 8]), ("hot", hq)
     # cold: page 1 holds 64 copies of the row, written by the INT4 writer; the sequence starts at position 64
     dc = PosTieredCache(1, H, D, n_pages=2, ring_total=64, max_seqs=1, max_pages=2, device=dev)
     ones = torch.ones(H, D, dtype=torch.float16, device=dev)
-    sa.quant_store_kv_int4(xk.expand(64, H, D).contiguous().to(dev), xv.expand(64, H, D).contiguous().to(dev),
+    kv = torch.randint(-7, 8, (H, D), generator=gen)
+    kv[:, ::32] = 7
+    xv_c = (kv.float() / 8).to(torch.bfloat16).unsqueeze(0)
+    sa.quant_store_kv_int4(xk.expand(64, H, D).contiguous().to(dev), xv_c.expand(64, H, D).contiguous().to(dev),
                            torch.arange(64, 128, device=dev), dc.k4[0], dc.v4[0], dc.ks4[0], dc.vs4[0], ones, ones)
     dc.add_seq(64, ring_start=64, shared_pages=[1])
     out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma").cpu()
     codes = ref.unpack4(dc.v4[0][64].cpu()).float()
-    vrow = (codes * dc.vs4[0][64].cpu().float().repeat_interleave(32, -1)).half().float()
+    vrow = codes * dc.vs4[0][64].cpu().float().repeat_interleave(32, -1)
+    assert torch.equal(dc.vs4[0][64].cpu().float(), torch.full((H, 8), 0.125)) and torch.equal(vrow, kv.float() / 8)
     for hq in range(HQ):
         assert torch.equal(out[0, hq], vrow[hq // 8]), ("cold", hq)
 
