@@ -120,20 +120,24 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
 
 /* Split-K GQA decode attention on the matrix cores (v_mfma_f32_16x16x32_f16) over position rings + page tables
  * (the mode-0 layout of kvt_decode_ref): QK^T with exact fp16 integer codes and the per-group scales folded in
- * fp32, P.V with fp16 P and fp16 code*scale values, fp32 accumulation.  Each split holds 4 wavefront ranges of
- * equal cost.  split_map NULL: every (sequence, KV head) gets n_splits splits; otherwise split_map (int32
+ * fp32; P.V with the raw INT4 codes as exact fp16 values and the V scale folded into fp16 P; fp32 accumulation.
+ * Each split is one block of 8 wavefronts (one block per CU) over a position range of equal cost; its 32-position
+ * tiles go to the wavefronts either first come (flags & KVT_DECODE_DYNAMIC: the wavefronts finish together; the
+ * fp32 summation order, and so the last bits of the result, then depend on timing) or in a fixed order
+ * (bit-reproducible).  split_map NULL: every (sequence, KV head) gets n_splits splits; otherwise split_map (int32
  * [n_map][3] = {sequence, split index, splits of that sequence}) lists the splits (per-sequence counts for ragged
  * batches) and n_splits is the partial slot stride per (sequence, head).  Partials in the layout of kvt_decode_ref;
- * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 8, D = 256; pool_rows = rows of the INT4
- * pool (byte offsets are 32-bit: pool_rows * H * D / 2 < 2^31, else KVT_ERANGE).  No reference counterpart: it
- * replaces the compact gather + FA2 pair (flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense
- * decode. */
+ * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 8, D = 256, q and q_stride_b 16-byte
+ * aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 <
+ * 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the compact gather + FA2 pair (flat patch
+ * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode. */
+#define KVT_DECODE_DYNAMIC 1
 int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    void* stream);
+                    int flags, void* stream);
 
 /* Merge the split-K partials: out[b, hq, :] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c (fp32 and/or bf16
  * output, either may be NULL; batch stride out_stride_b elements).  chunk > 0: split c covers positions

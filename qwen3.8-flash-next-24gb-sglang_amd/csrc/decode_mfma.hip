@@ -1,41 +1,42 @@
 // Split-K GQA decode attention over the position-indexed tiered cache on gfx950 matrix cores.
 //
-// Work split: every (sequence, KV head) has n_splits blocks of 4 wavefronts.  The position range [0, L) is cut into
-// 4 * n_splits consecutive wavefront ranges of equal cost, where a ring position (INT8, 2 x 256 code bytes) costs
-// kHotCost4 / 4 of a paged position (INT4, 2 x 128 code bytes; the ring tile takes about the same time per position
-// as the paged tile): the waves holding the ring finish with the others.
-// Range boundaries inside the paged part are multiples of 32.  GQA groups of up to 8 q heads per KV head.
-//   Cold positions (< hot_start, INT4-G32 pages through the page table) stream in 32-token tiles: a 32-aligned tile
-//   lies in one 64-token page, i.e. 32 consecutive pool rows.  Each wavefront double-buffers its tiles in LDS with
-//   direct-to-LDS copies (buffer_load_dwordx4 ... lds, 16 B per lane) issued one tile ahead, so HBM traffic of tile
-//   i+1 overlaps the matrix work of tile i.  16-byte chunks are XOR-swizzled with the token index at the source
-//   address, which spreads the per-lane LDS reads over the banks.
-//   Hot positions (the INT8 ring row, position mod R) take the same pipeline in 16-token tiles (K 4 KB + V 4 KB),
-//   with P.V on v_mfma_f32_16x16x16_f16, whose A operand is again the score layout.
+// Work split: every (sequence, KV head) has n_splits blocks of 8 wavefronts, one block per CU (the block takes all
+// of the CU's LDS).  The position range [0, L) is cut into n_splits block ranges of equal cost (a ring position costs
+// kHotCost4 / 4 of a paged one; boundaries in the paged part are multiples of 32).  Inside a block, 32-position paged
+// tiles and 16-position ring tiles go to the wavefronts one at a time, from a counter in LDS (first come: the
+// wavefronts finish together although the oldest get more issue slots) or in a fixed order (bit-reproducible).
+// GQA groups of up to 8 q heads per KV head; the block copies the group's Q rows to LDS once.
+//   Paged positions (< hot_start, INT4-G32 pages through the page table): a 32-aligned tile lies in one 64-position
+//   page, i.e. 32 consecutive pool rows.  Each wavefront double-buffers its tiles in LDS with direct-to-LDS copies
+//   (buffer_load_dwordx4 ... lds, 16 B per lane): the next-but-one tile's K codes and scale rows are issued before a
+//   step's math, its V codes after the step's P.V reads.  16-byte chunks are XOR-swizzled at the source address
+//   (slot = chunk ^ ckey(token)), so the LDS reads below spread over the banks.
+//   Software pipeline: one step is P.V of tile i and QK^T of tile i + 1 in one basic block, so the matrix and VALU
+//   work of the two tiles interleave; then the online softmax of tile i + 1.
+//   Ring positions (the INT8 ring row, position mod R) take 16-position tiles (K 4 KB + V 4 KB), double-buffered.
 //
-// QK^T (cold) on v_mfma_f32_16x16x32_f16, one instruction per 16 tokens x 32 channels (= one INT4 scale group):
+// QK^T (paged) on v_mfma_f32_16x16x32_f16, one instruction per 16 tokens x 32 channels (= one INT4 scale group):
 //   A = raw magic-number values of the codes (0x6400 | nibble = 1024 + n for even channels, 0x6400 | nibble << 4 =
-//   1024 + 16 n for odd channels: one v_and_or_b32 per two values, no arithmetic), channel order [0,4,1,5,2,6,3,7]
-//   of each 8; B = Q in the same order with odd channels divided by 16, the group's q heads in columns 0-7 and again
-//   in 8-15.  Each product then carries a constant excess: (1024 + n) q = (n - 8) q + 1032 q and
-//   (1024 + 16 n) q / 16 = (n - 8) q + 1152 (q / 16).  The per-(group, head) excess bias_g is token independent; the
-//   score of token t is sum_g s_g(t) D_g(t) - sum_g s_g(t) bias_g.  The first sum folds the fp32 group results with
-//   the fp16 scales (v_fma_mix); the second is one more MFMA per 16 tokens: A = the token's 8 scales (k 0-7 and
-//   again 8-15), B = -bias as two fp16 parts (k 0-7 the leading part, k 8-15 the remainder, k >= 16 zero), scaled
-//   by a per-head power of two that keeps the parts in the fp16 range; the products are exact in fp32.
-// Softmax: scores stay in the D layout (lane = q head, 4 tokens of each 16-token tile), which is the A operand
-//   layout of P.V, so P needs no transpose.  exp2 with log2(e) folded into the score scale; the running max is
-//   rescaled only when it grows (wave-uniform test).
-// P.V, block-diagonal: a 16 x 16 accumulator tile holds 8 heads x 16 dims in rows 0-7 and the same 8 heads x 16
-//   other dims in rows 8-15.  Because columns 8-15 of Q duplicate 0-7, lane (row m >= 8) holds P of head m - 8;
-//   A_X = (m < 8 ? own P : 0) with B = V(own tokens, dims A) and A_Y = (m >= 8 ? P of lane ^ 32 : 0) with
-//   B = V(tokens of lane ^ 32, dims B) accumulate into the same tile: 32 accumulator registers for 256 dims.
-//   V is dequantized to fp16 (exact code conversion, then one packed multiply by the per-(token, group) scale pair).
-// The four wavefronts merge (max, sum, o) in LDS; one fp32 partial per (split, q head) goes to kvt_decode_combine.
+//   1024 + 16 n for odd channels: one v_and_or_b32 per two values), channel order [0,4,1,5,2,6,3,7] of each 8; B = Q
+//   in the same order with odd channels divided by 16, the group's q heads in columns 0-7 and again in 8-15.  Each
+//   product carries a constant excess: (1024 + n) q = (n - 8) q + 1032 q and (1024 + 16 n) q / 16 = (n - 8) q +
+//   1152 (q / 16); the per-(group, head) excess bias_g is token independent, so the score of token t is
+//   sum_g s_g(t) D_g(t) - sum_g s_g(t) bias_g.  The first sum folds the fp32 group results with the fp16 scales
+//   (v_fma_mix); the second is one more MFMA per 16 tokens (A = the token's 8 scales, B = -bias as two fp16 parts
+//   scaled by a per-head power of two; the products are exact in fp32).  A rows are ordered so that the D layout
+//   leaves each lane the scores of 8 consecutive tokens: the A operand of P.V, no transpose.
+// P.V (paged) per scale group g and half: acc[2 g + hf] += A_g * B + A_g * C, A_g = P * s_v(t, g) (fp16; tokens
+//   whose codes arrive as 16 n carry P / 16), B = the raw magic values of the V codes, C = -(1032 | 1152) per k.
+//   The V scale never multiplies a code and the constant excess is removed per tile (exact fp32 products).  B comes
+//   from ds_read_b64_tr_b4, a 16 x 16 nibble transpose per 16 lanes, which turns token-major code rows into the
+//   channel-major operand layout in one LDS instruction.
+// Ring P.V: v_mfma_f32_16x16x16_f16 with B from ds_read_b64_tr_b8 (exact fp16 codes) and the ring scale folded
+//   into P the same way.  Accumulators: acc[a] = 16 channels x 8 heads (rows 8-15 repeat 0-7).
+// The block's wavefronts merge (max, sum, o) in LDS; one fp32 partial per (split, q head) goes to kvt_decode_combine.
 //
-// Numerics versus the oracle (bf16(code * scale) rows, fp32 softmax): K codes enter exactly, scales in fp32; V as
-// fp16(code * scale) (finer than the oracle's bf16 rounding); P as fp16; fp32 accumulation.  V entries beyond the
-// fp16 range (|v| > 65504) are not representable on this path (the reference-precision kernel handles them).
+// Numerics versus the oracle (bf16(code * scale) rows, fp32 softmax): codes enter exactly, K scales in fp32, V scales
+// through fp16 P * s (P <= 1, so P * s stays in the fp16 range of the scale itself); fp32 accumulation.  A single
+// position returns exactly code * scale.
 
 #include "kvt_common.h"
 
@@ -50,9 +51,10 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;          // wavefronts per block (one block per CU: all of the CU's LDS)
 constexpr int kD = 256;
-constexpr int kHotCost4 = 4;    // cost of a ring position; a paged position costs 4 (measured: equal time)
+constexpr int kHotCost4 = 5;       // cost of a ring position when blocks split a sequence; a paged position costs 4
+constexpr int kBlockPages = 900;   // page ids of a block's paged range staged in LDS per round
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct PosArgs {
@@ -78,11 +80,23 @@ KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
 KVT_DEV h8 as_h8(u4v u) { return __builtin_bit_cast(h8, u); }
 KVT_DEV u4v as_u4(h8 h) { return __builtin_bit_cast(u4v, h); }
 
-// (a & m) | o in one VOP3 instruction (the compiler otherwise splits it in two around the literal constants).
-KVT_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(o));
-  return r;
+// (a & m) | o: one v_and_or_b32 when m and o are VGPR values the compiler cannot fold into literals (see
+// NibbleMasks).  Plain code, not inline assembly, so that the compiler's hazard checks see every write (an MFMA may
+// still be reading its source registers when the next instruction overwrites them).
+KVT_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
+
+// A value in a VGPR that the compiler treats as unknown (no literal folding, no instruction emitted here).
+KVT_DEV uint32_t opaque_vgpr(uint32_t x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
+// Masks of the magic-number code conversion, held in VGPRs once per wavefront.
+struct NibbleMasks {
+  uint32_t lo, hi, magic;
+};
+KVT_DEV NibbleMasks nibble_masks() {
+  return NibbleMasks{opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
 }
 
 // 8 INT4 codes (one dword, channels c0..c7 = nibbles 0..7) -> raw magic values in the order
@@ -134,9 +148,21 @@ struct MergeArea {
   float o[kWaves][kMergePitch];
 };
 
-union Lds {
-  WaveArea w[kWaves];
-  MergeArea merge;
+// Block-wide data: the group's q heads (copied once; rows beyond the group read as zero) and the work handed out
+// inside the block (the next paged tile of the current round, the next ring tile, the round's page ids).
+struct BlockQueue {
+  uint16_t q[8][kD];
+  int32_t cold_next;
+  int32_t hot_next;
+  int32_t pages[kBlockPages];   // physical page of the round's page pg0 + i
+};
+
+struct Lds {
+  union {
+    WaveArea w[kWaves];
+    MergeArea merge;
+  };
+  BlockQueue q;
 };
 
 // Raw buffer resource over [p, p + bytes): loads beyond the range return zero instead of faulting.
@@ -151,11 +177,12 @@ KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
 }
 
 // 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
-// statement, so the compiler sets it.  Inline assembly rather than the builtin so that the compiler does not treat
+// statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.  Inline assembly rather than the builtin so that the compiler does not treat
 // every later LDS read as dependent on the copy: completion is tracked explicitly with wait_vmcnt by the caller.
 KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base) : "memory");
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
+               : "memory");
 }
 
 // s_waitcnt vmcnt(<= n) leaving the other counters alone (gfx9 encoding).
@@ -315,10 +342,11 @@ KVT_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
 // QK^T of one staged tile.  Block nt (0, 1) of 16 A rows: row i is token 8 (i >> 2) + 4 nt + (i & 3), so that the
 // D layout leaves lane (n16, kb) with the scores of q head n16 % 8 for tokens 8 kb + 4 nt + r in s[4 nt + r]: the
 // lane's 8 scores are tokens 8 kb .. 8 kb + 7 in natural order, the A operand of P.V.  Scores in log2 units.
-KVT_DEV void cold_qk(const ColdStage& st, const h8 qop[8], h8 kbias, int bexp, float cscale, float s[8]) {
+KVT_DEV void cold_qk(const ColdStage& st, const h8 qop[8], h8 kbias, int bexp, float cscale, NibbleMasks nm,
+                     float s[8]) {
   const int lane = threadIdx.x & 63;
   const int n16 = lane & 15, kb = lane >> 4;
-  const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  const uint32_t mlo = nm.lo, mhi = nm.hi, magic = nm.magic;
   const int t0 = 8 * (n16 >> 2) + (n16 & 3);   // A row n16 of block 0; block 1 reads token t0 + 4 (key ^ 4)
   // chunk g of token t0 at byte t0 * 128 + 16 (g ^ ckey(t0)); dword kb of the chunk
   const uint32_t base = lds_off(st.k) + (uint32_t)(t0 * 128 + 16 * ckey(t0) + 4 * kb);
@@ -404,10 +432,10 @@ KVT_DEV u4v cold_softmax(const float s[8], f4 acc[16], float& m_run, float& l_ru
 // nibble transpose per 16 lanes: source lane k supplies 8 bytes (16 channels) of token 8 kb + pi(k & 7), half k >> 3,
 // and receives channel 32 g + 16 (word) + (k) of the 8 tokens, in the nibble order that int4_codes_raw turns into
 // natural token order (pi = 0, 2, 4, 6, 1, 3, 5, 7).
-KVT_DEV void cold_pv(const ColdStage& st, u4v p16, f4 acc[16]) {
+KVT_DEV void cold_pv(const ColdStage& st, u4v p16, NibbleMasks nm, f4 acc[16]) {
   const int lane = threadIdx.x & 63;
   const int k = lane & 15, kb = lane >> 4;
-  const uint32_t mlo = 0x000F000Fu, mhi = 0x00F000F0u, magic = 0x64006400u;
+  const uint32_t mlo = nm.lo, mhi = nm.hi, magic = nm.magic;
   const int tv = 8 * kb + 2 * (k & 3) + ((k >> 2) & 1);
   const uint32_t vbase = lds_off(st.v) + (uint32_t)(tv * 128 + 16 * ckey(tv) + 8 * (k >> 3));
   const h8 bc = {(_Float16)-1032.0f, (_Float16)-1032.0f, (_Float16)-1152.0f, (_Float16)-1152.0f,
@@ -432,99 +460,154 @@ KVT_DEV void wait_lgkm0() {
   asm volatile("" ::: "memory");
 }
 
-// Tiles of one window of a cold range: tile i covers positions c0 + 32 i .. (at most c1), all in one page.
-struct ColdTiles {
-  int32_t pages;   // physical page of window page `lane` (lanes beyond the window hold 0)
+// The next tile of this wavefront: from the block's shared counter (dyn: the wavefronts that run ahead take more
+// tiles, so the block's wavefronts finish together; the floating-point summation order then depends on timing) or in
+// the fixed order w, w + kWaves, w + 2 kWaves, ... (bit-reproducible).
+KVT_DEV int take_tile(int32_t* next, bool dyn, int& taken) {
+  int t = 0;
+  if (dyn) {
+    if ((threadIdx.x & 63) == 0) t = atomicAdd(next, 1);
+  } else {
+    t = (int)(threadIdx.x >> 6) + kWaves * taken;
+  }
+  ++taken;
+  return __builtin_amdgcn_readfirstlane(t);
+}
+
+// One round of a block's paged range: positions [c0, c1) (c0 32-aligned) in 32-position tiles, handed out one at
+// a time from the block's counter; the round's page ids sit in LDS.
+struct ColdRound {
   int64_t c0, c1, pg0;
-  KVT_DEV uint32_t row0(int i) const {
-    const int64_t p = c0 + 32 * (int64_t)i;
-    const uint32_t page = (uint32_t)__builtin_amdgcn_readlane(pages, (int)((p >> 6) - pg0));
+  int ntiles;
+  int32_t* next;
+  const int32_t* pages;
+  bool dyn;           // tiles from the shared counter (first come), else wavefront w takes w, w + kWaves, ...
+  mutable int taken;  // tiles this wavefront has taken (static order)
+  KVT_DEV int grab() const { return take_tile(next, dyn, taken); }
+  KVT_DEV uint32_t row0(int t) const {
+    const int64_t p = c0 + 32 * (int64_t)t;
+    const uint32_t page = (uint32_t)__builtin_amdgcn_readfirstlane(pages[(p >> 6) - pg0]);
     return page * (uint32_t)kPage + (uint32_t)(p & (kPage - 1));
   }
-  KVT_DEV int n(int i) const { return (int)min((int64_t)32, c1 - (c0 + 32 * (int64_t)i)); }
+  KVT_DEV int n(int t) const { return (int)min((int64_t)32, c1 - (c0 + 32 * (int64_t)t)); }
 };
 
+// Q operands of the paged tiles (filled by the first round, from the block's copy of Q in LDS, while the first
+// tiles' copies are in flight) and the constants of the tile math.
 struct ColdMath {
-  const h8* qop;
+  h8 qop[8];
   h8 kbias;
   int bexp;
   float cscale;
+  NibbleMasks nm;
+  const uint16_t* qrow;   // this lane's q head in LDS
+  bool qvalid;
+  bool ready;
 };
 
-// One step of the software pipeline: P.V of tile i (stage S, P in p16) and QK^T + softmax of tile i + 1 (stage S ^ 1).
-// In flight on entry, oldest first: K/scales of tile i + 1 (6 copies), V of tile i + 1 (4).  The step issues tile
-// i + 2's K/scales into stage S (whose K and scale rows tile i no longer needs) before the math and its V after P.V.
+// The tiles a wavefront has in hand: ta (P in p16, V in stage S), tb (stage S ^ 1, copies in flight or landed),
+// tc (next to issue), td (taken during the step).
+struct ColdHand {
+  int ta, tb, tc, td;
+};
+
+// One step of the software pipeline: P.V of tile ta (stage S) and QK^T + softmax of tile tb (stage S ^ 1).
+// In flight on entry, oldest first: K/scales of tb (6 copies), V of tb (4).  The step issues tc's K/scales into
+// stage S (whose K and scale rows ta no longer needs) before the math and tc's V after P.V.
 template <int S>
-KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdTiles& T, int i, int ntiles, const ColdMath& M,
+KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHand& hd, const ColdMath& M,
                        f4 acc[16], float& m_run, float& l_run, u4v& p16) {
-  const bool more = i + 2 < ntiles;
-  uint32_t row2 = 0;
+  const bool more = hd.tc < Q.ntiles;
+  uint32_t rowc = 0;
   if (more) {
-    row2 = T.row0(i + 2);
-    cold_issue_k(C, W.cold[S], row2, T.n(i + 2));
-    wait_vmcnt<10>();                     // K/scales of tile i + 1 have landed (and V of tile i before them)
+    rowc = Q.row0(hd.tc);
+    cold_issue_k(C, W.cold[S], rowc, Q.n(hd.tc));
+    wait_vmcnt<10>();                     // K/scales of tb have landed (and V of ta before them)
+    hd.td = Q.grab();
   } else {
     wait_vmcnt<4>();
+    hd.td = Q.ntiles;
   }
   cold_scatter_vs(W.cold[S ^ 1]);
   wave_sync();
   float s[8];
-  cold_pv(W.cold[S], p16, acc);           // one basic block: the two tiles' matrix and VALU work interleave
-  cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, s);
-  wait_lgkm0();                           // tile i's V reads are done before its stage takes new V copies
-  if (more) cold_issue_v(C, W.cold[S], row2);
-  const int n1 = T.n(i + 1);
-  if (n1 < 32) cold_mask(s, n1);
+  cold_pv(W.cold[S], p16, M.nm, acc);     // one basic block: the two tiles' matrix and VALU work interleave
+  cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, M.nm, s);
+  wait_lgkm0();                           // ta's V reads are done before its stage takes new V copies
+  if (more) cold_issue_v(C, W.cold[S], rowc);
+  const int nb = Q.n(hd.tb);
+  if (nb < 32) cold_mask(s, nb);
   p16 = cold_softmax(s, acc, m_run, l_run);
+  hd.ta = hd.tb;
+  hd.tb = hd.tc;
+  hd.tc = hd.td;
 }
 
-// The cold range [c0, c1) of one wavefront: c0 is 32-aligned, every tile lies in one page.  Processed in windows of
-// at most 64 pages (the page ids of a window are held one per lane), each through the two-stage pipeline.
-KVT_DEV void cold_segment(const PosArgs& A, const ColdCtx& C, WaveArea& W, int b, int64_t c0, int64_t c1,
-                          const ColdMath& M, f4 acc[16], float& m_run, float& l_run) {
-  const int lane = threadIdx.x & 63;
+// A wavefront's share of one round: tiles taken from the block counter until none is left, through the two-stage
+// pipeline.
+KVT_DEV void cold_round(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdMath& M, f4 acc[16],
+                        float& m_run, float& l_run) {
+  ColdHand hd;
+  hd.ta = Q.grab();
+  if (hd.ta >= Q.ntiles) return;
+  hd.tb = Q.grab();
+  hd.tc = hd.tb < Q.ntiles ? Q.grab() : Q.ntiles;
+  hd.td = Q.ntiles;
+  wave_sync();
+  const uint32_t r0 = Q.row0(hd.ta);
+  cold_issue_k(C, W.cold[0], r0, Q.n(hd.ta));
+  cold_issue_v(C, W.cold[0], r0);
+  if (hd.tb < Q.ntiles) {
+    const uint32_t r1 = Q.row0(hd.tb);
+    cold_issue_k(C, W.cold[1], r1, Q.n(hd.tb));
+    cold_issue_v(C, W.cold[1], r1);
+  }
+  if (!M.ready) {   // Q operands while the first tiles are in flight
+    load_q_int4(M.qrow, true, M.qvalid, (threadIdx.x & 63) >> 4, M.qop, M.kbias, M.bexp);
+    M.ready = true;
+  }
+  if (hd.tb < Q.ntiles) wait_vmcnt<14>(); else wait_vmcnt<4>();
+  cold_scatter_vs(W.cold[0]);
+  wave_sync();
+  u4v p16;
+  {
+    float s[8];
+    cold_qk(W.cold[0], M.qop, M.kbias, M.bexp, M.cscale, M.nm, s);
+    const int n0 = Q.n(hd.ta);
+    if (n0 < 32) cold_mask(s, n0);
+    p16 = cold_softmax(s, acc, m_run, l_run);
+  }
+  int sa = 0;   // stage of ta
+  while (hd.tb < Q.ntiles) {
+    cold_step<0>(C, W, Q, hd, M, acc, m_run, l_run, p16);
+    sa = 1;
+    if (hd.tb >= Q.ntiles) break;
+    cold_step<1>(C, W, Q, hd, M, acc, m_run, l_run, p16);
+    sa = 0;
+  }
+  // epilogue: P.V of the last tile
+  wait_vmcnt<0>();
+  wave_sync();
+  cold_pv(W.cold[sa], p16, M.nm, acc);
+  wait_lgkm0();
+  wave_sync();
+}
+
+// The block's paged range [c0, c1) (c0 32-aligned), in rounds of at most kBlockPages pages.  Every wavefront of the
+// block calls this (the rounds synchronize the block).
+KVT_DEV void cold_block(const PosArgs& A, const ColdCtx& C, Lds& L, int wave, int b, int64_t c0, int64_t c1,
+                        bool dyn, ColdMath& M, f4 acc[16], float& m_run, float& l_run) {
   for (int64_t s0 = c0; s0 < c1;) {
-    const int64_t s1 = min(c1, ((s0 >> 6) + 64) << 6);
-    ColdTiles T;
-    T.c0 = s0;
-    T.c1 = s1;
-    T.pg0 = s0 >> 6;
-    const int npg = (int)(((s1 - 1) >> 6) - T.pg0 + 1);
-    T.pages = lane < npg ? A.page_table[b * A.pt_stride + T.pg0 + lane] : 0;
-    const int ntiles = (int)((s1 - s0 + 31) >> 5);
-    wave_sync();
-    // prologue: tiles 0 and 1 in flight, QK^T + softmax of tile 0
-    const uint32_t r0 = T.row0(0);
-    cold_issue_k(C, W.cold[0], r0, T.n(0));
-    cold_issue_v(C, W.cold[0], r0);
-    if (ntiles > 1) {
-      const uint32_t r1 = T.row0(1);
-      cold_issue_k(C, W.cold[1], r1, T.n(1));
-      cold_issue_v(C, W.cold[1], r1);
-      wait_vmcnt<14>();
-    } else {
-      wait_vmcnt<4>();
-    }
-    cold_scatter_vs(W.cold[0]);
-    wave_sync();
-    u4v p16;
-    {
-      float s[8];
-      cold_qk(W.cold[0], M.qop, M.kbias, M.bexp, M.cscale, s);
-      const int n0 = T.n(0);
-      if (n0 < 32) cold_mask(s, n0);
-      p16 = cold_softmax(s, acc, m_run, l_run);
-    }
-    for (int i = 0; i + 1 < ntiles; i += 2) {
-      cold_step<0>(C, W, T, i, ntiles, M, acc, m_run, l_run, p16);
-      if (i + 2 < ntiles) cold_step<1>(C, W, T, i + 1, ntiles, M, acc, m_run, l_run, p16);
-    }
-    // epilogue: P.V of the last tile
-    wait_vmcnt<0>();
-    wave_sync();
-    cold_pv(W.cold[(ntiles - 1) & 1], p16, acc);
-    wait_lgkm0();
-    wave_sync();
+    const int64_t s1 = min(c1, ((s0 >> 6) + kBlockPages) << 6);
+    const int64_t pg0 = s0 >> 6;
+    const int npg = (int)(((s1 - 1) >> 6) - pg0 + 1);
+    wait_vmcnt<0>();                      // (the first round: this wavefront's part of the Q copy has landed)
+    __syncthreads();                      // the previous round's tiles and page ids are done with
+    if (threadIdx.x == 0) L.q.cold_next = 0;
+    for (int i = threadIdx.x; i < npg; i += 64 * kWaves) L.q.pages[i] = A.page_table[b * A.pt_stride + pg0 + i];
+    __syncthreads();
+    ColdRound Q{s0, s1, pg0, (int)((s1 - s0 + 31) >> 5), &L.q.cold_next, L.q.pages, dyn, 0};
+    cold_round(C, L.w[wave], Q, M, acc, m_run, l_run);
     s0 = s1;
   }
 }
@@ -672,42 +755,52 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
   }
 }
 
-template <int G8, int S>
-KVT_DEV void hot_step(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, int i, int ntiles, const h8 qop[8],
-                      float cscale, f4 acc[16], float& m_run, float& l_run) {
-  const int64_t p = p0 + 16 * (int64_t)i;
-  if (i + 1 < ntiles) {
-    hot_issue(C, W.hot[S ^ 1], p + 16, (int)min((int64_t)16, p1 - p - 16));
-    wait_vmcnt<10>();
-  } else {
-    wait_vmcnt<0>();
-  }
-  wave_sync();
-  hot_compute<G8>(C, W.hot[S], p, (int)min((int64_t)16, p1 - p), qop, cscale, acc, m_run, l_run);
-  wave_sync();
-}
-
-// Ring positions [p0, p1) of one wavefront in 16-position tiles, double-buffered like the paged range.
+// The block's ring positions [p0, p1) in 16-position tiles handed out from the block counter, double-buffered: the
+// next tile's copies are issued before the current tile's math.
 template <int G8>
-KVT_DEV void hot_segment(const HotCtx& C, WaveArea& W, int64_t p0, int64_t p1, const h8 qop[8], float cscale,
-                         f4 acc[16], float& m_run, float& l_run) {
+KVT_DEV void hot_block(const HotCtx& C, WaveArea& W, int32_t* next, bool dyn, int64_t p0, int64_t p1,
+                       const uint16_t* qrow, bool qvalid, float cscale, f4 acc[16], float& m_run, float& l_run) {
   const int ntiles = (int)((p1 - p0 + 15) >> 4);
+  int taken = 0;
+  auto grab = [&]() -> int { return take_tile(next, dyn, taken); };
+  auto tile_n = [&](int t) -> int { return (int)min((int64_t)16, p1 - p0 - 16 * (int64_t)t); };
+  int ta = grab();
+  if (ta >= ntiles) return;
+  int tb = grab();
   wave_sync();
-  hot_issue(C, W.hot[0], p0, (int)min((int64_t)16, p1 - p0));
-  for (int i = 0; i < ntiles; i += 2) {
-    hot_step<G8, 0>(C, W, p0, p1, i, ntiles, qop, cscale, acc, m_run, l_run);
-    if (i + 1 < ntiles) hot_step<G8, 1>(C, W, p0, p1, i + 1, ntiles, qop, cscale, acc, m_run, l_run);
+  hot_issue(C, W.hot[0], p0 + 16 * (int64_t)ta, tile_n(ta));
+  h8 qop[8];   // while the first tile is in flight
+  load_q_ring(qrow, true, qvalid, (threadIdx.x & 63) >> 4, qop);
+  int sa = 0;
+  for (;;) {
+    const bool more = tb < ntiles;
+    int tc = ntiles;
+    if (more) {
+      hot_issue(C, W.hot[sa ^ 1], p0 + 16 * (int64_t)tb, tile_n(tb));
+      wait_vmcnt<10>();
+      tc = grab();
+    } else {
+      wait_vmcnt<0>();
+    }
+    wave_sync();
+    hot_compute<G8>(C, W.hot[sa], p0 + 16 * (int64_t)ta, tile_n(ta), qop, cscale, acc, m_run, l_run);
+    wave_sync();
+    if (!more) break;
+    ta = tb;
+    tb = tc;
+    sa ^= 1;
   }
 }
 
 template <int G8>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32_t* seq_lens, int H, int gs,
                    int n_splits, const int32_t* split_map, float scale, float* part_o, float* part_ml,
-                   uint32_t pool_rows) {
+                   uint32_t pool_rows, int flags) {
   __shared__ __align__(128) Lds lds;
+  const bool dyn = (flags & KVT_DECODE_DYNAMIC) != 0;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar addressing of the page table
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n16 = lane & 15, kb = lane >> 4;
   // split c of n_b for sequence b: uniform (grid.x = n_splits, grid.y = batch x H) or from the split map
   // (grid.x = total splits, grid.y = H; entry = {b, c, n_b})
@@ -728,47 +821,57 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   const int64_t R = A.ring_len[b];
   const int64_t rbase = A.ring_base[b];
   const int64_t hs = min(max(max(A.ring_start[b], L - R), (int64_t)0), L);   // first ring position
-  // this wavefront's positions [w0, w1): equal shares of the cost 4 hs + kHotCost4 (L - hs)
-  const int64_t n_w = (int64_t)n_b * kWaves;
-  const int64_t wg = (int64_t)c * kWaves + wave;
+  // this block's positions [w0, w1): equal shares of the cost 4 hs + kHotCost4 (L - hs) (paged boundaries 32-aligned)
   const int64_t cost = 4 * hs + kHotCost4 * (L - hs);
   auto bound = [&](int64_t w) -> int64_t {
-    if (w >= n_w) return L;
-    const int64_t x = cost * w / n_w;
+    if (w >= n_b) return L;
+    const int64_t x = cost * w / n_b;
     if (x <= 4 * hs) return (x >> 2) & ~(int64_t)31;
     return hs + (x - 4 * hs + kHotCost4 - 1) / kHotCost4;
   };
-  const int64_t w0 = bound(wg);
-  const int64_t w1 = bound(wg + 1);
+  const int64_t w0 = bound(c);
+  const int64_t w1 = bound(c + 1);
   const float cscale = scale * kLog2e;
   const int hq = n16 & 7;
   const bool qvalid = hq < gs;
-  const uint16_t* qrow = q + b * q_stride_b + (int64_t)(h * gs + (qvalid ? hq : 0)) * kD;
-  const bool qvec16 = (((uintptr_t)q | (uintptr_t)(q_stride_b * 2)) & 15) == 0;   // uniform
+  // the group's q heads into LDS (waves 0-3, 1 KB each; heads beyond the group read as zero)
+  if (wave < 4) {
+    const i32x4 rq = buffer_rsrc(q + b * q_stride_b + (int64_t)h * gs * kD, (uint32_t)gs * kD * 2u);
+    copy16_to_lds(rq, &lds.q.q[2 * wave][0], (uint32_t)(1024 * wave + 16 * lane));
+  }
+  if (threadIdx.x == 0) {
+    lds.q.cold_next = 0;
+    lds.q.hot_next = 0;
+  }
 
   f4 acc[16];   // acc[a]: channels 16 a + j (lane j + 16 kb), q heads 4 kb + i in rows (kb 2, 3 repeat kb 0, 1)
 #pragma unroll
   for (int a = 0; a < 16; ++a) acc[a] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  h8 qop[8];
 
-  // cold segment [w0, min(w1, hs)) from INT4 pages
+  // paged positions [w0, min(w1, hs)) from INT4 pages
   const int64_t ce = min(w1, hs);
-  if (w0 < ce) {
-    h8 kbias;
-    int bexp;
-    load_q_int4(qrow, qvec16, qvalid, kb, qop, kbias, bexp);
+  const bool has_cold = w0 < ce;
+  if (has_cold) {   // (cold_block's first barrier publishes the counters and Q)
     ColdCtx C{buffer_rsrc(A.k4, pool_rows * (uint32_t)H * 128u), buffer_rsrc(A.v4, pool_rows * (uint32_t)H * 128u),
               buffer_rsrc(A.ks4, pool_rows * (uint32_t)H * 16u), buffer_rsrc(A.vs4, pool_rows * (uint32_t)H * 16u),
               (uint32_t)H * 128u, (uint32_t)h * 128u, H, h, {0u, 0u, 0u, 0u}, 0u};
     cold_lane_offsets(C);
-    const ColdMath M{qop, kbias, bexp, cscale};
-    cold_segment(A, C, lds.w[wave], b, w0, ce, M, acc, m_run, l_run);
+    ColdMath M;
+    M.cscale = cscale;
+    M.nm = nibble_masks();
+    M.qrow = &lds.q.q[hq][0];
+    M.qvalid = qvalid;
+    M.ready = false;
+    cold_block(A, C, lds, wave, b, w0, ce, dyn, M, acc, m_run, l_run);
   }
-  // hot segment [max(w0, hs), w1) from the INT8 ring
+  // ring positions [max(w0, hs), w1) from the INT8 ring
   const int64_t hp = max(w0, hs);
   if (hp < w1) {
-    load_q_ring(qrow, qvec16, qvalid, kb, qop);
+    if (!has_cold) {   // Q copied and counters set
+      wait_vmcnt<0>();
+      __syncthreads();
+    }
     constexpr uint32_t NG8 = kD / G8;
     const uint32_t ring_rows = (uint32_t)R;
     HotCtx C{buffer_rsrc(A.rk + rbase * H * kD, ring_rows * (uint32_t)H * kD),
@@ -776,11 +879,12 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
              buffer_rsrc(A.rks + rbase * H * NG8, ring_rows * (uint32_t)H * NG8 * 2u),
              buffer_rsrc(A.rvs + rbase * H * NG8, ring_rows * (uint32_t)H * NG8 * 2u),
              (uint32_t)H * kD, (uint32_t)h * kD, (uint32_t)H * NG8 * 2u, (uint32_t)h * NG8 * 2u, R - 1};
-    hot_segment<G8>(C, lds.w[wave], hp, w1, qop, cscale, acc, m_run, l_run);
+    hot_block<G8>(C, lds.w[wave], &lds.q.hot_next, dyn, hp, w1, &lds.q.q[hq][0], qvalid, cscale, acc, m_run, l_run);
   }
 
-  // ---- merge the four wavefronts (heads 0-7 of the group; lanes n16 >= 8 duplicate n16 - 8)
+  // ---- merge the wavefronts (heads 0-7 of the group; lanes n16 >= 8 duplicate n16 - 8)
   l_run = sum_xor16_32(l_run);
+  wait_vmcnt<0>();                        // (a block without positions still has its Q copy in flight)
   __syncthreads();                        // every wavefront is done with its staging area
   if (kb == 0 && n16 < 8) {
     lds.merge.m[wave][n16] = m_run;
@@ -808,18 +912,16 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   }
   __syncthreads();
   {
-    const int d = threadIdx.x;   // one dim per thread, all heads
-    const int base = d * 8 + (d >> 3) * 4;
-    f4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
+    const int d = threadIdx.x & (kD - 1), half = threadIdx.x / kD;   // one dim and 4 heads per thread
+    const int base = d * 8 + (d >> 3) * 4 + 4 * half;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      o0 += *reinterpret_cast<const f4*>(&lds.merge.o[w][base]);
-      o1 += *reinterpret_cast<const f4*>(&lds.merge.o[w][base + 4]);
+    for (int w = 0; w < kWaves; ++w) o += *reinterpret_cast<const f4*>(&lds.merge.o[w][base]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hh = 4 * half + i;
+      if (hh < gs) part_o[(item * gs + hh) * kD + d] = o[i];
     }
-    const float ov[8] = {o0[0], o0[1], o0[2], o0[3], o1[0], o1[1], o1[2], o1[3]};
-#pragma unroll
-    for (int hh = 0; hh < 8; ++hh)
-      if (hh < gs) part_o[(item * gs + hh) * kD + d] = ov[hh];
   }
   const int tid = threadIdx.x;
   if (tid < gs) {
@@ -844,8 +946,9 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    void* stream) {
+                    int flags, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD) return KVT_EINVAL;
+  if ((((uintptr_t)q) | (uintptr_t)(q_stride_b * 2)) & 15) return KVT_EINVAL;   // Q rows are copied in 16-byte pieces
   if (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL) return KVT_ERANGE;   // 32-bit byte offsets
   const int gs = Hq / H;
   if (gs > 8 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
@@ -857,15 +960,15 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                                          : dim3((unsigned)n_splits, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
   if (group8 == 64) {
-    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(256), 0, st, A, (const uint16_t*)q, q_stride_b,
+    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
                        (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
                        (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows);
+                       (uint32_t)pool_rows, flags);
   } else if (group8 == 256) {
-    hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(256), 0, st, A, (const uint16_t*)q, q_stride_b,
+    hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
                        (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
                        (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows);
+                       (uint32_t)pool_rows, flags);
   } else {
     return KVT_EINVAL;
   }

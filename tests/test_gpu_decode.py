@@ -2,9 +2,10 @@
 bf16-dequantized rows, gemv/test_kv_paged_prefix.py:520-528).
 
 Tolerances: the reference-precision kernel dequantizes exactly like the oracle and accumulates in fp32, so it is
-held to 2e-5 max-abs; the MFMA kernel (fp16 V = code * scale, fp16 P, fp32 accumulation) to the stated bound
-2e-3 max-abs / 1e-3 mean-abs on the configurations' data.  On a single-position context the MFMA output is exactly
-the fp16 dequantized V row (checked bit-exact); it differs from the oracle's bf16 row by at most half a bf16 ulp.
+held to 2e-5 max-abs; the MFMA kernel (exact fp16 codes, scales folded in fp32 (K) or into fp16 P (V), fp32
+accumulation) to the stated bound 2e-3 max-abs / 1e-3 mean-abs on the configurations' data.  On a single-position
+context the MFMA output is exactly code * scale of that V row (checked bit-exact), which differs from the oracle's
+bf16 row by at most half a bf16 ulp.
 """
 import pytest
 import torch
@@ -215,23 +216,33 @@ def test_decode_slot_rings_config0(kvt_pkg):
     assert float((out[0] - exp).abs().max()) < 2e-5
 
 
-def test_decode_graph_replay(kvt_pkg):
-    """The decode step (split-K + combine, both layers) captured in a HIP graph: every replay, with eager work and
-    synchronizations in between, equals the eager result bit for bit."""
+@pytest.mark.parametrize("deterministic", [True, False])
+def test_decode_graph_replay(kvt_pkg, deterministic):
+    """The decode step (split-K + combine) captured in a HIP graph: every replay, with eager work and
+    synchronizations in between, equals the eager result -- bit for bit with the fixed tile order; with tiles taken
+    first come only the fp32 summation order differs (partial sums carry the 1032 x excess of the raw codes until it
+    is removed per tile, so reordering moves the result by about 1e-4 of its scale: bound 2e-4 absolute, a tenth of
+    the oracle tolerance), and every replay stays within the oracle tolerance."""
     from kvtier.kvt import kvt_decode_attn
     dc, oc, q = _build([2500, 900], [1024, 512], seed=7)
     qd = q.to(dev)
     ws = {}
-    eager = kvt_decode_attn(dc, 0, qd, impl="mfma", workspace=ws).clone()
+    eager = kvt_decode_attn(dc, 0, qd, impl="mfma", workspace=ws, deterministic=deterministic).clone()
     out = torch.empty_like(eager)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        kvt_decode_attn(dc, 0, qd, out=out, impl="mfma", workspace=ws)
+        kvt_decode_attn(dc, 0, qd, out=out, impl="mfma", workspace=ws, deterministic=deterministic)
+    exp = _oracle_out(oc, q)
     for i in range(4):
         out.zero_()
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out, eager), f"replay {i}"
+        if deterministic:
+            assert torch.equal(out, eager), f"replay {i}"
+        else:
+            assert float((out - eager).abs().max()) <= 2e-4, f"replay {i}"
+        err = (out.cpu() - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (i, float(err.max()))
         _ = (qd.float() * 2).sum()          # unrelated eager work between replays
         torch.cuda.synchronize()
 
