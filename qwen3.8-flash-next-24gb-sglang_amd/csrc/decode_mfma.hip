@@ -314,8 +314,10 @@ KVT_DEV void cold_issue_k(const ColdCtx& C, ColdStage& st, uint32_t row0, int n)
   }
 }
 
+// row0 = kNoRow: the copies fall outside the buffer (zeros, no memory traffic), so the instruction count stays fixed.
+constexpr uint32_t kNoRow = 0xffffffffu;
 KVT_DEV void cold_issue_v(const ColdCtx& C, ColdStage& st, uint32_t row0) {
-  const uint32_t cb = row0 * C.rowbytes;
+  const uint32_t cb = row0 == kNoRow ? 0x80000000u : row0 * C.rowbytes;
 #pragma unroll
   for (int j = 0; j < 4; ++j) copy16_to_lds(C.rv4, st.v + 1024 * j, cb + C.coff[j]);
 }
@@ -534,7 +536,7 @@ KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHa
   cold_pv(W.cold[S], p16, M.nm, acc);     // one basic block: the two tiles' matrix and VALU work interleave
   cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, M.nm, s);
   wait_lgkm0();                           // ta's V reads are done before its stage takes new V copies
-  if (more) cold_issue_v(C, W.cold[S], rowc);
+  cold_issue_v(C, W.cold[S], more ? rowc : kNoRow);   // unconditional: no branch splits the math above
   const int nb = Q.n(hd.tb);
   if (nb < 32) cold_mask(s, nb);
   p16 = cold_softmax(s, acc, m_run, l_run);
