@@ -296,6 +296,9 @@ KVT_DEV void cold_lane_offsets(ColdCtx& C) {
   C.soff = ((uint32_t)(lane & 31) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
 }
 
+// row0 = kNoRow: the copies fall outside the buffer (zeros, no memory traffic), so the instruction count stays fixed.
+constexpr uint32_t kNoRow = 0xffffffffu;
+
 // Direct-to-LDS copies of one 32-token cold tile (pool rows row0 .. row0 + 31, n valid) into `st`, in two parts:
 // cold_issue_k copies the K codes and both scale rows (exactly 6 vector-memory instructions), cold_issue_v the V codes
 // (exactly 4).  The vmcnt accounting of the tile loop relies on these counts.  Rows beyond n are copied as they are
@@ -303,19 +306,18 @@ KVT_DEV void cold_lane_offsets(ColdCtx& C) {
 // every scale that meets a zero probability is finite.
 KVT_DEV void cold_issue_k(const ColdCtx& C, ColdStage& st, uint32_t row0, int n) {
   const int lane = threadIdx.x & 63;
-  const uint32_t cb = row0 * C.rowbytes;
+  const bool none = row0 == kNoRow;
+  const uint32_t cb = none ? 0x80000000u : row0 * C.rowbytes;
 #pragma unroll
   for (int j = 0; j < 4; ++j) copy16_to_lds(C.rk4, st.k + 1024 * j, cb + C.coff[j]);
   const uint32_t tl = (uint32_t)min(lane & 31, n - 1);
-  const uint32_t soff = ((row0 + tl) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
+  const uint32_t soff = none ? 0x80000000u : ((row0 + tl) * (uint32_t)C.H + (uint32_t)C.h) * 16u;
   if (lane < 32) {
     copy16_to_lds(C.rks4, &st.ks[0][0], soff);
     copy16_to_lds(C.rvs4, &st.vsn[0][0], soff);
   }
 }
 
-// row0 = kNoRow: the copies fall outside the buffer (zeros, no memory traffic), so the instruction count stays fixed.
-constexpr uint32_t kNoRow = 0xffffffffu;
 KVT_DEV void cold_issue_v(const ColdCtx& C, ColdStage& st, uint32_t row0) {
   const uint32_t cb = row0 == kNoRow ? 0x80000000u : row0 * C.rowbytes;
 #pragma unroll
@@ -520,25 +522,18 @@ template <int S>
 KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHand& hd, const ColdMath& M,
                        f4 acc[16], float& m_run, float& l_run, u4v& p16) {
   const bool more = hd.tc < Q.ntiles;
-  uint32_t rowc = 0;
-  if (more) {
-    rowc = Q.row0(hd.tc);
-    cold_issue_k(C, W.cold[S], rowc, Q.n(hd.tc));
-    wait_vmcnt<10>();                     // K/scales of tb have landed (and V of ta before them)
-    hd.td = Q.grab();
-  } else {
-    wait_vmcnt<4>();
-    hd.td = Q.ntiles;
-  }
+  const uint32_t rowc = more ? Q.row0(hd.tc) : kNoRow;
+  cold_issue_k(C, W.cold[S], rowc, more ? Q.n(hd.tc) : 32);   // (dummies past the end: fixed counts)
+  wait_vmcnt<10>();                       // K/scales of tb have landed (and V of ta before them)
+  hd.td = more ? Q.grab() : Q.ntiles;
   cold_scatter_vs(W.cold[S ^ 1]);
   wave_sync();
   float s[8];
   cold_pv(W.cold[S], p16, M.nm, acc);     // one basic block: the two tiles' matrix and VALU work interleave
   cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, M.nm, s);
   wait_lgkm0();                           // ta's V reads are done before its stage takes new V copies
-  cold_issue_v(C, W.cold[S], more ? rowc : kNoRow);   // unconditional: no branch splits the math above
-  const int nb = Q.n(hd.tb);
-  if (nb < 32) cold_mask(s, nb);
+  cold_issue_v(C, W.cold[S], rowc);       // unconditional: no branch splits the math above
+  cold_mask(s, Q.n(hd.tb));
   p16 = cold_softmax(s, acc, m_run, l_run);
   hd.ta = hd.tb;
   hd.tb = hd.tc;
