@@ -54,7 +54,7 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 constexpr int kWaves = 8;          // wavefronts per block (one block per CU: all of the CU's LDS)
 constexpr int kD = 256;
 constexpr int kHotCost4 = 5;       // cost of a ring position when blocks split a sequence; a paged position costs 4
-constexpr int kBlockPages = 900;   // page ids of a block's paged range staged in LDS per round
+constexpr int kBlockPages = 896;   // page ids of a block's paged range staged in LDS per round (14 x 64)
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct PosArgs {
@@ -177,11 +177,19 @@ KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
 }
 
 // 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
-// statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.  Inline assembly rather than the builtin so that the compiler does not treat
-// every later LDS read as dependent on the copy: completion is tracked explicitly with wait_vmcnt by the caller.
+// statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.
+// Inline assembly rather than the builtin so that the compiler does not treat every later LDS read as dependent on
+// the copy: completion is tracked explicitly with wait_vmcnt by the caller.
 KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
   asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
+               : "memory");
+}
+
+// 4 bytes per lane from rsrc + voffset into lds + 4 * lane (same conventions).
+KVT_DEV void copy4_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
                : "memory");
 }
 
@@ -542,23 +550,10 @@ KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHa
 
 // A wavefront's share of one round: tiles taken from the block counter until none is left, through the two-stage
 // pipeline.
-KVT_DEV void cold_round(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdMath& M, f4 acc[16],
-                        float& m_run, float& l_run) {
-  ColdHand hd;
-  hd.ta = Q.grab();
-  if (hd.ta >= Q.ntiles) return;
-  hd.tb = Q.grab();
-  hd.tc = hd.tb < Q.ntiles ? Q.grab() : Q.ntiles;
-  hd.td = Q.ntiles;
-  wave_sync();
-  const uint32_t r0 = Q.row0(hd.ta);
-  cold_issue_k(C, W.cold[0], r0, Q.n(hd.ta));
-  cold_issue_v(C, W.cold[0], r0);
-  if (hd.tb < Q.ntiles) {
-    const uint32_t r1 = Q.row0(hd.tb);
-    cold_issue_k(C, W.cold[1], r1, Q.n(hd.tb));
-    cold_issue_v(C, W.cold[1], r1);
-  }
+// The rest of a round once tiles ta (stage 0) and tb (stage 1, if any) are in flight: the pipeline until the block's
+// tiles run out.
+KVT_DEV void cold_round_run(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHand& hd, ColdMath& M,
+                            f4 acc[16], float& m_run, float& l_run) {
   if (!M.ready) {   // Q operands while the first tiles are in flight
     load_q_int4(M.qrow, true, M.qvalid, (threadIdx.x & 63) >> 4, M.qop, M.kbias, M.bexp);
     M.ready = true;
@@ -590,10 +585,78 @@ KVT_DEV void cold_round(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdM
   wave_sync();
 }
 
+// A wavefront's share of one round: tiles taken from the block counter until none is left.
+KVT_DEV void cold_round(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdMath& M, f4 acc[16],
+                        float& m_run, float& l_run) {
+  ColdHand hd;
+  hd.ta = Q.grab();
+  if (hd.ta >= Q.ntiles) return;
+  hd.tb = Q.grab();
+  hd.tc = hd.tb < Q.ntiles ? Q.grab() : Q.ntiles;
+  hd.td = Q.ntiles;
+  wave_sync();
+  const uint32_t r0 = Q.row0(hd.ta);
+  cold_issue_k(C, W.cold[0], r0, Q.n(hd.ta));
+  cold_issue_v(C, W.cold[0], r0);
+  if (hd.tb < Q.ntiles) {
+    const uint32_t r1 = Q.row0(hd.tb);
+    cold_issue_k(C, W.cold[1], r1, Q.n(hd.tb));
+    cold_issue_v(C, W.cold[1], r1);
+  }
+  cold_round_run(C, W, Q, hd, M, acc, m_run, l_run);
+}
+
 // The block's paged range [c0, c1) (c0 32-aligned), in rounds of at most kBlockPages pages.  Every wavefront of the
 // block calls this (the rounds synchronize the block).
 KVT_DEV void cold_block(const PosArgs& A, const ColdCtx& C, Lds& L, int wave, int b, int64_t c0, int64_t c1,
                         bool dyn, ColdMath& M, f4 acc[16], float& m_run, float& l_run) {
+  // First round, started without waiting for anything: tiles wave and wave + kWaves (page ids by scalar loads)
+  // and the round's page ids (2 direct-to-LDS copies of 64 ids per wavefront; copies past the round read nothing
+  // and land in this wavefront's stage 1, which tile wave + kWaves overwrites afterwards) go out at once; one
+  // barrier then publishes the page ids and the block's Q.  The shared counter starts at 2 kWaves.
+  {
+    const int64_t s1 = min(c1, ((c0 >> 6) + kBlockPages) << 6);
+    const int64_t pg0 = c0 >> 6;
+    const int npg = (int)(((s1 - 1) >> 6) - pg0 + 1);
+    const int lane = threadIdx.x & 63;
+    const i32x4 rp = buffer_rsrc(A.page_table + b * A.pt_stride + pg0, (uint32_t)npg * 4u);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int chunk = wave + kWaves * j;
+      void* dst = chunk * 64 < kBlockPages ? (void*)&L.q.pages[64 * chunk] : (void*)L.w[wave].cold[1].k;
+      copy4_to_lds(rp, dst, (uint32_t)(256 * chunk + 4 * lane));
+    }
+    ColdRound Q{c0, s1, pg0, (int)((s1 - c0 + 31) >> 5), &L.q.cold_next, L.q.pages, dyn, 2};
+    ColdHand hd;
+    hd.ta = wave;
+    hd.tb = wave + kWaves;
+    auto page_row = [&](int t) -> uint32_t {
+      const int64_t p = c0 + 32 * (int64_t)t;
+      return (uint32_t)A.page_table[b * A.pt_stride + (p >> 6)] * (uint32_t)kPage + (uint32_t)(p & (kPage - 1));
+    };
+    int issued = 0;
+    if (hd.ta < Q.ntiles) {
+      const uint32_t r0 = page_row(hd.ta);
+      cold_issue_k(C, L.w[wave].cold[0], r0, Q.n(hd.ta));
+      cold_issue_v(C, L.w[wave].cold[0], r0);
+      issued = 1;
+      if (hd.tb < Q.ntiles) {
+        const uint32_t r1 = page_row(hd.tb);
+        cold_issue_k(C, L.w[wave].cold[1], r1, Q.n(hd.tb));
+        cold_issue_v(C, L.w[wave].cold[1], r1);
+        issued = 2;
+      }
+    }
+    // the Q copy (waves 0-3) and the page-id copies are older than the tiles: wait for them only
+    if (issued == 2) wait_vmcnt<20>(); else if (issued == 1) wait_vmcnt<10>(); else wait_vmcnt<0>();
+    __syncthreads();
+    if (hd.ta < Q.ntiles) {
+      hd.tc = hd.tb < Q.ntiles ? Q.grab() : Q.ntiles;
+      hd.td = Q.ntiles;
+      cold_round_run(C, L.w[wave], Q, hd, M, acc, m_run, l_run);
+    }
+    c0 = s1;
+  }
   for (int64_t s0 = c0; s0 < c1;) {
     const int64_t s1 = min(c1, ((s0 >> 6) + kBlockPages) << 6);
     const int64_t pg0 = s0 >> 6;
@@ -837,7 +900,7 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
     copy16_to_lds(rq, &lds.q.q[2 * wave][0], (uint32_t)(1024 * wave + 16 * lane));
   }
   if (threadIdx.x == 0) {
-    lds.q.cold_next = 0;
+    lds.q.cold_next = 2 * kWaves;   // the first round starts with tiles w and w + kWaves of each wavefront
     lds.q.hot_next = 0;
   }
 
