@@ -322,6 +322,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--impl", default=os.environ.get("KVT_DECODE_IMPL", "mfma"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fused-combine", action="store_true",
+                    help="merge the split partials inside the split-K launch instead of in the combine kernel")
     ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
@@ -354,7 +356,8 @@ def main():
 
     def step(events=None):
         for layer in range(LAYERS):
-            kvt_decode_attn(cache, layer, q[layer], out=outs[layer], impl=args.impl, workspace=ws, events=events)
+            kvt_decode_attn(cache, layer, q[layer], out=outs[layer], impl=args.impl, workspace=ws, events=events,
+                            fused_combine=args.fused_combine)
 
     for _ in range(args.warmup):
         step()
@@ -414,6 +417,7 @@ def main():
             "workload": "decode 262144-token context x 12 layers: 16 Q / 2 KV heads, D 256, INT8-G64 ring 8192 + "
                         "253952 tokens in 3968 INT4-G32 pages (permuted), batch 1",
             "impl": args.impl,
+            "combine": "fused (in the split-K launch)" if args.fused_combine else "combine kernel",
             "kv_bytes_per_layer": bytes_layer,
             "kv_bytes_per_step": bytes_step,
         },

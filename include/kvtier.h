@@ -130,14 +130,20 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
  * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 8, D = 256, q and q_stride_b 16-byte
  * aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 <
  * 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the compact gather + FA2 pair (flat patch
- * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode. */
+ * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode.
+ * counters non-NULL (int32 [batch * H * 4], zero before the first call; every call leaves them zero): the kernel
+ * also merges its partials into out_f32 and/or out_bf16 ([batch, Hq, D], batch stride out_stride_b elements), so no
+ * kvt_decode_combine is needed.  Every block writes its partial (the slot of its split) and counts itself; the last
+ * min(16, splits, CUs / 2) arrivals of a (sequence, KV head) wait until every partial is written (each waits for
+ * blocks that have arrived or can still run on the CUs no waiter holds) and merge (q head, 32-dim) slices over all
+ * partials.  The summation order follows the arrival order.  Calls sharing counters must not run concurrently. */
 #define KVT_DECODE_DYNAMIC 1
 int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    int flags, void* stream);
+                    int flags, void* counters, void* out_f32, void* out_bf16, int64_t out_stride_b, void* stream);
 
 /* Merge the split-K partials: out[b, hq, :] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c (fp32 and/or bf16
  * output, either may be NULL; batch stride out_stride_b elements).  chunk > 0: split c covers positions

@@ -53,7 +53,8 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 8;          // wavefronts per block (one block per CU: all of the CU's LDS)
 constexpr int kD = 256;
-constexpr int kHotCost4 = 5;       // cost of a ring position when blocks split a sequence; a paged position costs 4
+constexpr int kHotCost4 = 7;       // cost of a ring position when blocks split a sequence; a paged position costs 4
+                                   // (measured: with 5 the blocks that hold ring positions finish last)
 constexpr int kBlockPages = 896;   // page ids of a block's paged range staged in LDS per round (14 x 64)
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -148,6 +149,11 @@ struct MergeArea {
   float o[kWaves][kMergePitch];
 };
 
+// A merging block's per-wavefront weights of one chunk of 128 partials (in-kernel merge).
+struct MergeWeights {
+  float w[kWaves][128];
+};
+
 // Block-wide data: the group's q heads (copied once; rows beyond the group read as zero) and the work handed out
 // inside the block (the next paged tile of the current round, the next ring tile, the round's page ids).
 struct BlockQueue {
@@ -161,6 +167,7 @@ struct Lds {
   union {
     WaveArea w[kWaves];
     MergeArea merge;
+    MergeWeights mw;
   };
   BlockQueue q;
 };
@@ -610,10 +617,12 @@ KVT_DEV void cold_round(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdM
 // block calls this (the rounds synchronize the block).
 KVT_DEV void cold_block(const PosArgs& A, const ColdCtx& C, Lds& L, int wave, int b, int64_t c0, int64_t c1,
                         bool dyn, ColdMath& M, f4 acc[16], float& m_run, float& l_run) {
-  // First round, started without waiting for anything: tiles wave and wave + kWaves (page ids by scalar loads)
-  // and the round's page ids (2 direct-to-LDS copies of 64 ids per wavefront; copies past the round read nothing
-  // and land in this wavefront's stage 1, which tile wave + kWaves overwrites afterwards) go out at once; one
-  // barrier then publishes the page ids and the block's Q.  The shared counter starts at 2 kWaves.
+  // First round: the round's page ids (2 direct-to-LDS copies of 64 ids per wavefront; copies past the round read
+  // nothing and land in this wavefront's stage 1, which tile wave + kWaves overwrites afterwards) and tile wave (page
+  // id by a scalar load) go out at once.  Tile wave + kWaves goes out only once they have landed: at start-up every
+  // CU asks at once, and a first burst of one tile per wavefront lands sooner than one of two (the second lands
+  // while the first is computed).  One barrier publishes the page ids and the block's Q.  The shared counter starts
+  // at 2 kWaves.
   {
     const int64_t s1 = min(c1, ((c0 >> 6) + kBlockPages) << 6);
     const int64_t pg0 = c0 >> 6;
@@ -634,22 +643,19 @@ KVT_DEV void cold_block(const PosArgs& A, const ColdCtx& C, Lds& L, int wave, in
       const int64_t p = c0 + 32 * (int64_t)t;
       return (uint32_t)A.page_table[b * A.pt_stride + (p >> 6)] * (uint32_t)kPage + (uint32_t)(p & (kPage - 1));
     };
-    int issued = 0;
+    uint32_t r0 = 0, r1 = 0;
     if (hd.ta < Q.ntiles) {
-      const uint32_t r0 = page_row(hd.ta);
+      r0 = page_row(hd.ta);
       cold_issue_k(C, L.w[wave].cold[0], r0, Q.n(hd.ta));
       cold_issue_v(C, L.w[wave].cold[0], r0);
-      issued = 1;
-      if (hd.tb < Q.ntiles) {
-        const uint32_t r1 = page_row(hd.tb);
-        cold_issue_k(C, L.w[wave].cold[1], r1, Q.n(hd.tb));
-        cold_issue_v(C, L.w[wave].cold[1], r1);
-        issued = 2;
-      }
     }
-    // the Q copy (waves 0-3) and the page-id copies are older than the tiles: wait for them only
-    if (issued == 2) wait_vmcnt<20>(); else if (issued == 1) wait_vmcnt<10>(); else wait_vmcnt<0>();
+    if (hd.tb < Q.ntiles) r1 = page_row(hd.tb);
+    wait_vmcnt<0>();   // the first tile, the Q copy and the page ids have landed
     __syncthreads();
+    if (hd.tb < Q.ntiles) {
+      cold_issue_k(C, L.w[wave].cold[1], r1, Q.n(hd.tb));
+      cold_issue_v(C, L.w[wave].cold[1], r1);
+    }
     if (hd.ta < Q.ntiles) {
       hd.tc = hd.tb < Q.ntiles ? Q.grab() : Q.ntiles;
       hd.td = Q.ntiles;
@@ -852,11 +858,102 @@ KVT_DEV void hot_block(const HotCtx& C, WaveArea& W, int32_t* next, bool dyn, in
   }
 }
 
+// ---- split merge inside the kernel (optional; counters != nullptr).  Every block writes its partial (the slot of
+// its split, as for the combine kernel), counts itself flushed and takes an arrival ticket per (sequence, KV head).
+// The last K arrivals (K = min(kmerge, n_b), kmerge <= kMergers and at most half the CUs) wait until all n_b
+// partials are flushed -- fewer than half the CUs wait, each for blocks that have arrived or can still be
+// dispatched onto the other CUs -- and merge the output in slices of (q head, 32 dims) over all partials, one
+// slice per wavefront: reading the partials is spread over K CUs.  The last merger to finish resets the counters.
+constexpr int kMergers = 16;
+constexpr int kSc1 = 16;             // cache-policy operand of the raw buffer builtins: sc1 (device-coherent)
+constexpr int kSpinLimit = 1 << 22;  // polls of a waiting merger (each ~1 us)
+constexpr int kCounterStride = 4;    // counter words per (sequence, KV head): arrivals, flushed, mergers done, -
+
+KVT_DEV __amdgpu_buffer_rsrc_t rsrc_dev(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Partials cross XCDs (each has its own L2): they are written and read with device-coherent accesses (sc1: written
+// through to, and read from, the coherence point past the L2), so neither side needs a whole-L2 writeback or
+// invalidate; a wait for the stores' completion (vmcnt 0) orders them before the count.
+KVT_DEV void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+KVT_DEV void st_dev_i32(int32_t* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+KVT_DEV int ld_dev_i32(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KVT_DEV int add_dev_i32(int32_t* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+KVT_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One wavefront merges q head hh, dims d0 .. d0 + 31, over the n partial slots sbase .. sbase + n - 1, in chunks of
+// 128 partials (online rescaling between chunks).  In a chunk, lanes l and l + 64 hold (m, l) of parts l and
+// l + 64; lane l reads dims d0 + 4 (l & 7) .. + 3 of parts 8 k + (l >> 3), k < 16 -- all 18 loads in flight at once
+// -- and the 8 lane groups are summed at the end.  out[hh][d] = o / l; an empty whole gives 0 / 0 = NaN (as the
+// combine kernel).
+KVT_DEV void merge_head(const float* part_o, const float* part_ml, int64_t sbase, int n, int gs, int hh, int d0,
+                        float* wbuf, bool valid, float* out_f32, uint16_t* out_bf16, int64_t row0) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t rows = (uint32_t)n * gs;
+  const auto rml = rsrc_dev(part_ml + sbase * gs * 2, rows * 8u);
+  const auto ro = rsrc_dev(part_o + sbase * gs * kD, rows * (uint32_t)(kD * 4));
+  const uint32_t none = 0x80000000u;   // beyond the range: the load returns zeros
+  float M = -INFINITY, L = 0.f;
+  f4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < n; c0 += 128) {
+    f4 v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int p = c0 + 8 * k + (lane >> 3);
+      const uint32_t off = p < n ? (uint32_t)(((p * gs + hh) * kD + d0 + 4 * (lane & 7)) * 4) : none;
+      v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, kSc1));
+    }
+    const int p0 = c0 + lane, p1 = c0 + 64 + lane;
+    const v2i a0 = __builtin_amdgcn_raw_buffer_load_b64(rml, p0 < n ? (uint32_t)((p0 * gs + hh) * 8) : none, 0, kSc1);
+    const v2i a1 = __builtin_amdgcn_raw_buffer_load_b64(rml, p1 < n ? (uint32_t)((p1 * gs + hh) * 8) : none, 0, kSc1);
+    const float m0 = p0 < n ? __int_as_float(a0.x) : -INFINITY;
+    const float m1 = p1 < n ? __int_as_float(a1.x) : -INFINITY;
+    const float Mn = fmaxf(M, group_max<64>(fmaxf(m0, m1)));
+    const float alpha = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((M - Mn) * kLog2e);
+    M = Mn;
+    const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m0 - M) * kLog2e);
+    const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m1 - M) * kLog2e);
+    L = L * alpha + wave_sum(w0 * __int_as_float(a0.y) + w1 * __int_as_float(a1.y));
+    o *= alpha;
+    wbuf[lane] = w0;
+    wbuf[64 + lane] = w1;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o += wbuf[8 * k + (lane >> 3)] * v[k];
+    __builtin_amdgcn_wave_barrier();
+  }
+#pragma unroll
+  for (int x = 8; x < 64; x <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] += __shfl_xor(o[i], x, 64);
+  }
+  if (lane < 8) {
+    const int64_t row = row0 + (int64_t)hh * kD + d0 + 4 * lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float r = valid ? o[i] / L : __builtin_nanf("");
+      if (out_f32 != nullptr) out_f32[row + i] = r;
+      if (out_bf16 != nullptr) out_bf16[row + i] = bf16_rne(r);
+    }
+  }
+}
+
 template <int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32_t* seq_lens, int H, int gs,
                    int n_splits, const int32_t* split_map, float scale, float* part_o, float* part_ml,
-                   uint32_t pool_rows, int flags) {
+                   uint32_t pool_rows, int flags, int32_t* counters, int kmerge, float* out_f32,
+                   uint16_t* out_bf16, int64_t out_stride_b) {
   __shared__ __align__(128) Lds lds;
   const bool dyn = (flags & KVT_DECODE_DYNAMIC) != 0;
   const int lane = threadIdx.x & 63;
@@ -946,6 +1043,11 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
   l_run = sum_xor16_32(l_run);
   wait_vmcnt<0>();                        // (a block without positions still has its Q copy in flight)
   __syncthreads();                        // every wavefront is done with its staging area
+  const int tid = threadIdx.x;
+  const bool fused = counters != nullptr;
+  int32_t* ctr = fused ? counters + ((int64_t)b * H + h) * kCounterStride : nullptr;
+  int ticket_raw = 0;
+  if (fused && tid == 0) ticket_raw = add_dev_i32(&ctr[0], 1);   // arrival ticket, in flight during the merge
   if (kb == 0 && n16 < 8) {
     lds.merge.m[wave][n16] = m_run;
     lds.merge.l[wave][n16] = l_run;
@@ -971,29 +1073,70 @@ decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32
     }
   }
   __syncthreads();
+  // the block's partial: thread (d, half) holds o of dim d for q heads 4 half .. + 3; threads < gs (m, l) of a head
+  const int d = tid & (kD - 1), half = tid / kD;
+  f4 ob = {0.f, 0.f, 0.f, 0.f};
   {
-    const int d = threadIdx.x & (kD - 1), half = threadIdx.x / kD;   // one dim and 4 heads per thread
     const int base = d * 8 + (d >> 3) * 4 + 4 * half;
-    f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) o += *reinterpret_cast<const f4*>(&lds.merge.o[w][base]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int hh = 4 * half + i;
-      if (hh < gs) part_o[(item * gs + hh) * kD + d] = o[i];
-    }
+    for (int w = 0; w < kWaves; ++w) ob += *reinterpret_cast<const f4*>(&lds.merge.o[w][base]);
   }
-  const int tid = threadIdx.x;
+  float mb = -INFINITY, lb = 0.f;   // natural-log units
   if (tid < gs) {
     float M = lds.merge.m[0][tid];
     for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds.merge.m[w][tid]);
-    float l = 0.f;
     for (int w = 0; w < kWaves; ++w) {
       const float mw = lds.merge.m[w][tid];
-      l += mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M) * lds.merge.l[w][tid];
+      lb += mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M) * lds.merge.l[w][tid];
     }
-    part_ml[(item * gs + tid) * 2 + 0] = M == -INFINITY ? -INFINITY : M / kLog2e;   // natural-log units
-    part_ml[(item * gs + tid) * 2 + 1] = l;
+    mb = M == -INFINITY ? -INFINITY : M / kLog2e;
+  }
+  // the partial, in the slot of this split (read by the combine kernel or by the mergers below)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (4 * half + i < gs) st_dev(&part_o[(item * gs + 4 * half + i) * kD + d], ob[i]);
+  if (tid < gs) {
+    st_dev(&part_ml[(item * gs + tid) * 2 + 0], mb);
+    st_dev(&part_ml[(item * gs + tid) * 2 + 1], lb);
+  }
+  if (!fused) return;
+  // ---- in-kernel merge of the splits (see merge_head)
+  int* lds_word = &lds.q.hot_next;                         // (the block's tile counters are no longer used)
+  wait_vmcnt<0>();                                         // the partial has reached the coherence point
+  __syncthreads();
+  if (tid == 0) {
+    add_dev_i32(&ctr[1], 1);                               // flushed
+    *lds_word = ticket_raw;
+  }
+  __syncthreads();
+  const int ticket = *lds_word;
+  const int K = min(kmerge, n_b);
+  if (ticket < n_b - K) return;
+  // one of the last K arrivals: wait until all n_b partials are flushed
+  __syncthreads();                                         // (everyone has read the ticket word)
+  if (tid == 0) {
+    int ok = 0;
+    for (int it = 0; it < kSpinLimit; ++it) {
+      if (ld_dev_i32(&ctr[1]) >= n_b) {
+        ok = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(10);
+    }
+    *lds_word = ok;
+  }
+  __syncthreads();
+  const bool ok = *lds_word != 0;                          // (a poll limit that ran out leaves NaN in the output)
+  const int64_t sbase = ((int64_t)b * H + h) * n_splits;   // this (sequence, KV head)'s first partial slot
+  const int64_t out_row0 = (int64_t)b * out_stride_b + (int64_t)h * gs * kD;
+  for (int j = ticket - (n_b - K) + K * wave; j < gs * 8; j += K * kWaves)   // slice j: q head j / 8, dims 32 (j % 8)
+    merge_head(part_o, part_ml, sbase, n_b, gs, j >> 3, 32 * (j & 7), lds.mw.w[wave], ok, out_f32, out_bf16,
+               out_row0);
+  __syncthreads();
+  if (tid == 0 && add_dev_i32(&ctr[2], 1) == K - 1) {    // the last merger: every count has been read
+    st_dev_i32(&ctr[0], 0);
+    st_dev_i32(&ctr[1], 0);
+    st_dev_i32(&ctr[2], 0);
   }
 }
 
@@ -1006,12 +1149,21 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    int flags, void* stream) {
+                    int flags, void* counters, void* out_f32, void* out_bf16, int64_t out_stride_b, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD) return KVT_EINVAL;
   if ((((uintptr_t)q) | (uintptr_t)(q_stride_b * 2)) & 15) return KVT_EINVAL;   // Q rows are copied in 16-byte pieces
   if (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL) return KVT_ERANGE;   // 32-bit byte offsets
   const int gs = Hq / H;
   if (gs > 8 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
+  if (counters != nullptr && out_f32 == nullptr && out_bf16 == nullptr) return KVT_EINVAL;
+  // mergers of the in-kernel merge: they wait for the others, so at most half the CUs may hold them
+  static int cu_count[64];   // per device, read once (a benign race: every writer stores the same value)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return KVT_ELAUNCH;
+  if (cu_count[dev] == 0 &&
+      hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return KVT_ELAUNCH;
+  const int kmerge = max(1, min(kMergers, cu_count[dev] / 2));
   PosArgs A{(const uint8_t*)k4,         (const uint8_t*)v4,        (const uint16_t*)ks4,     (const uint16_t*)vs4,
             (const int8_t*)rk,          (const int8_t*)rv,         (const uint16_t*)rks,     (const uint16_t*)rvs,
             (const int64_t*)ring_base,  (const int32_t*)ring_len,  (const int64_t*)ring_start,
@@ -1023,12 +1175,14 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
     hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
                        (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
                        (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows, flags);
+                       (uint32_t)pool_rows, flags, (int32_t*)counters, kmerge, (float*)out_f32,
+                       (uint16_t*)out_bf16, out_stride_b);
   } else if (group8 == 256) {
     hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
                        (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
                        (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows, flags);
+                       (uint32_t)pool_rows, flags, (int32_t*)counters, kmerge, (float*)out_f32,
+                       (uint16_t*)out_bf16, out_stride_b);
   } else {
     return KVT_EINVAL;
   }

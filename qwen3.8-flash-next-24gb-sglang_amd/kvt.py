@@ -236,7 +236,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                     impl: str = "ref", chunk: Optional[int] = None, max_len: Optional[int] = None,
                     out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
                     events: Optional[list] = None, splits: Optional[int] = None,
-                    deterministic: bool = False) -> torch.Tensor:
+                    deterministic: bool = False, fused_combine: bool = False,
+                    tile_order: Optional[str] = None) -> torch.Tensor:
     """Decode attention of one query token per sequence over the tiered cache of `layer`.
 
     q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
@@ -244,9 +245,17 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per (sequence, KV head), or, by
     default for more than one sequence, split counts in proportion to each sequence's length.
     events: if a list, timing events (start, after the split-K kernel, after the combine) are appended.
-    deterministic (impl "mfma"): tiles go to the wavefronts of a block in a fixed order, so repeated calls give
-    bit-identical results; by default they go first come (the block's wavefronts finish together, about 4 % faster
-    at 262,144 positions) and the fp32 summation order varies in the last bits from call to call.
+    deterministic (impl "mfma"): bit-identical results from call to call: tiles go to the wavefronts of a block in
+    a fixed order and the combine kernel merges the splits.  By default tiles go first come (the block's wavefronts
+    finish together, about 4 % faster at 262,144 positions) and the fp32 summation order varies in the last bits.
+    tile_order ("fixed" / "dynamic", impl "mfma"): overrides the tile order alone.
+    fused_combine (impl "mfma", not deterministic): the split-K kernel merges its own partials and writes `out`
+    (every block writes its partial and counts itself; the last 16 arrivals wait for all partials and each merges
+    (q head, 32-dim) slices over all of them); otherwise kvt_decode_combine runs after it.  One launch instead of
+    two: faster when launches are not in a graph (262,144 positions: 44.6 against 46.5 us per layer), slower in a
+    graph (42.9 against 41.9 us), hence off by default.  The merged sum's order follows the arrival order, so
+    deterministic calls always use the combine kernel.  The merge counters live in the workspace and return to zero
+    after every call; concurrent calls must not share a workspace.
     """
     S = cache.n_seqs
     assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == cache.D and q.dtype == torch.bfloat16
@@ -272,11 +281,13 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         if chunk is None:
             chunk = _choose_chunk(max_len, S * H)
         n_chunks = max(1, -(-max_len // chunk))
-    need_o = S * H * n_chunks * gs * D
+    fused = impl == "mfma" and fused_combine and not deterministic and n_chunks <= 1024
+    n_slots = n_chunks   # partial slots per (sequence, KV head)
+    need_o = S * H * n_slots * gs * D
     po = ws.get("part_o")
     if po is None or po.numel() < need_o:
         po = torch.empty(need_o, dtype=torch.float32, device=q.device)
-        pml = torch.empty(S * H * n_chunks * gs * 2, dtype=torch.float32, device=q.device)
+        pml = torch.empty(S * H * n_slots * gs * 2, dtype=torch.float32, device=q.device)
         ws["part_o"], ws["part_ml"] = po, pml
     pml = ws["part_ml"]
     if out is None:
@@ -299,13 +310,28 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     elif impl == "mfma":
         if cache.rk[layer].numel() >= 2 ** 31:
             raise ValueError("kvt_decode_mfma: ring buffers beyond 2^31 bytes per layer are not supported")
+        fixed_order = (tile_order or ("fixed" if deterministic else "dynamic")) == "fixed"
+        ctr = None
+        if fused:
+            # 4 words per (sequence, KV head): arrivals, flushed partials, finished mergers (zero between calls)
+            ctr = ws.get("merge_counters")
+            if ctr is None or ctr.numel() < S * H * 4 or ctr.device != q.device:
+                ctr = torch.zeros(max(S * H * 4, 64), dtype=torch.int32, device=q.device)
+                ws["merge_counters"] = ctr
         _lib.call("kvt_decode_mfma", q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8,
                   cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
                   cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
                   cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
                   cache.page_table.stride(0), cache.k4[layer].shape[0], scale, n_chunks, _lib.ptr(split_map), n_map,
-                  po.data_ptr(), pml.data_ptr(), 0 if deterministic else 1, _lib.stream())
+                  po.data_ptr(), pml.data_ptr(), 0 if fixed_order else 1, _lib.ptr(ctr),
+                  out.data_ptr() if fused and out.dtype == torch.float32 else None,
+                  out.data_ptr() if fused and out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
+        if fused:
+            if events is not None:
+                ev1.record()
+                events.append((ev0, ev1, ev1))
+            return out
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
