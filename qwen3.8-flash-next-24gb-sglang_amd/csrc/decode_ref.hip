@@ -172,17 +172,19 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 }
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
-// grid (D / 16, Hq, batch), 256 threads: thread (d = 16 blockIdx.x + tid % 16, part = tid / 16) loads splits
-// c = part (mod 16) of one output channel, all loads in flight at once, and merges them in one pass with a running
-// max (m, num, den) <- (max(m, m_c), num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')); the 16
-// parts merge the same way through LDS.  One block per CU-sized piece spreads the merge over the whole chip.
-// An empty context gives 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
-constexpr int kCombParts = 16;
-constexpr int kCombDims = 16;
-constexpr int kCombUnroll = 16;   // splits per thread and round
+// grid (D / 64, Hq, batch), 256 threads = 4 wavefronts: lane l of wavefront w holds dims 4 (l & 15) .. + 3 of the
+// block's 64 and merges splits c = 16 k + 4 (l >> 4) + w, k < 8, of each round of 128 (8 16-byte loads of o and 8
+// of (m, l) per lane, all in flight at once), with a running max: (m, num, den) <- (max(m, m_c),
+// num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')).  The 16 merges of a dim quad then combine
+// across lanes (xor 16, 32) and wavefronts (LDS).  An empty context gives 0/0 = NaN
+// (gemv/test_kv_paged_prefix.py:524-526).
+constexpr int kCombDims = 64;
+constexpr int kCombRound = 128;   // splits per round
+
+typedef float f4c __attribute__((ext_vector_type(4)));
 
 // Partial maxima are in natural-log units; the weights use the hardware exp2 on log2-scaled differences (<= 0).
-KVT_DEV void merge_into(float& m, float& num, float& den, float mc, float oc, float lc) {
+KVT_DEV void merge_into(float& m, f4c& num, float& den, float mc, f4c oc, float lc) {
   constexpr float kL2e = 1.4426950408889634f;
   const float mn = fmaxf(m, mc);
   if (mn == -INFINITY) return;   // both empty
@@ -192,47 +194,66 @@ KVT_DEV void merge_into(float& m, float& num, float& den, float mc, float oc, fl
   m = mn;
 }
 
-__global__ void __launch_bounds__(kCombDims * kCombParts) decode_combine_kernel(
+__global__ void __launch_bounds__(256) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
     const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
     int64_t out_stride_b) {
-  __shared__ float red[kCombParts][3][kCombDims];
+  __shared__ float red[4][16][6];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
-  const int tid = threadIdx.x, dl = tid % kCombDims, part = tid / kCombDims;
-  const int d = blockIdx.x * kCombDims + dl;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int dq = lane & 15, sub = lane >> 4;
+  const int d0 = blockIdx.x * kCombDims + 4 * dq;
   const int64_t L = seq_lens[b];
   // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
   // split_counts (chunk 0): sequence b uses the first split_counts[b] slots
   const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
                              : (split_counts != nullptr ? split_counts[b] : n_chunks);
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
-  float m = -INFINITY, num = 0.0f, den = 0.0f;
-  for (int c0 = part; c0 < used; c0 += kCombUnroll * kCombParts) {
-    float mv[kCombUnroll], lv[kCombUnroll], ov[kCombUnroll];
+  float m = -INFINITY, den = 0.0f;
+  f4c num = {0.f, 0.f, 0.f, 0.f};
+  for (int r0 = 0; r0 < used; r0 += kCombRound) {
+    f4c ov[8];
+    float mv[8], lv[8];
 #pragma unroll
-    for (int u = 0; u < kCombUnroll; ++u) {
-      const int c = c0 + u * kCombParts;
+    for (int k = 0; k < 8; ++k) {
+      const int c = r0 + 16 * k + 4 * sub + w;
       const int64_t it = (base + (c < used ? c : 0)) * gs + j;
-      mv[u] = c < used ? part_ml[it * 2] : -INFINITY;
-      lv[u] = part_ml[it * 2 + 1];
-      ov[u] = part_o[it * D + d];
+      ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
+      mv[k] = c < used ? part_ml[it * 2] : -INFINITY;
+      lv[k] = part_ml[it * 2 + 1];
     }
 #pragma unroll
-    for (int u = 0; u < kCombUnroll; ++u) merge_into(m, num, den, mv[u], ov[u], lv[u]);
+    for (int k = 0; k < 8; ++k) merge_into(m, num, den, mv[k], ov[k], lv[k]);
   }
-  red[part][0][dl] = m;
-  red[part][1][dl] = num;
-  red[part][2][dl] = den;
-  __syncthreads();
-  if (part == 0) {
 #pragma unroll
-    for (int p = 1; p < kCombParts; ++p) merge_into(m, num, den, red[p][0][dl], red[p][1][dl], red[p][2][dl]);
-    const float o = num / den;
-    const int64_t oi = b * out_stride_b + (int64_t)hq * D + d;
-    if (out_f32) out_f32[oi] = o;
-    if (out_bf16) out_bf16[oi] = bf16_rne(o);
+  for (int x = 16; x < 64; x <<= 1) {
+    f4c no;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) no[i] = __shfl_xor(num[i], x, 64);
+    merge_into(m, num, den, __shfl_xor(m, x, 64), no, __shfl_xor(den, x, 64));
+  }
+  if (sub == 0) {
+    red[w][dq][0] = m;
+    red[w][dq][1] = den;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[w][dq][2 + i] = num[i];
+  }
+  __syncthreads();
+  if (w == 0 && sub == 0) {
+#pragma unroll
+    for (int v = 1; v < 4; ++v) {
+      const f4c no = {red[v][dq][2], red[v][dq][3], red[v][dq][4], red[v][dq][5]};
+      merge_into(m, num, den, red[v][dq][0], no, red[v][dq][1]);
+    }
+    const int64_t oi = b * out_stride_b + (int64_t)hq * D + d0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float o = num[i] / den;
+      if (out_f32) out_f32[oi + i] = o;
+      if (out_bf16) out_bf16[oi + i] = bf16_rne(o);
+    }
   }
 }
 
@@ -284,7 +305,7 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
                        int64_t out_stride_b, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % kCombDims != 0) return KVT_EINVAL;
   hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch),
-                     dim3(kCombDims * kCombParts), 0,
+                     dim3(256), 0,
                      (hipStream_t)stream,
                      (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
                      (const int32_t*)seq_lens, (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16,
