@@ -7,6 +7,8 @@ Every .hip file under csrc/ is compiled to an object with hipcc (in parallel), t
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                               no packed fp32 VALU instructions
   no -ffast-math: rounding must follow IEEE round-to-nearest-even.
+Per file: decode_mfma.hip preloads its first 16 kernel-argument dwords into SGPRs
+(-mllvm -amdgpu-kernarg-preload-count=16; the arguments its start-up chain needs come first).
 """
 from __future__ import annotations
 
@@ -38,13 +40,18 @@ CFLAGS = [
 ]
 
 
+EXTRA_CFLAGS = {
+    "decode_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA_CFLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

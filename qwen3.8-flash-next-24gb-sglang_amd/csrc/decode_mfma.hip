@@ -950,10 +950,15 @@ KVT_DEV void merge_head(const float* part_o, const float* part_ml, int64_t sbase
 
 template <int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
-decode_mfma_kernel(PosArgs A, const uint16_t* q, int64_t q_stride_b, const int32_t* seq_lens, int H, int gs,
-                   int n_splits, const int32_t* split_map, float scale, float* part_o, float* part_ml,
-                   uint32_t pool_rows, int flags, int32_t* counters, int kmerge, float* out_f32,
+decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64_t* ring_start,
+                   const int32_t* page_table, int64_t pt_stride, const int32_t* split_map, int H, int n_splits,
+                   int gs, int flags, const uint16_t* q, int64_t q_stride_b, const int64_t* ring_base,
+                   const uint8_t* k4, const uint8_t* v4, const uint16_t* ks4, const uint16_t* vs4, const int8_t* rk,
+                   const int8_t* rv, const uint16_t* rks, const uint16_t* rvs, float scale, float* part_o,
+                   float* part_ml, uint32_t pool_rows, int32_t* counters, int kmerge, float* out_f32,
                    uint16_t* out_bf16, int64_t out_stride_b) {
+  // (the arguments the start-up chain needs come first: the first 16 dwords are preloaded into SGPRs)
+  const PosArgs A{k4, v4, ks4, vs4, rk, rv, rks, rvs, ring_base, ring_len, ring_start, page_table, pt_stride};
   __shared__ __align__(128) Lds lds;
   const bool dyn = (flags & KVT_DECODE_DYNAMIC) != 0;
   const int lane = threadIdx.x & 63;
@@ -1164,25 +1169,20 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
       hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return KVT_ELAUNCH;
   const int kmerge = max(1, min(kMergers, cu_count[dev] / 2));
-  PosArgs A{(const uint8_t*)k4,         (const uint8_t*)v4,        (const uint16_t*)ks4,     (const uint16_t*)vs4,
-            (const int8_t*)rk,          (const int8_t*)rv,         (const uint16_t*)rks,     (const uint16_t*)rvs,
-            (const int64_t*)ring_base,  (const int32_t*)ring_len,  (const int64_t*)ring_start,
-            (const int32_t*)page_table, pt_stride};
+#define KVT_DECODE_ARGS                                                                                          \
+  (const int32_t*)seq_lens, (const int32_t*)ring_len, (const int64_t*)ring_start, (const int32_t*)page_table,       \
+      pt_stride, (const int32_t*)split_map, H, n_splits, gs, flags, (const uint16_t*)q, q_stride_b,                \
+      (const int64_t*)ring_base, (const uint8_t*)k4, (const uint8_t*)v4, (const uint16_t*)ks4, (const uint16_t*)vs4, \
+      (const int8_t*)rk, (const int8_t*)rv, (const uint16_t*)rks, (const uint16_t*)rvs, scale, (float*)part_o,     \
+      (float*)part_ml, (uint32_t)pool_rows, (int32_t*)counters, kmerge, (float*)out_f32, (uint16_t*)out_bf16,      \
+      out_stride_b
   const dim3 grid = split_map != nullptr ? dim3((unsigned)n_map, (unsigned)H)
                                          : dim3((unsigned)n_splits, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
   if (group8 == 64) {
-    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
-                       (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
-                       (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows, flags, (int32_t*)counters, kmerge, (float*)out_f32,
-                       (uint16_t*)out_bf16, out_stride_b);
+    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else if (group8 == 256) {
-    hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(64 * kWaves), 0, st, A, (const uint16_t*)q, q_stride_b,
-                       (const int32_t*)seq_lens, H, gs, n_splits, (const int32_t*)split_map, scale,
-                       (float*)part_o, (float*)part_ml,
-                       (uint32_t)pool_rows, flags, (int32_t*)counters, kmerge, (float*)out_f32,
-                       (uint16_t*)out_bf16, out_stride_b);
+    hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else {
     return KVT_EINVAL;
   }
