@@ -205,27 +205,36 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int dq = lane & 15, sub = lane >> 4;
   const int d0 = blockIdx.x * kCombDims + 4 * dq;
-  const int64_t L = seq_lens[b];
-  // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
-  // split_counts (chunk 0): sequence b uses the first split_counts[b] slots
-  const int used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
-                             : (split_counts != nullptr ? split_counts[b] : n_chunks);
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
   float m = -INFINITY, den = 0.0f;
   f4c num = {0.f, 0.f, 0.f, 0.f};
-  for (int r0 = 0; r0 < used; r0 += kCombRound) {
+  // the loads of a round index the n_chunks slots only: the first round's go out before the sequence length (which
+  // bounds the splits in use) has arrived; splits beyond it are dropped at the merge
+  int used = 0;
+  for (int r0 = 0; r0 < n_chunks; r0 += kCombRound) {
     f4c ov[8];
     float mv[8], lv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int c = r0 + 16 * k + 4 * sub + w;
-      const int64_t it = (base + (c < used ? c : 0)) * gs + j;
+      const int64_t it = (base + (c < n_chunks ? c : 0)) * gs + j;
       ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
-      mv[k] = c < used ? part_ml[it * 2] : -INFINITY;
+      mv[k] = part_ml[it * 2];
       lv[k] = part_ml[it * 2 + 1];
     }
+    if (r0 == 0) {
+      // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
+      // split_counts (chunk 0): sequence b uses the first split_counts[b] slots
+      const int64_t L = seq_lens[b];
+      used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
+                       : (split_counts != nullptr ? split_counts[b] : n_chunks);
+    }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) merge_into(m, num, den, mv[k], ov[k], lv[k]);
+    for (int k = 0; k < 8; ++k) {   // (slots beyond `used` may hold anything, NaN included: select, not scale)
+      const int c = r0 + 16 * k + 4 * sub + w;
+      if (c < used) merge_into(m, num, den, mv[k], ov[k], lv[k]);
+    }
+    if (r0 + kCombRound >= used) break;
   }
 #pragma unroll
   for (int x = 16; x < 64; x <<= 1) {

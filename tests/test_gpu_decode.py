@@ -129,6 +129,25 @@ def test_decode_fused_merge_ragged(kvt_pkg):
     assert float((fused2 - sep2).abs().max()) < 2e-4
 
 
+def test_combine_ignores_unused_slots(kvt_pkg):
+    """Partial slots beyond the splits a sequence uses may hold anything (here NaN, left in a reused workspace): the
+    combine kernel loads them with the others but must not let them into the sum (reference-precision path with
+    more chunks than the context needs, and the MFMA path with a ragged split map)."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([3000, 700], [1024, 512], seed=41)
+    qd = q.to(dev)
+    exp = _oracle_out(oc, q)
+    for kw in (dict(impl="ref", chunk=256, max_len=20000), dict(impl="mfma", deterministic=True)):
+        ws = {}
+        kvt_decode_attn(dc, 0, qd, workspace=ws, **kw)
+        ws["part_o"].fill_(float("nan"))
+        ws["part_ml"].fill_(float("nan"))
+        out = kvt_decode_attn(dc, 0, qd, workspace=ws, **kw).cpu()
+        assert not bool(torch.isnan(out).any()), kw
+        err = (out - exp).abs()
+        assert float(err.max()) < 2e-3, (kw, float(err.max()))
+
+
 def test_decode_mfma_page_windows(kvt_pkg):
     """One split over 40,000 positions: each wavefront walks about 9,000 paged positions, i.e. several 64-page
     windows of page ids."""
