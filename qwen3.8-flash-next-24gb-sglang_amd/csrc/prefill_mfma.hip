@@ -63,8 +63,8 @@ struct KVSrc {
 };
 
 struct __align__(16) Lds {
-  uint8_t k[kT * kKPitch];
-  uint8_t vt[kD * kVPitch];
+  uint8_t k[2][kT * kKPitch];    // double-buffered: tile i + 1 is dequantized while tile i is in use
+  uint8_t vt[2][kD * kVPitch];
   int32_t pages[kMaxLdsPages];
 };
 
@@ -91,8 +91,8 @@ KVT_DEV uint32_t ld16(Rsrc r, uint32_t off) { return (uint32_t)__builtin_amdgcn_
 // stay in flight across the matrix work of the current one.
 struct Tier {
   Rsrc k4, v4, ks4, vs4, rk, rv, rks, rvs, kb, vb;
-  int64_t hs, rmask, key_end;
-  int64_t kb_n, kb_h, vb_n, vb_h;
+  int hs, rmask, key_end;   // positions (< 2^31: the entry point bounds the context)
+  int kb_n, kb_h, vb_n, vb_h;
   int H, h;
 };
 
@@ -111,11 +111,11 @@ struct RawV {
 };
 
 template <int G8, bool BF16>
-KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int64_t p, int dc) {
+KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int p, int dc) {
   RawK x;
   p = min(p, T.key_end - 1);   // keys past the end: valid rows, masked in the scores
   if constexpr (BF16) {
-    const uint32_t off = (uint32_t)((p * T.kb_n + (int64_t)T.h * T.kb_h + 32 * dc) * 2);
+    const uint32_t off = (uint32_t)(p * T.kb_n + T.h * T.kb_h + 32 * dc) * 2u;
     x.a = ld128(T.kb, off);
     x.b = ld128(T.kb, off + 16);
     x.c = ld128(T.kb, off + 32);
@@ -124,9 +124,9 @@ KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int64_t p, int dc) {
   } else {
     constexpr int NG8 = kD / G8;
     const bool hot = p >= T.hs;
-    const int64_t pg = hot ? 0 : min(p >> 6, (int64_t)kMaxLdsPages - 1);
-    const uint32_t rh4 = (uint32_t)(((int64_t)lpages[pg] * kPage + (p & (kPage - 1))) * T.H + T.h);
-    const uint32_t rh8 = (uint32_t)((p & T.rmask) * T.H + T.h);
+    const int pg = hot ? 0 : min(p >> 6, kMaxLdsPages - 1);
+    const uint32_t rh4 = ((uint32_t)lpages[pg] * kPage + (uint32_t)(p & (kPage - 1))) * T.H + T.h;
+    const uint32_t rh8 = (uint32_t)(p & T.rmask) * T.H + T.h;
     x.a = ld128(T.k4, hot ? kOOB : rh4 * 128u + 16u * dc);
     x.s4 = ld16(T.ks4, hot ? kOOB : (rh4 * 8u + dc) * 2u);
     x.b = ld128(T.rk, hot ? rh8 * 256u + 32u * dc : kOOB);
@@ -138,22 +138,22 @@ KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int64_t p, int dc) {
 }
 
 template <int G8, bool BF16>
-KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int64_t p0, int db) {
+KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   RawV x;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int64_t p = min(p0 + t, T.key_end - 1);
+    const int p = min(p0 + t, T.key_end - 1);
     if constexpr (BF16) {
-      const uint32_t off = (uint32_t)((p * T.vb_n + (int64_t)T.h * T.vb_h + 16 * db) * 2);
+      const uint32_t off = (uint32_t)(p * T.vb_n + T.h * T.vb_h + 16 * db) * 2u;
       x.a[t] = ld128(T.vb, off);
       x.bb[t] = ld128(T.vb, off + 16);
       x.hot[t] = 2;
     } else {
       constexpr int NG8 = kD / G8;
       const bool hot = p >= T.hs;
-      const int64_t pg = hot ? 0 : min(p >> 6, (int64_t)kMaxLdsPages - 1);
-      const uint32_t rh4 = (uint32_t)(((int64_t)lpages[pg] * kPage + (p & (kPage - 1))) * T.H + T.h);
-      const uint32_t rh8 = (uint32_t)((p & T.rmask) * T.H + T.h);
+      const int pg = hot ? 0 : min(p >> 6, kMaxLdsPages - 1);
+      const uint32_t rh4 = ((uint32_t)lpages[pg] * kPage + (uint32_t)(p & (kPage - 1))) * T.H + T.h;
+      const uint32_t rh8 = (uint32_t)(p & T.rmask) * T.H + T.h;
       x.c4[t] = ld64(T.v4, hot ? kOOB : rh4 * 128u + 8u * db);
       x.s4[t] = ld16(T.vs4, hot ? kOOB : (rh4 * 8u + db / 2) * 2u);
       x.a[t] = ld128(T.rv, hot ? rh8 * 256u + 16u * db : kOOB);
@@ -246,8 +246,10 @@ KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   }
 }
 
+constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 2 queries x 8 heads = 16 rows
+
 template <int G8, bool BF16>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                     const int32_t* kv_lens, int H, int gs, int n_qtiles, float scale, void* out, int out_f32,
                     int64_t so_n, int64_t so_h) {
@@ -273,11 +275,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   Tier T;
   T.H = H;
   T.h = h;
-  T.key_end = key_end;
-  T.kb_n = S.kb_n;
-  T.kb_h = S.kb_h;
-  T.vb_n = S.vb_n;
-  T.vb_h = S.vb_h;
+  T.key_end = (int)key_end;
+  T.kb_n = (int)S.kb_n;
+  T.kb_h = (int)S.kb_h;
+  T.vb_n = (int)S.vb_n;
+  T.vb_h = (int)S.vb_h;
   if constexpr (BF16) {
     const uint32_t kbytes = (uint32_t)(((S.kb_rows - 1) * S.kb_n + (int64_t)(H - 1) * S.kb_h + kD) * 2);
     const uint32_t vbytes = (uint32_t)(((S.kb_rows - 1) * S.vb_n + (int64_t)(H - 1) * S.vb_h + kD) * 2);
@@ -288,8 +290,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   } else {
     const int64_t R = S.ring_len[b];
     const int64_t rbase = S.ring_base[b];
-    T.hs = min(max(max(S.ring_start[b], L - R), (int64_t)0), L);
-    T.rmask = R - 1;
+    T.hs = (int)min(max(max(S.ring_start[b], L - R), (int64_t)0), L);
+    T.rmask = (int)(R - 1);
     T.k4 = make_rsrc(S.k4, S.pool_rows * (uint32_t)H * 128u);
     T.v4 = make_rsrc(S.v4, S.pool_rows * (uint32_t)H * 128u);
     T.ks4 = make_rsrc(S.ks4, S.pool_rows * (uint32_t)H * 16u);
@@ -299,134 +301,152 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     T.rks = make_rsrc(S.rks + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
     T.rvs = make_rsrc(S.rvs + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
     // page ids of the paged key range, once per block
-    const int64_t npg = min((min(T.hs, key_end) + kPage - 1) / kPage, (int64_t)kMaxLdsPages);
-    for (int64_t i = tid; i < npg; i += 256) lds.pages[i] = S.page_table[b * S.pt_stride + i];
+    const int64_t npg = min((min((int64_t)T.hs, key_end) + kPage - 1) / kPage, (int64_t)kMaxLdsPages);
+    for (int64_t i = tid; i < npg; i += 64 * kWaves) lds.pages[i] = S.page_table[b * S.pt_stride + i];
     if (tid == 0 && npg == 0) lds.pages[0] = 0;
   }
   __syncthreads();
 
-  // ---- Q operands: rows j of block rb = query qt0 + 4 wave + 2 rb + (j >> 3), head j & 7
-  h8 qop[2][8];
-  int64_t qpos[2];   // position of this lane's query row (as the S^T column), per row block
-  const float qmul = scale * kLog2e;
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int64_t qi = qt0 + 4 * wave + 2 * rb + (n16 >> 3);
+  // ---- Q operands: row j of the wavefront's 16 = query qt0 + 2 wave + (j >> 3), head j & 7
+  h8 qop[8];
+  int64_t qpos;   // position of this lane's query row (as the S^T column)
+  {
+    const float qmul = scale * kLog2e;
+    const int64_t qi = qt0 + 2 * wave + (n16 >> 3);
     const int hq = n16 & 7;
     const bool ok = qi < q_len && hq < gs;
-    qpos[rb] = q_pos0 + qi;
+    qpos = q_pos0 + qi;
     const uint16_t* qr = q + (qs + (ok ? qi : 0)) * sq_n + (int64_t)(h * gs + (ok ? hq : 0)) * sq_h;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int st = 0; st < 8; ++st) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = bf16_to_f32(qr[32 * s + 8 * kb + e]) * qmul;
-        qop[rb][s][e] = (_Float16)(ok ? x : 0.0f);
+        const float x = bf16_to_f32(qr[32 * st + 8 * kb + e]) * qmul;
+        qop[st][e] = (_Float16)(ok ? x : 0.0f);
       }
     }
   }
 
-  f4 acc[2][16];
+  f4 acc[16];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int c = 0; c < 16; ++c) acc[rb][c] = f4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  for (int c = 0; c < 16; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
 
-  // dequant roles: K row tk = tid >> 3, channels 32 (tid & 7) ..; V keys 2 tp, 2 tp + 1 (tp = tid & 15),
-  // channels 16 db .. (db = tid >> 4)
-  const int tk = tid >> 3, dc = tid & 7;
-  const int tp = tid & 15, db = tid >> 4;
+  // dequant roles: threads 0-255 the K tile (row tk = t >> 3, channels 32 (t & 7) ..), threads 256-511 the V tile
+  // (keys 2 tp, 2 tp + 1 with tp = t & 15, channels 16 db .. with db = t >> 4), t = tid mod 256
+  const bool krole = tid < 256;
+  const int t8 = tid & 255;
+  const int tk = t8 >> 3, dc = t8 & 7;
+  const int tp = t8 & 15, db = t8 >> 4;
   const int ntiles = (int)((key_end + kT - 1) / kT);
-  RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
+  RawK rk_next;
+  RawV rv_next;
+  if (krole) {
+    rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
+    store_k(rk_next, lds.k[0] + tk * kKPitch + 64 * dc);
+    if (ntiles > 1) rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
+  } else {
+    rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
+    store_v(rv_next, lds.vt[0], db, tp);
+    if (ntiles > 1) rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
+  }
+  __syncthreads();
+  const int qmin = (int)(q_pos0 + qt0);   // the block's first query position: tiles below it need no causal mask
+  const int qp = (int)qpos, kend = (int)key_end;
   for (int it = 0; it < ntiles; ++it) {
-    const int64_t t0 = (int64_t)it * kT;
-    __syncthreads();   // the previous tile's fragments are consumed
-    store_k(rk_next, lds.k + tk * kKPitch + 64 * dc);
-    store_v(rv_next, lds.vt, db, tp);
-    __syncthreads();
-    if (it + 1 < ntiles) {   // next tile's codes travel during this tile's matrix work
-      const int64_t t1 = t0 + kT;
-      rk_next = fetch_k<G8, BF16>(T, lds.pages, t1 + tk, dc);
-      rv_next = fetch_v<G8, BF16>(T, lds.pages, t1 + 2 * tp, db);
-    }
+    const int t0 = it * kT;
+    const int cb = it & 1;
     // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16
-    float s[2][2][4];
+    float s[2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      f4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* krow = lds.k + (16 * nt + n16) * kKPitch + 16 * kb;
+      f4 d0 = {0.f, 0.f, 0.f, 0.f};
+      const uint8_t* krow = lds.k[cb] + (16 * nt + n16) * kKPitch + 16 * kb;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
         const h8 a = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(krow + 64 * st));
-        d0 = mfma(a, qop[0][st], d0);
-        d1 = mfma(a, qop[1][st], d1);
+        d0 = mfma(a, qop[st], d0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t kp = t0 + 16 * nt + 4 * kb + r;
-        s[0][nt][r] = (kp <= qpos[0] && kp < key_end) ? d0[r] : -INFINITY;
-        s[1][nt][r] = (kp <= qpos[1] && kp < key_end) ? d1[r] : -INFINITY;
+      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r];
+    }
+    // ---- tile it + 1 into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go
+    // out: the dequantization's VALU work overlaps this tile's matrix work
+    if (it + 1 < ntiles) {
+      const int t2 = t0 + 2 * kT;
+      if (krole) {
+        store_k(rk_next, lds.k[cb ^ 1] + tk * kKPitch + 64 * dc);
+        if (it + 2 < ntiles) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
+      } else {
+        store_v(rv_next, lds.vt[cb ^ 1], db, tp);
+        if (it + 2 < ntiles) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
       }
     }
-    // ---- online softmax per row block; P as the A operand of P.V
-    h8 pa[2];
+    // causal / end mask, only on the tiles that reach the block's first query or the key end
+    if (t0 + kT > qmin || t0 + kT > kend) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kp = t0 + 16 * nt + 4 * kb + r;
+          s[nt][r] = (kp <= qp && kp < kend) ? s[nt][r] : -INFINITY;
+        }
+    }
+    // ---- online softmax; P as the A operand of P.V
+    h8 pa;
+    {
       float mloc = -INFINITY;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[rb][nt][r]);
+        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[nt][r]);
       mloc = max_xor16_32(mloc);
       // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
       // by more than 8 (log2 units), so P = 2^(s - m) <= 256 stays well inside fp16
-      const float m_new = fmaxf(m_run[rb], mloc);
-      if (__any(m_new > m_run[rb] + 8.0f)) {
-        const float alpha = m_run[rb] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[rb] - m_new);
-        l_run[rb] *= alpha;
+      const float m_new = fmaxf(m_run, mloc);
+      if (__any(m_new > m_run + 8.0f)) {
+        const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
         float arow[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);
 #pragma unroll
         for (int c = 0; c < 16; ++c)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) acc[rb][c][i] *= arow[i];
-        m_run[rb] = m_new;
+          for (int i = 0; i < 4; ++i) acc[c][i] *= arow[i];
+        m_run = m_new;
       }
       // rows with no visible key yet keep m = -inf and contribute nothing
-      const float m_use = m_run[rb] == -INFINITY ? 0.f : m_run[rb];
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
       float psum = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s[rb][nt][r] = __builtin_amdgcn_exp2f(s[rb][nt][r] - m_use);
-          psum += s[rb][nt][r];
+          s[nt][r] = __builtin_amdgcn_exp2f(s[nt][r] - m_use);
+          psum += s[nt][r];
         }
-      l_run[rb] += psum;
-      pa[rb] = h8{(_Float16)s[rb][0][0], (_Float16)s[rb][0][1], (_Float16)s[rb][0][2], (_Float16)s[rb][0][3],
-                  (_Float16)s[rb][1][0], (_Float16)s[rb][1][1], (_Float16)s[rb][1][2], (_Float16)s[rb][1][3]};
+      l_run += psum;
+      pa = h8{(_Float16)s[0][0], (_Float16)s[0][1], (_Float16)s[0][2], (_Float16)s[0][3],
+              (_Float16)s[1][0], (_Float16)s[1][1], (_Float16)s[1][2], (_Float16)s[1][3]};
     }
     // ---- O += P V: B = V^T row (dim 16 c + n16), keys {4 kb .. +3, 16 + 4 kb .. +3}
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const uint8_t* vrow = lds.vt + (16 * c + n16) * kVPitch + 8 * kb;
+      const uint8_t* vrow = lds.vt[cb] + (16 * c + n16) * kVPitch + 8 * kb;
       const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
       const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 32);
       const h8 bv = __builtin_bit_cast(h8, u4v{lo.x, lo.y, hi.x, hi.y});
-      acc[0][c] = mfma(pa[0], bv, acc[0][c]);
-      acc[1][c] = mfma(pa[1], bv, acc[1][c]);
+      acc[c] = mfma(pa, bv, acc[c]);
     }
+    __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
   }
 
-  // ---- normalize and store: accumulator row 4 kb + i of block rb = query qt0 + 4 wave + 2 rb + (kb >> 1),
-  // head 4 (kb & 1) + i; column n16 of block c = dim 16 c + n16
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const float l = sum_xor16_32(l_run[rb]);
-    const int64_t qi = qt0 + 4 * wave + 2 * rb + (kb >> 1);
+  // ---- normalize and store: accumulator row 4 kb + i = query qt0 + 2 wave + (kb >> 1), head 4 (kb & 1) + i;
+  // column n16 of block c = dim 16 c + n16
+  {
+    const float l = sum_xor16_32(l_run);
+    const int64_t qi = qt0 + 2 * wave + (kb >> 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float lr = __shfl(l, 4 * kb + i, 64);
@@ -436,11 +456,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         if (out_f32) {
           float* orow = reinterpret_cast<float*>(out) + o0;
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[rb][c][i] / lr;
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[c][i] / lr;
         } else {
           uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[rb][c][i] / lr);
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[c][i] / lr);
         }
       }
     }
@@ -477,7 +497,7 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
   const dim3 grid((unsigned)n_qtiles, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
 #define KVT_PF(G, B)                                                                                              \
-  hipLaunchKernelGGL((prefill_mfma_kernel<G, B>), grid, dim3(256), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,  \
+  hipLaunchKernelGGL((prefill_mfma_kernel<G, B>), grid, dim3(64 * kWaves), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,  \
                      cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n, so_h)
   if (bf16) {
     KVT_PF(64, true);
