@@ -32,8 +32,15 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 constexpr int kD = 256;
 constexpr int kQT = 16;                 // queries per block
 constexpr int kT = 32;                  // key positions per tile
-constexpr int kKPitch = kD * 2 + 16;    // bytes per fp16 K row in LDS (padded: spreads the 16 rows over the banks)
-constexpr int kVPitch = kT * 2 + 16;    // bytes per fp16 V^T row (one dim, 32 keys)
+// LDS tiles, XOR-swizzled so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
+//   K: fp16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
+//      4 st + kb of 16 consecutive keys: 16 distinct chunks mod 16, i.e. all 64 banks.
+//   V^T: fp16 row per dim (64 B = 32 keys); its 8-byte chunk j (keys 4 j .. 4 j + 3) lives at chunk
+//      j ^ ((dim >> 2) & 7).  A B-operand read takes chunk j of 16 consecutive dims: (dim & 3, chunk) distinct.
+constexpr int kKPitch = kD * 2;         // bytes per fp16 K row
+constexpr int kVPitch = kT * 2;         // bytes per fp16 V^T row
+KVT_DEV uint32_t k_chunk(int key, int c) { return 16u * (uint32_t)(c ^ (key & 15)); }
+KVT_DEV uint32_t vt_chunk(int dim, int j) { return 8u * (uint32_t)(j ^ ((dim >> 2) & 7)); }
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -194,8 +201,8 @@ KVT_DEV uint32_t bf16x2_to_f16x2(uint32_t w) {
 
 KVT_DEV h2 splat(uint32_t s) { return as_h2((s & 0xffffu) | ((s & 0xffffu) << 16)); }
 
-// K row fragment -> LDS (fp16, natural order): 32 channels = 64 bytes.
-KVT_DEV void store_k(const RawK& x, uint8_t* dst) {
+// K row fragment -> LDS (fp16, natural order): channels 32 dc .. 32 dc + 31 of key row `key` (4 chunks).
+KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
   uint32_t o[16];
   if (x.hot == 2) {
     const uint32_t w[16] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w,
@@ -213,7 +220,8 @@ KVT_DEV void store_k(const RawK& x, uint8_t* dst) {
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<uint4*>(dst + 16 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    *reinterpret_cast<uint4*>(row + k_chunk(key, 4 * dc + i)) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2],
+                                                                          o[4 * i + 3]);
 }
 
 // 16 channels of one V row -> 8 fp16 pairs (natural order).
@@ -241,8 +249,9 @@ KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   for (int i = 0; i < 8; ++i) {
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
     const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
-    *reinterpret_cast<uint32_t*>(vt + (16 * db + 2 * i) * kVPitch + 4 * tp) = lo;
-    *reinterpret_cast<uint32_t*>(vt + (16 * db + 2 * i + 1) * kVPitch + 4 * tp) = hi;
+    const int d0 = 16 * db + 2 * i, d1 = d0 + 1;   // keys 2 tp, 2 tp + 1: chunk tp >> 1, dword tp & 1
+    *reinterpret_cast<uint32_t*>(vt + d0 * kVPitch + vt_chunk(d0, tp >> 1) + 4 * (tp & 1)) = lo;
+    *reinterpret_cast<uint32_t*>(vt + d1 * kVPitch + vt_chunk(d1, tp >> 1) + 4 * (tp & 1)) = hi;
   }
 }
 
@@ -343,7 +352,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   RawV rv_next;
   if (krole) {
     rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-    store_k(rk_next, lds.k[0] + tk * kKPitch + 64 * dc);
+    store_k(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
     if (ntiles > 1) rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
   } else {
     rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
@@ -361,10 +370,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       f4 d0 = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* krow = lds.k[cb] + (16 * nt + n16) * kKPitch + 16 * kb;
+      const uint8_t* krow = lds.k[cb] + (16 * nt + n16) * kKPitch;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const h8 a = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(krow + 64 * st));
+        const h8 a = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(krow + k_chunk(n16, 4 * st + kb)));
         d0 = mfma(a, qop[st], d0);
       }
 #pragma unroll
@@ -375,7 +384,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     if (it + 1 < ntiles) {
       const int t2 = t0 + 2 * kT;
       if (krole) {
-        store_k(rk_next, lds.k[cb ^ 1] + tk * kKPitch + 64 * dc);
+        store_k(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
         if (it + 2 < ntiles) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
       } else {
         store_v(rv_next, lds.vt[cb ^ 1], db, tp);
@@ -433,9 +442,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     // ---- O += P V: B = V^T row (dim 16 c + n16), keys {4 kb .. +3, 16 + 4 kb .. +3}
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const uint8_t* vrow = lds.vt[cb] + (16 * c + n16) * kVPitch + 8 * kb;
-      const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 32);
+      const int dim = 16 * c + n16;
+      const uint8_t* vrow = lds.vt[cb] + dim * kVPitch;
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + vt_chunk(dim, kb));
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + vt_chunk(dim, 4 + kb));
       const h8 bv = __builtin_bit_cast(h8, u4v{lo.x, lo.y, hi.x, hi.y});
       acc[c] = mfma(pa, bv, acc[c]);
     }
