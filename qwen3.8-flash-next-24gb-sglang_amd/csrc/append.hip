@@ -3,6 +3,9 @@
 // One wavefront (64 lanes) owns one (token, KV head) row; lane l holds channels 4l..4l+3, so a 32-channel INT4
 // group is 8 lanes and a 64-channel INT8 group is 16 lanes: the group absmax is a lane butterfly inside the wave
 // and every load/store is a contiguous per-lane chunk (row-coalesced).  Four rows per 256-thread block.
+// The arithmetic is the reference's bit for bit (IEEE quotients, round-half-even, fp16 scales) but avoids the
+// division on the common path: scales from a * fl(1/qmax) and codes from x * rcp(s), each checked against the
+// rounding ties it could get wrong, with the IEEE division for the lanes that are close to one.
 //
 //   kvt_quant_store_tiered  dual write (patches/kv_tiers.py:272-443): owner stamp launch, then the INT8 ring row
 //                           (owner only) + INT4 pool row (always) launch.
@@ -19,7 +22,12 @@ using namespace kvt;
 
 namespace {
 
-constexpr int kRowsPerBlock = 4;
+constexpr int kWavesPerBlock = 4;
+// (token, head) rows per wavefront.  One row per wave gives twice as many waves as fit at once on the chip for
+// an 8192-token append, so later waves' loads overlap earlier waves' quantization (2 and 4 rows per wave, with
+// every load issued up front, measured slower).
+constexpr int kRowsPerWave = 1;
+constexpr int kRowsPerBlock = kWavesPerBlock * kRowsPerWave;
 
 struct RowIn {
   const void* base;
@@ -27,44 +35,175 @@ struct RowIn {
   int64_t stride_h;  // elements
 };
 
-template <int DT>
+// Raw buffer over [p, p + bytes): a load outside it returns zero without a memory access, so a row that is not
+// needed costs no traffic and no branch.
+KVT_DEV __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// How a kernel reads its 4 input channels per lane (chosen by the launcher):
+//   kLoadElem   element loads, smoothing inverse optional at run time (any strides);
+//   kLoadVec    one 8-byte (16-bit types) or 16-byte (fp32) load, no smoothing inverse;
+//   kLoadVecSm  the same plus one 8-byte load of the 4 smoothing values.
+// The vector forms need the base and both strides to keep every 4-channel chunk aligned.
+enum LoadMode : int { kLoadElem = 0, kLoadVec = 1, kLoadVecSm = 2 };
+
+// The 4 input channels c0..c0+3 of row (t, h) as fp32, times the smoothing inverse when one is given:
+// x = f32(k) * f32(sm_inv) (patches/kv_tiers.py:332-333).
+template <int DT, int LM>
 KVT_DEV void load4(const RowIn& in, int64_t t, int h, int c0, const uint16_t* sm_inv, int D, float x[4]) {
   const int64_t off = t * in.stride_n + (int64_t)h * in.stride_h + c0;
+  if constexpr (LM == kLoadElem) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = load_in<DT>(in.base, off + i);
+      x[i] = sm_inv ? v * f16_bits_to_f32(sm_inv[h * D + c0 + i]) : v;
+    }
+  } else {
+    if constexpr (DT == kF32) {
+      const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(in.base) + off);
+      x[0] = v.x;
+      x[1] = v.y;
+      x[2] = v.z;
+      x[3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(in.base) + off);
+      const uint16_t e[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = DT == kBF16 ? bf16_to_f32(e[i]) : f16_bits_to_f32(e[i]);
+    }
+    if constexpr (LM == kLoadVecSm) {
+      const uint2 m = *reinterpret_cast<const uint2*>(sm_inv + h * D + c0);
+      x[0] *= f16_bits_to_f32((uint16_t)m.x);
+      x[1] *= f16_bits_to_f32((uint16_t)(m.x >> 16));
+      x[2] *= f16_bits_to_f32((uint16_t)m.y);
+      x[3] *= f16_bits_to_f32((uint16_t)(m.y >> 16));
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------- lane quantizers
+// The group absmax works on |x| bit patterns: for non-negative floats the unsigned order of the patterns is the
+// float order, and a NaN sorts above +inf, so a NaN in a group reaches its absmax (as with torch's amax) and the
+// scale falls back to 1 (a > 0 is false for NaN).
+KVT_DEV uint32_t absmax4_bits(const float x[4]) {
+  const uint32_t m = 0x7fffffffu;
+  return max(max(__float_as_uint(x[0]) & m, __float_as_uint(x[1]) & m),
+             max(__float_as_uint(x[2]) & m, __float_as_uint(x[3]) & m));
+}
+
+template <int CTRL>
+KVT_DEV uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
+}
+
+// Max over aligned groups of `width` lanes.  Inside a 16-lane row DPP does it: quad_perm [1,0,3,2] and [2,3,0,1]
+// reduce each quad, row_half_mirror (lane i <- 7 - i) joins the two quads of a half-row and row_mirror
+// (i <- 15 - i) the two half-rows; wider groups finish with LDS permutes.  Every lane of a group must be active.
+template <int width>
+KVT_DEV uint32_t group_max_bits(uint32_t v) {
+  static_assert(width >= 8 && width <= 64 && (width & (width - 1)) == 0, "group width");
+  v = max(v, dpp_u32<0xb1>(v));
+  v = max(v, dpp_u32<0x4e>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  if constexpr (width >= 16) v = max(v, dpp_u32<0x140>(v));
+#pragma unroll
+  for (int o = 16; o < width; o <<= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
+// group_scale(a, QMAX) (fp16 bits) from a * fl(1 / QMAX) where that is safe: the product carries at most ~1.5 ulp
+// of relative error against a / QMAX, so it lies within 2.5 fp32 ulps of fl(a / QMAX), and both round to the same
+// fp16 value when the product is in the normal fp16 range below 32768 (the min with 65504 then does nothing) and
+// its 13 discarded mantissa bits are more than 4 away from the rounding tie 0x1000.  Anything else (zero, tiny,
+// huge, NaN, near a tie) takes the IEEE division.
+template <int QMAX>
+KVT_DEV uint16_t scale_bits(float a) {
+  constexpr float kInv = 1.0f / QMAX;
+  const float z = a * kInv;
+  const uint32_t b = __float_as_uint(z);
+  const bool fast = b - 0x38800000u < 0x47000000u - 0x38800000u && (b & 0x1fffu) - 0x0ffcu > 8u;
+  uint16_t h = f32_to_f16_bits(z);
+  if (!fast) h = group_scale(a, (float)QMAX);
+  return h;
+}
+
+// Codes q_i = clamp(rne(fl(x_i / s)), -QMAX, QMAX) of one lane, returned as floats.  The common path uses
+// y = x * k with k ~ 1 / s (k = rcp(s), or a product of exact factors with it; relative error within a few ulps):
+// after the clamp, |y| <= QMAX < 128 where a few ulps are below 2^-15, so rne(y) equals rne(fl(x / s)) unless y is
+// within 2^-12 of a half-integer; lanes holding such a value redo their four quotients with the IEEE division.
+// Clamping first is exact (the bounds are integers) and leaves clamped values far from any tie.
+template <int QMAX, typename ExactX>
+KVT_DEV void round_codes(const float y_in[4], float s, ExactX exact_x, float q[4]) {
+  float dmax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    float v = load_in<DT>(in.base, off + i);
-    float m = sm_inv ? f16_bits_to_f32(sm_inv[h * D + c0 + i]) : 1.0f;
-    x[i] = v * m;  // x = f32(k) * f32(sm_inv)  (patches/kv_tiers.py:332-333)
+    const float y = __builtin_amdgcn_fmed3f(y_in[i], -(float)QMAX, (float)QMAX);
+    q[i] = rintf(y);
+    dmax = fmaxf(dmax, fabsf(y - q[i]));
   }
+  if (dmax > 0.5f - 0x1p-12f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q[i] = quant_code(exact_x(i), s, (float)QMAX);
+  }
+}
+
+// 4 INT8 codes, little-endian bytes of one dword.
+KVT_DEV uint32_t pack8(const float q[4]) {
+  const uint32_t c0 = (uint32_t)(int)q[0], c1 = (uint32_t)(int)q[1], c2 = (uint32_t)(int)q[2], c3 = (uint32_t)(int)q[3];
+  return __builtin_amdgcn_perm(c1, c0, 0x0c0c0400u) | __builtin_amdgcn_perm(c3, c2, 0x04000c0cu);
+}
+
+// 4 INT4 codes as offset-binary nibbles (low nibble = even channel, patches/kv_int4.py:337-339):
+// sum_i (q_i + 8) 16^i, every partial sum an integer below 2^16 and so exact in fp32.
+KVT_DEV uint32_t pack4(const float q[4]) {
+  const float p = fmaf(q[3], 4096.0f, fmaf(q[2], 256.0f, fmaf(q[1], 16.0f, q[0] + 34952.0f)));
+  return (uint32_t)p;
 }
 
 // INT8-G row part held by this lane: 4 codes packed little-endian, plus the group scale (fp16 bits).
 template <int LANES_PER_GROUP>
-KVT_DEV uint32_t quant8_lane(const float x[4], uint16_t* scale_bits) {
-  float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-  a = group_max<LANES_PER_GROUP>(a);
-  const uint16_t sb = group_scale(a, 127.0f);
+KVT_DEV uint32_t quant8_lane(const float x[4], uint16_t* scale_bits_out) {
+  const float a = __uint_as_float(group_max_bits<LANES_PER_GROUP>(absmax4_bits(x)));
+  const uint16_t sb = scale_bits<127>(a);
   const float s = f16_bits_to_f32(sb);
-  uint32_t packed = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int q = (int)quant_code(x[i], s, 127.0f);
-    packed |= ((uint32_t)(q & 0xff)) << (8 * i);
-  }
-  *scale_bits = sb;
-  return packed;
+  const float r = __builtin_amdgcn_rcpf(s);
+  const float y[4] = {x[0] * r, x[1] * r, x[2] * r, x[3] * r};
+  float q[4];
+  round_codes<127>(y, s, [&](int i) { return x[i]; }, q);
+  *scale_bits_out = sb;
+  return pack8(q);
 }
 
 // INT4-G32 row part held by this lane: 2 bytes (4 nibbles), plus the group scale (fp16 bits).
-KVT_DEV uint32_t quant4_lane(const float x[4], uint16_t* scale_bits) {
-  float a = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-  a = group_max<8>(a);
-  const uint16_t sb = group_scale(a, 7.0f);
+KVT_DEV uint32_t quant4_lane(const float x[4], uint16_t* scale_bits_out) {
+  const float a = __uint_as_float(group_max_bits<8>(absmax4_bits(x)));
+  const uint16_t sb = scale_bits<7>(a);
   const float s = f16_bits_to_f32(sb);
-  const uint32_t b0 = pack_pair(quant_code(x[0], s, 7.0f), quant_code(x[1], s, 7.0f));
-  const uint32_t b1 = pack_pair(quant_code(x[2], s, 7.0f), quant_code(x[3], s, 7.0f));
-  *scale_bits = sb;
-  return b0 | (b1 << 8);
+  const float r = __builtin_amdgcn_rcpf(s);
+  const float y[4] = {x[0] * r, x[1] * r, x[2] * r, x[3] * r};
+  float q[4];
+  round_codes<7>(y, s, [&](int i) { return x[i]; }, q);
+  *scale_bits_out = sb;
+  return pack4(q);
+}
+
+// INT4-G32 requantization of 4 INT8 ring codes with scale s8: x_i = c_i * s8 is exact, so the group absmax is
+// s8 * max|c_i| and y_i = c_i * (s8 * rcp(s4)) stays within a few ulps of x_i / s4.
+KVT_DEV uint32_t requant4_lane(uint32_t codes, uint16_t s8bits, uint16_t* scale_bits_out) {
+  const float s8 = f16_bits_to_f32(s8bits);
+  float c[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c[i] = (float)(int8_t)(codes >> (8 * i));
+  const float a = __uint_as_float(group_max_bits<8>(absmax4_bits(c))) * s8;
+  const uint16_t sb = scale_bits<7>(a);
+  const float s = f16_bits_to_f32(sb);
+  const float k = s8 * __builtin_amdgcn_rcpf(s);
+  const float y[4] = {c[0] * k, c[1] * k, c[2] * k, c[3] * k};
+  float q[4];
+  round_codes<7>(y, s, [&](int i) { return c[i] * s8; }, q);
+  *scale_bits_out = sb;
+  return pack4(q);
 }
 
 template <int D, int G8>
@@ -89,6 +228,51 @@ KVT_DEV int64_t load_loc(const void* loc, int loc64, int64_t t) {
   return loc64 ? reinterpret_cast<const int64_t*>(loc)[t] : (int64_t) reinterpret_cast<const int32_t*>(loc)[t];
 }
 
+// load_loc without a branch on the index width: the high word of an int32 index comes from a load outside the
+// buffer (zero, no access) and is replaced by the sign extension.
+KVT_DEV int64_t load_loc_nb(const void* loc, int loc64, uint32_t t, uint32_t n) {
+  const auto rs = row_rsrc(loc, loc64 ? n * 8u : n * 4u);
+  const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(rs, loc64 ? t * 8u : t * 4u, 0, 0);
+  const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(rs, loc64 ? t * 8u + 4u : 0x80000000u, 0, 0);
+  return loc64 ? (int64_t)(((uint64_t)hi << 32) | lo) : (int64_t)(int32_t)lo;
+}
+
+// (token, head) of the ROWS consecutive rows from item0 (uniform across the wave); rows past NH are clamped onto
+// the last row for their loads and flagged so that they store nothing.  Row indices fit 32 bits (the launchers
+// reject larger N * H).
+template <int ROWS>
+struct RowSet {
+  uint32_t t[ROWS];
+  int h[ROWS];
+  bool ok[ROWS];
+  KVT_DEV RowSet(uint32_t item0, uint32_t NH, int H) {
+#pragma unroll
+    for (int i = 0; i < ROWS; ++i) {
+      ok[i] = item0 + i < NH;
+      const uint32_t item = ok[i] ? item0 + i : NH - 1;
+      t[i] = item / (uint32_t)H;
+      h[i] = (int)(item - t[i] * (uint32_t)H);
+    }
+  }
+};
+
+// First row of this wavefront; lane l < ROWS also gets the token of row first + l (clamped) in *lane_t, so that the
+// per-row metadata loads of the wave are one vector load each.
+KVT_DEV uint32_t wave_rows(int rows, uint32_t NH, int H, int lane, uint32_t* lane_t) {
+  const uint32_t item0 =
+      ((uint32_t)blockIdx.x * kWavesPerBlock + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * rows;
+  uint32_t it = item0 + (uint32_t)(lane < rows ? lane : rows - 1);
+  it = it < NH ? it : NH - 1;
+  *lane_t = it / (uint32_t)H;
+  return item0;
+}
+
+KVT_DEV int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __global__ void __launch_bounds__(256) stamp_owner_kernel(const void* loc, int loc64, int64_t N, int32_t* owner,
                                                           int64_t ring_mask) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -97,85 +281,144 @@ __global__ void __launch_bounds__(256) stamp_owner_kernel(const void* loc, int l
   owner[slot & ring_mask] = (int32_t)slot;  // one winner per contested ring row (patches/kv_tiers.py:272-280)
 }
 
-// MODE 0: tiered dual write; 1: INT8 only (ring buffers are the pool); 2: INT4 only.
-template <int DT, int D, int G8, int MODE>
+// MODE 0: tiered dual write; 1: INT8 only (ring buffers are the pool); 2: INT4 only.  Each wavefront handles
+// kRowsPerWave rows: their slot indices (one per lane) and inputs are loaded first, then (MODE 0) the owner words.
+template <int DT, int D, int G8, int MODE, int LM>
 __global__ void __launch_bounds__(256) quant_store_kernel(
-    RowIn kin, RowIn vin, const void* loc, int loc64, int64_t N, int H, uint8_t* k4, uint8_t* v4, uint16_t* ks4,
+    RowIn kin, RowIn vin, const void* loc, int loc64, uint32_t NH, int H, uint8_t* k4, uint8_t* v4, uint16_t* ks4,
     uint16_t* vs4, int8_t* rk, int8_t* rv, uint16_t* rks, uint16_t* rvs, const int32_t* owner,
     const uint16_t* sm_k_inv, const uint16_t* sm_v_inv, int64_t ring_mask) {
+  constexpr int R = kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (item >= N * H) return;
-  const int64_t t = item / H;
-  const int h = (int)(item - t * H);
-  if (lane >= D / 4) return;
-  const int64_t slot = load_loc(loc, loc64, t);
+  uint32_t lt;
+  const uint32_t item0 = wave_rows(R, NH, H, lane, &lt);
+  if (item0 >= NH || lane >= D / 4) return;
+  const int64_t lslot = load_loc_nb(loc, loc64, lt, NH / (uint32_t)H);
+  const RowSet<R> rs(item0, NH, H);
   const int c0 = 4 * lane;
-  float xk[4], xv[4];
-  load4<DT>(kin, t, h, c0, sm_k_inv, D, xk);
-  load4<DT>(vin, t, h, c0, sm_v_inv, D, xv);
+  float xk[R][4], xv[R][4];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    load4<DT, LM>(kin, rs.t[i], rs.h[i], c0, sm_k_inv, D, xk[i]);
+    load4<DT, LM>(vin, rs.t[i], rs.h[i], c0, sm_v_inv, D, xv[i]);
+  }
   if constexpr (MODE == 0) {
-    const int64_t r = slot & ring_mask;
-    const bool hot = (int64_t)owner[r] == slot;  // owner stamped by the preceding launch
-    if (hot) {  // wave-uniform: the whole row belongs to one token
-      store_ring_row<D, G8>(rk, rks, r, H, h, lane, xk);
-      store_ring_row<D, G8>(rv, rvs, r, H, h, lane, xv);
+    const bool lhot = (int64_t)owner[lslot & ring_mask] == lslot;  // stamped by the preceding launch
+    const uint64_t hot = __ballot(lhot);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (!rs.ok[i]) continue;
+      const int64_t slot = readlane64(lslot, i);
+      if ((hot >> i) & 1) {  // the whole row belongs to one token
+        const int64_t r = slot & ring_mask;
+        store_ring_row<D, G8>(rk, rks, r, H, rs.h[i], lane, xk[i]);
+        store_ring_row<D, G8>(rv, rvs, r, H, rs.h[i], lane, xv[i]);
+      }
+      store_pool_row<D>(k4, ks4, slot, H, rs.h[i], lane, xk[i]);
+      store_pool_row<D>(v4, vs4, slot, H, rs.h[i], lane, xv[i]);
     }
-    store_pool_row<D>(k4, ks4, slot, H, h, lane, xk);
-    store_pool_row<D>(v4, vs4, slot, H, h, lane, xv);
-  } else if constexpr (MODE == 1) {
-    store_ring_row<D, G8>(rk, rks, slot, H, h, lane, xk);
-    store_ring_row<D, G8>(rv, rvs, slot, H, h, lane, xv);
   } else {
-    store_pool_row<D>(k4, ks4, slot, H, h, lane, xk);
-    store_pool_row<D>(v4, vs4, slot, H, h, lane, xv);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (!rs.ok[i]) continue;
+      const int64_t slot = readlane64(lslot, i);
+      if constexpr (MODE == 1) {
+        store_ring_row<D, G8>(rk, rks, slot, H, rs.h[i], lane, xk[i]);
+        store_ring_row<D, G8>(rv, rvs, slot, H, rs.h[i], lane, xv[i]);
+      } else {
+        store_pool_row<D>(k4, ks4, slot, H, rs.h[i], lane, xk[i]);
+        store_pool_row<D>(v4, vs4, slot, H, rs.h[i], lane, xv[i]);
+      }
+    }
   }
 }
 
-// Requantize the INT8 ring row r (its 4 codes held by this lane) into INT4 pool row `row`.
+// The ring row about to be overwritten, as loaded ahead of its requantization: this lane's 4 INT8 codes of K and
+// of V and the scales of their groups.
+struct RingRow {
+  uint32_t ck, cv;
+  uint16_t sk, sv;
+};
+
 template <int D, int G8>
-KVT_DEV void evict_row(const int8_t* rbuf, const uint16_t* rscale, int64_t r, uint8_t* pbuf, uint16_t* pscale,
-                       int64_t row, int H, int h, int lane) {
+KVT_DEV RingRow load_ring_row(const int8_t* rk, const int8_t* rv, const uint16_t* rks, const uint16_t* rvs,
+                              int64_t r, int H, int h, int lane, bool live) {
   constexpr int NG8 = D / G8;
-  const uint32_t codes = reinterpret_cast<const uint32_t*>(rbuf + (r * H + h) * D)[lane];
-  const float s8 = f16_bits_to_f32(rscale[(r * H + h) * NG8 + (4 * lane) / G8]);
-  float x[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = (float)(int8_t)(codes >> (8 * i)) * s8;  // exact in fp32
-  store_pool_row<D>(pbuf, pscale, row, H, h, lane, x);
+  const int64_t row = r * H + h;
+  const uint32_t nc = live ? D : 0, ns = live ? NG8 * 2 : 0;
+  const int soff = (4 * lane) / G8 * 2;
+  RingRow o;
+  o.ck = __builtin_amdgcn_raw_buffer_load_b32(row_rsrc(rk + row * D, nc), 4 * lane, 0, 0);
+  o.cv = __builtin_amdgcn_raw_buffer_load_b32(row_rsrc(rv + row * D, nc), 4 * lane, 0, 0);
+  o.sk = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(rks + row * NG8, ns), soff, 0, 0);
+  o.sv = __builtin_amdgcn_raw_buffer_load_b16(row_rsrc(rvs + row * NG8, ns), soff, 0, 0);
+  return o;
 }
 
-template <int DT, int D, int G8>
+// The INT8 ring row part of this lane (codes + group scale) requantized into INT4 pool row `row`.
+template <int D>
+KVT_DEV void store_pool_requant(uint8_t* pbuf, uint16_t* pscale, int64_t row, int H, int h, int lane, uint32_t codes,
+                                uint16_t s8bits) {
+  constexpr int NG4 = D / kG4;
+  uint16_t sb;
+  const uint32_t b = requant4_lane(codes, s8bits, &sb);
+  reinterpret_cast<uint16_t*>(pbuf + (row * H + h) * (D / 2))[lane] = (uint16_t)b;
+  if ((lane & 7) == 0) pscale[(row * H + h) * NG4 + lane / 8] = sb;
+}
+
+// Position-indexed ring append with eviction.  Each wavefront handles kRowsPerWave rows, lane l < kRowsPerWave
+// loading the metadata of row l, in three dependent rounds: (1) sequence id and position, with the new K/V inputs
+// of every row right behind; (2) the sequence's ring placement; (3) the page-table entry, with the ring rows being
+// overwritten.  Then per row: the new token's INT8 row takes the ring row's place and the evicted row, held in
+// registers, is requantized into its INT4 page.
+template <int DT, int G8, int LM>
 __global__ void __launch_bounds__(256) append_evict_kernel(
-    RowIn kin, RowIn vin, const int32_t* seq_ids, const int64_t* positions, int64_t N, int H, uint8_t* k4,
+    RowIn kin, RowIn vin, const int32_t* seq_ids, const int64_t* positions, uint32_t NH, int H, uint8_t* k4,
     uint8_t* v4, uint16_t* ks4, uint16_t* vs4, int8_t* rk, int8_t* rv, uint16_t* rks, uint16_t* rvs,
     const int64_t* ring_base, const int32_t* ring_len, const int64_t* ring_start, const int32_t* page_table,
     int64_t pt_stride, const uint16_t* sm_k_inv, const uint16_t* sm_v_inv) {
+  constexpr int D = 256;
+  constexpr int R = kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (item >= N * H) return;
-  const int64_t t = item / H;
-  const int h = (int)(item - t * H);
-  if (lane >= D / 4) return;
-  const int s = seq_ids[t];
-  const int64_t p = positions[t];
-  const int64_t R = ring_len[s];
-  const int64_t r = ring_base[s] + (p & (R - 1));
-  const int64_t e = p - R;  // the position whose ring row this token overwrites
-  if (e >= ring_start[s]) {
-    const int32_t page = page_table[s * pt_stride + (e >> 6)];
-    if (page >= 0) {
-      const int64_t row = (int64_t)page * kPage + (e & (kPage - 1));
-      evict_row<D, G8>(rk, rks, r, k4, ks4, row, H, h, lane);
-      evict_row<D, G8>(rv, rvs, r, v4, vs4, row, H, h, lane);
+  uint32_t lt;
+  const uint32_t item0 = wave_rows(R, NH, H, lane, &lt);
+  if (item0 >= NH) return;
+  const int lsq = seq_ids[lt];
+  const int64_t lp = positions[lt];
+  const RowSet<R> rs(item0, NH, H);
+  const int c0 = 4 * lane;
+  float xk[R][4], xv[R][4];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    load4<DT, LM>(kin, rs.t[i], rs.h[i], c0, sm_k_inv, D, xk[i]);
+    load4<DT, LM>(vin, rs.t[i], rs.h[i], c0, sm_v_inv, D, xv[i]);
+  }
+  const int64_t llen = ring_len[lsq];
+  const int64_t lr = ring_base[lsq] + (lp & (llen - 1));
+  const int64_t le = lp - llen;  // the position whose ring row this token overwrites
+  const bool lev = le >= ring_start[lsq];
+  const uint64_t ev = __ballot(lev);
+  int64_t r[R];
+  RingRow old[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    r[i] = readlane64(lr, i);
+    old[i] = load_ring_row<D, G8>(rk, rv, rks, rvs, r[i], H, rs.h[i], lane, (ev >> i) & 1);
+  }
+  const int pg = page_table[lsq * pt_stride + (lev ? le >> 6 : 0)];  // entry 0 of the row when unused
+  const int64_t lrow = lev && pg >= 0 ? (int64_t)pg * kPage + (le & (kPage - 1)) : -1;  // INT4 row of the evictee
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (!rs.ok[i]) continue;
+    // The new row goes in first: its stores alias the old row's loads, which keeps those loads up front.
+    store_ring_row<D, G8>(rk, rks, r[i], H, rs.h[i], lane, xk[i]);
+    store_ring_row<D, G8>(rv, rvs, r[i], H, rs.h[i], lane, xv[i]);
+    const int64_t row = readlane64(lrow, i);
+    if (row >= 0) {
+      store_pool_requant<D>(k4, ks4, row, H, rs.h[i], lane, old[i].ck, old[i].sk);
+      store_pool_requant<D>(v4, vs4, row, H, rs.h[i], lane, old[i].cv, old[i].sv);
     }
   }
-  float xk[4], xv[4];
-  const int c0 = 4 * lane;
-  load4<DT>(kin, t, h, c0, sm_k_inv, D, xk);
-  load4<DT>(vin, t, h, c0, sm_v_inv, D, xv);
-  store_ring_row<D, G8>(rk, rks, r, H, h, lane, xk);
-  store_ring_row<D, G8>(rv, rvs, r, H, h, lane, xv);
 }
 
 __global__ void page_table_update_kernel(int32_t* pt, int64_t pt_stride, int64_t n, const int32_t* seq,
@@ -185,20 +428,43 @@ __global__ void page_table_update_kernel(int32_t* pt, int64_t pt_stride, int64_t
 }
 
 // ---------------------------------------------------------------------------------------------- dispatch helpers
+// The load mode of a launch: vector loads when every 4-channel chunk of k, v (and of the smoothing inverses) is
+// aligned to its size and the smoothing inverses are both given or both absent; element loads otherwise.
+int load_mode(const RowIn& kin, const RowIn& vin, int dtype, const void* smk, const void* smv) {
+  const uintptr_t chunk = dtype == kF32 ? 16 : 8;
+  auto ok = [&](const RowIn& in) {
+    return (uintptr_t)in.base % chunk == 0 && in.stride_n % 4 == 0 && in.stride_h % 4 == 0;
+  };
+  if (!ok(kin) || !ok(vin) || (uintptr_t)smk % 8 != 0 || (uintptr_t)smv % 8 != 0) return kLoadElem;
+  if (smk == nullptr && smv == nullptr) return kLoadVec;
+  return smk != nullptr && smv != nullptr ? kLoadVecSm : kLoadElem;
+}
+
 template <int MODE>
 int launch_quant_store(const RowIn& kin, const RowIn& vin, int dtype, const void* loc, int loc64, int64_t N, int H,
                        int D, int group8, uint8_t* k4, uint8_t* v4, uint16_t* ks4, uint16_t* vs4, int8_t* rk,
                        int8_t* rv, uint16_t* rks, uint16_t* rvs, const int32_t* owner, const uint16_t* smk,
                        const uint16_t* smv, int64_t ring_mask, hipStream_t stream) {
+  if (N > (int64_t)(UINT32_MAX / 8)) return KVT_EINVAL;  // slot indices are read through a 32-bit buffer range
   const dim3 grid((unsigned)((N * H + kRowsPerBlock - 1) / kRowsPerBlock));
-#define KVT_QS(DT_, D_, G_)                                                                                    \
-  hipLaunchKernelGGL((quant_store_kernel<DT_, D_, G_, MODE>), grid, dim3(256), 0, stream, kin, vin, loc, loc64, \
-                     N, H, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, smk, smv, ring_mask)
+  const int lm = load_mode(kin, vin, dtype, smk, smv);
+  const uint32_t NH = (uint32_t)(N * H);
+#define KVT_QS1(DT_, D_, G_, LM_)                                                                                  \
+  hipLaunchKernelGGL((quant_store_kernel<DT_, D_, G_, MODE, LM_>), grid, dim3(256), 0, stream, kin, vin, loc,      \
+                     loc64, NH, H, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, smk, smv, ring_mask)
+#define KVT_QS(DT_, D_, G_)              \
+  if (lm == kLoadVec) {                  \
+    KVT_QS1(DT_, D_, G_, kLoadVec);      \
+  } else if (lm == kLoadVecSm) {         \
+    KVT_QS1(DT_, D_, G_, kLoadVecSm);    \
+  } else {                               \
+    KVT_QS1(DT_, D_, G_, kLoadElem);     \
+  }
 #define KVT_QS_G(DT_, D_)                     \
   if (group8 == 64) {                         \
-    KVT_QS(DT_, D_, 64);                      \
+    KVT_QS(DT_, D_, 64)                       \
   } else if (group8 == D_ && D_ != 64) {      \
-    KVT_QS(DT_, D_, D_);                      \
+    KVT_QS(DT_, D_, D_)                       \
   } else {                                    \
     return KVT_EINVAL;                        \
   }
@@ -208,7 +474,7 @@ int launch_quant_store(const RowIn& kin, const RowIn& vin, int dtype, const void
   } else if (D == 128) {       \
     KVT_QS_G(DT_, 128)         \
   } else if (D == 64) {        \
-    KVT_QS(DT_, 64, 64);       \
+    KVT_QS(DT_, 64, 64)        \
   } else {                     \
     return KVT_EINVAL;         \
   }
@@ -224,6 +490,7 @@ int launch_quant_store(const RowIn& kin, const RowIn& vin, int dtype, const void
 #undef KVT_QS_D
 #undef KVT_QS_G
 #undef KVT_QS
+#undef KVT_QS1
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }
@@ -237,7 +504,7 @@ int kvt_quant_store_tiered(const void* k, const void* v, int dtype, int64_t sk_n
                            void* v_buf, void* k_scale, void* v_scale, void* ring_k, void* ring_v, void* ring_ks,
                            void* ring_vs, void* owner, const void* sm_k_inv, const void* sm_v_inv, int64_t ring_mask,
                            int group8, void* stream) {
-  if (N < 0 || H <= 0 || ring_mask < 0 || ((ring_mask + 1) & ring_mask) != 0) return KVT_EINVAL;
+  if (N < 0 || H <= 0 || N > INT32_MAX / H || ring_mask < 0 || ((ring_mask + 1) & ring_mask) != 0) return KVT_EINVAL;
   if (N == 0) return KVT_OK;
   hipStream_t st = (hipStream_t)stream;
   const unsigned sblocks = (unsigned)((N + 255) / 256);
@@ -255,7 +522,7 @@ int kvt_quant_store_int8(const void* k, const void* v, int dtype, int64_t sk_n, 
                          int64_t sv_h, const void* loc, int loc_is_int64, int64_t N, int H, int D, void* k_buf,
                          void* v_buf, void* k_scale, void* v_scale, const void* sm_k_inv, const void* sm_v_inv,
                          int group8, void* stream) {
-  if (N < 0 || H <= 0) return KVT_EINVAL;
+  if (N < 0 || H <= 0 || N > INT32_MAX / H) return KVT_EINVAL;
   if (N == 0) return KVT_OK;
   return launch_quant_store<1>(RowIn{k, sk_n, sk_h}, RowIn{v, sv_n, sv_h}, dtype, loc, loc_is_int64, N, H, D, group8,
                                nullptr, nullptr, nullptr, nullptr, (int8_t*)k_buf, (int8_t*)v_buf,
@@ -267,7 +534,7 @@ int kvt_quant_store_int4(const void* k, const void* v, int dtype, int64_t sk_n, 
                          int64_t sv_h, const void* loc, int loc_is_int64, int64_t N, int H, int D, void* k_buf,
                          void* v_buf, void* k_scale, void* v_scale, const void* sm_k_inv, const void* sm_v_inv,
                          void* stream) {
-  if (N < 0 || H <= 0) return KVT_EINVAL;
+  if (N < 0 || H <= 0 || N > INT32_MAX / H) return KVT_EINVAL;
   if (N == 0) return KVT_OK;
   return launch_quant_store<2>(RowIn{k, sk_n, sk_h}, RowIn{v, sv_n, sv_h}, dtype, loc, loc_is_int64, N, H, D, 64,
                                (uint8_t*)k_buf, (uint8_t*)v_buf, (uint16_t*)k_scale, (uint16_t*)v_scale, nullptr,
@@ -291,23 +558,33 @@ int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int6
                      void* k_scale, void* v_scale, void* ring_k, void* ring_v, void* ring_ks, void* ring_vs,
                      const void* ring_base, const void* ring_len, const void* ring_start, const void* page_table,
                      int64_t pt_stride, const void* sm_k_inv, const void* sm_v_inv, int group8, void* stream) {
-  if (N < 0 || H <= 0) return KVT_EINVAL;
+  if (N < 0 || H <= 0 || N > INT32_MAX / H) return KVT_EINVAL;
   if (N == 0) return KVT_OK;
   const dim3 grid((unsigned)((N * H + kRowsPerBlock - 1) / kRowsPerBlock));
   hipStream_t st = (hipStream_t)stream;
   const RowIn kin{k, sk_n, sk_h}, vin{v, sv_n, sv_h};
-#define KVT_AE(DT_, D_, G_)                                                                                        \
-  hipLaunchKernelGGL((append_evict_kernel<DT_, D_, G_>), grid, dim3(256), 0, st, kin, vin, (const int32_t*)seq_ids, \
-                     (const int64_t*)positions, N, H, (uint8_t*)k_buf, (uint8_t*)v_buf, (uint16_t*)k_scale,         \
-                     (uint16_t*)v_scale, (int8_t*)ring_k, (int8_t*)ring_v, (uint16_t*)ring_ks,                     \
+  const int lm = load_mode(kin, vin, dtype, sm_k_inv, sm_v_inv);
+  const uint32_t NH = (uint32_t)(N * H);
+#define KVT_AE1(DT_, G_, LM_)                                                                                      \
+  hipLaunchKernelGGL((append_evict_kernel<DT_, G_, LM_>), grid, dim3(256), 0, st, kin, vin,                        \
+                     (const int32_t*)seq_ids, (const int64_t*)positions, NH, H, (uint8_t*)k_buf, (uint8_t*)v_buf,  \
+                     (uint16_t*)k_scale, (uint16_t*)v_scale, (int8_t*)ring_k, (int8_t*)ring_v, (uint16_t*)ring_ks, \
                      (uint16_t*)ring_vs, (const int64_t*)ring_base, (const int32_t*)ring_len,                      \
                      (const int64_t*)ring_start, (const int32_t*)page_table, pt_stride, (const uint16_t*)sm_k_inv, \
                      (const uint16_t*)sm_v_inv)
+#define KVT_AE(DT_, G_)                \
+  if (lm == kLoadVec) {                \
+    KVT_AE1(DT_, G_, kLoadVec);        \
+  } else if (lm == kLoadVecSm) {       \
+    KVT_AE1(DT_, G_, kLoadVecSm);      \
+  } else {                             \
+    KVT_AE1(DT_, G_, kLoadElem);       \
+  }
 #define KVT_AE_G(DT_)              \
   if (group8 == 64) {              \
-    KVT_AE(DT_, 256, 64);          \
+    KVT_AE(DT_, 64)                \
   } else if (group8 == 256) {      \
-    KVT_AE(DT_, 256, 256);         \
+    KVT_AE(DT_, 256)               \
   } else {                         \
     return KVT_EINVAL;             \
   }
@@ -323,6 +600,7 @@ int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int6
   }
 #undef KVT_AE_G
 #undef KVT_AE
+#undef KVT_AE1
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }

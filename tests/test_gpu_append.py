@@ -255,3 +255,123 @@ def test_append_evict_matches_oracle(kvt_pkg):
     for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
         assert torch.equal(getattr(dc, name)[0].cpu(), getattr(oc, name)), name
     assert dc.seq_lens[:2].tolist() == lens
+
+
+def _boundary_rows(n, group, qmax, seed):
+    """fp32 rows [n, H, D] whose quotients x / s sit on, or one ulp either side of, half-integers: element 0 of each
+    group is +-qmax * s0 (so the stored scale is exactly the fp16 value s0) and the others are +-(k + 0.5) * s0,
+    k in [0, qmax), nudged by -1, 0 or +1 ulp.  All products are exact in fp32."""
+    rng = np.random.default_rng(seed)
+    g = n * H * D // group
+    s0 = rng.uniform(2.0 ** -8, 8.0, g).astype(np.float16).astype(np.float32)
+    s0[::7] = 2.0 ** rng.integers(-6, 4, s0[::7].size)                       # exact reciprocals too
+    k = rng.integers(0, int(qmax), (g, group)).astype(np.float32) + np.float32(0.5)
+    base = k * s0[:, None]
+    nudge = rng.integers(-1, 2, (g, group))
+    vals = np.where(nudge < 0, np.nextafter(base, np.float32(-np.inf)),
+                    np.where(nudge > 0, np.nextafter(base, np.float32(np.inf)), base)).astype(np.float32)
+    vals[:, 0] = np.float32(qmax) * s0
+    vals *= rng.choice(np.array([-1.0, 1.0], np.float32), (g, group))
+    return torch.from_numpy(vals.reshape(n, H, D))
+
+
+@pytest.mark.parametrize("aligned", [True, False])
+def test_quant_rounding_boundaries(kvt_pkg, aligned):
+    """Quotients on and one ulp around x.5 (ties to even, and the cases where a reciprocal multiply would round the
+    other way): INT8-G64 and INT4-G32 writers bit-exact vs the oracle's IEEE division, through the vector-load path
+    (aligned rows) and the element path (row stride H * D + 1)."""
+    from kvtier import sparse_attn as sa
+    n = 512
+    ones = torch.ones(H, D, dtype=torch.float16)
+    for group, qmax in ((64, 127.0), (32, 7.0)):
+        x = _boundary_rows(n, group, qmax, seed=int(qmax))
+        if aligned:
+            xd = x.to(dev)
+        else:
+            wide = torch.zeros(n, H * D + 1, dtype=torch.float32)
+            wide[:, :H * D] = x.reshape(n, H * D)
+            xd = wide.to(dev)[:, :H * D].view(n, H, D)
+        loc = torch.arange(n, dtype=torch.int64)
+        if group == 64:
+            k8 = torch.zeros(n, H, D, dtype=torch.int8, device=dev); v8 = torch.zeros_like(k8)
+            ks = torch.zeros(n, H, 4, dtype=torch.float16, device=dev); vs = torch.zeros_like(ks)
+            sa.quant_store_kv_int8(xd, xd, loc.to(dev), k8, v8, ks, vs, ones.to(dev), ones.to(dev))
+            q, s = ref.quant8(x)
+            got = (k8, ks)
+        else:
+            k4 = torch.zeros(n, H, D // 2, dtype=torch.uint8, device=dev); v4 = torch.zeros_like(k4)
+            ks = torch.zeros(n, H, 8, dtype=torch.float16, device=dev); vs = torch.zeros_like(ks)
+            sa.quant_store_kv_int4(xd, xd, loc.to(dev), k4, v4, ks, vs, ones.to(dev), ones.to(dev))
+            q, s = ref.quant4(x)
+            got = (k4, ks)
+        torch.cuda.synchronize()
+        assert torch.equal(got[1].cpu(), s), group
+        assert torch.equal(got[0].cpu(), q), group
+
+
+@pytest.mark.parametrize("g8", [64, 256])
+def test_append_evict_fp32_boundaries(kvt_pkg, g8):
+    """The ring append with fp32 boundary rows (quotients at x.5 +- 1 ulp for the G64 ring scale): 200 tokens in
+    chunks through a 64-row ring, so the requantized evictions are exercised too; every buffer bit-exact."""
+    from kvtier.kvt import PosTieredCache
+    dc = PosTieredCache(1, H, D, n_pages=8, ring_total=64, max_seqs=1, max_pages=8, device=dev, group8=g8,
+                        page_seed=5)
+    oc = ref.PosTieredCache(H, D, n_pages=8, ring_total=64, group8=g8)
+    alloc = ref.PageAllocator(8, seed=5)
+    dc.add_seq(64)
+    oc.add_seq(0, 64)
+    x = _boundary_rows(200, 64, 127.0, seed=9)
+    done = 0
+    for cnt in (1, 63, 64, 7, 64, 1):
+        plan = dc.plan_append([0], [cnt])
+        oc.plan_pages(0, cnt, alloc)
+        xk, xv = x[done:done + cnt], -x[done:done + cnt]
+        oc.append(0, xk, xv)
+        dc.append(0, plan, xk.to(dev), xv.to(dev))
+        dc.commit(plan)
+        done += cnt
+    torch.cuda.synchronize()
+    assert torch.equal(dc.page_table.cpu(), oc.page_table(8))
+    for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
+        assert torch.equal(getattr(dc, name)[0].cpu(), getattr(oc, name)), name
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_unaligned_rows_all_writers(kvt_pkg, dt):
+    """Rows whose stride (H * D + 1 elements) breaks the 8-byte chunk alignment take the element-load path: every
+    token of the INT8, INT4 and ring-append writers bit-exact vs the oracle (600 tokens, more than one launch wave)."""
+    from kvtier import sparse_attn as sa
+    from kvtier.kvt import PosTieredCache
+    gen = torch.Generator().manual_seed(12)
+    n = 600
+    x = (torch.randn(n, H, D, generator=gen) * 3).to(dt)
+    wide = torch.zeros(n, H * D + 1, dtype=dt)
+    wide[:, :H * D] = x.reshape(n, H * D)
+    xd = wide.to(dev)[:, :H * D].view(n, H, D)
+    smi = (0.5 + 1.5 * torch.rand(H, D, generator=gen)).half()
+    loc = torch.arange(n, dtype=torch.int32)
+    k8 = torch.zeros(n, H, D, dtype=torch.int8, device=dev); v8 = torch.zeros_like(k8)
+    ks8 = torch.zeros(n, H, 4, dtype=torch.float16, device=dev); vs8 = torch.zeros_like(ks8)
+    sa.quant_store_kv_int8(xd, xd, loc.to(dev), k8, v8, ks8, vs8, smi.to(dev), smi.to(dev))
+    k4 = torch.zeros(n, H, D // 2, dtype=torch.uint8, device=dev); v4 = torch.zeros_like(k4)
+    ks4 = torch.zeros(n, H, 8, dtype=torch.float16, device=dev); vs4 = torch.zeros_like(ks4)
+    sa.quant_store_kv_int4(xd, xd, loc.to(dev), k4, v4, ks4, vs4, smi.to(dev), smi.to(dev))
+    dc = PosTieredCache(1, H, D, n_pages=16, ring_total=512, max_seqs=1, max_pages=16, device=dev, page_seed=2)
+    oc = ref.PosTieredCache(H, D, n_pages=16, ring_total=512)
+    alloc = ref.PageAllocator(16, seed=2)
+    dc.add_seq(512)
+    oc.add_seq(0, 512)
+    for a, cnt in ((0, 512), (512, 88)):
+        plan = dc.plan_append([0], [cnt])
+        oc.plan_pages(0, cnt, alloc)
+        oc.append(0, x[a:a + cnt], x[a:a + cnt])
+        dc.append(0, plan, xd[a:a + cnt], xd[a:a + cnt])
+        dc.commit(plan)
+    torch.cuda.synchronize()
+    q8, s8 = ref.quant8(x, sm_inv=smi)
+    p4, s4 = ref.quant4(x, sm_inv=smi)
+    assert torch.equal(k8.cpu(), q8) and torch.equal(ks8.cpu(), s8) and torch.equal(v8.cpu(), q8)
+    assert torch.equal(k4.cpu(), p4) and torch.equal(ks4.cpu(), s4) and torch.equal(vs4.cpu(), s4)
+    assert torch.equal(dc.page_table.cpu(), oc.page_table(16))
+    for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
+        assert torch.equal(getattr(dc, name)[0].cpu(), getattr(oc, name)), name
