@@ -113,7 +113,8 @@ def pmc_sample(impl: str) -> None:
 
 def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, impl: str) -> None:
     """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel from two rocprofv3 --pmc counter
-    CSVs, scaled by the ratio of the calibration copy's known bytes to its counter reading."""
+    CSVs, scaled by the ratio of the calibration copy's known bytes to its counter reading; also the median per
+    dispatch of the cache build's append launches, scaled the same way."""
     import csv
 
     def per_kernel(path, counter):
@@ -142,6 +143,17 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
         lines.append(f"{counter}: decode kernel {dec_kib:.1f} KiB/dispatch over {len(dec_v)} dispatches; copy of "
                      f"{CAL_BYTES} B {key}s {cal_kib:.1f} KiB -> factor {factor:.4f} -> {dec_kib * 1024 * factor:.0f} B")
     res["hbm_bytes_per_launch"] = res["read"]["bytes_per_launch"] + res["write"]["bytes_per_launch"]
+    # the write path: the cache build's 384 append launches (8,192 tokens each; all but the first 12 evict)
+    app = {}
+    for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
+        vals = sorted(x for k, v in per_kernel(path, counter).items() if "append_evict_kernel" in k for x in v)
+        if vals:
+            med = vals[len(vals) // 2]
+            app[key] = round(med * 1024 * res[key]["factor"])
+            lines.append(f"{counter}: append_evict median {med:.1f} KiB/dispatch over {len(vals)} dispatches -> "
+                         f"{app[key]} B")
+    if app:
+        res["append_evict_bytes_per_launch"] = app
     with open(out_json, "w") as f:
         json.dump(res, f, indent=1)
     with open(out_txt, "a") as f:  # appended under the commands already written at the top of the file
@@ -220,6 +232,67 @@ def prefill_workload(args) -> dict:
                      "unit": "TFLOP/s", "frac": round(flops / t_prefill / 2.5e15, 4), "traffic": None,
                      "kernel": "prefill (causal, all chunks and layers)", "kernel_ms": round(t_prefill * 1e3, 3),
                      "flops": flops},
+    }
+
+
+def append_workload(args) -> dict:
+    """Steady-state quantize-append: 12 layers, 4 steps of 8,192-token appends into a full 8,192-row ring (every
+    token evicts the oldest ring row into an INT4 page), fresh bf16 K/V per (step, layer).  The 48 launches are
+    captured in one HIP graph so the timing is the device's (a Python launch costs more than a kernel); value = GB/s
+    of the path's algorithmic HBM bytes."""
+    import kvtier  # noqa: F401
+    from kvtier.kvt import PosTieredCache
+    S, N = 4, RING
+    n_pages = (S + 1) * N // PAGE + 2
+    cache = PosTieredCache(LAYERS, H, D, n_pages=n_pages, ring_total=RING, max_seqs=1, max_pages=n_pages + 1,
+                           device="cuda", page_seed=1)
+    cache.add_seq(RING)
+    fill = cache.plan_append([0], [N])
+    for layer in range(LAYERS):
+        k, v = _layer_kv(N, layer, seed=20)
+        cache.append(layer, fill, k, v)
+    cache.commit(fill)
+    plans = []
+    for _ in range(S):
+        plans.append(cache.plan_append([0], [N]))
+        cache.commit(plans[-1])
+    kv = [[_layer_kv(N, layer, seed=21 + s) for layer in range(LAYERS)] for s in range(S)]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for s in range(S):                                        # warm-up outside the capture
+            for layer in range(LAYERS):
+                cache.append(layer, plans[s], *kv[s][layer])
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for s in range(S):
+            for layer in range(LAYERS):
+                cache.append(layer, plans[s], *kv[s][layer])
+    for _ in range(max(1, args.warmup)):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t_launch = e0.elapsed_time(e1) / 1e3 / (reps * S * LAYERS)
+    nbytes = cache.append_bytes(N, N)
+    gbps = nbytes / t_launch / 1e9
+    return {
+        "metric": "quantize-append with ring eviction: GB/s of algorithmic HBM bytes (8,192 tokens per launch)",
+        "value": round(gbps, 1), "unit": "GB/s", "higher_is_better": True, "steps": reps, "warmup": args.warmup,
+        "us_per_launch": round(t_launch * 1e6, 2), "dtype": "f32 (bf16 in, INT8/INT4 out)", "data": "synthetic",
+        "config": {"workload": "append 8,192 tokens x 12 layers into a full 8,192-row ring, 2 KV heads, D 256, "
+                               "INT8-G64 ring, INT4-G32 pages; 4 steps per graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None, "kernel": "append_evict",
+                     "bytes_per_launch": nbytes},
     }
 
 
@@ -324,7 +397,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fused-combine", action="store_true",
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
-    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged"],
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
@@ -337,12 +410,12 @@ def main():
         pmc_sample(args.impl)
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU layout is a design in "
-              "DESIGN.md, not a measured path", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); sharding across GPUs is a documented "
+              "design, not a measured path", file=sys.stderr)
         sys.exit(2)
     if args.workload != "decode262k":
         fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
-              "ragged": lambda a: decode_steps_workload(a, True)}[args.workload]
+              "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload}[args.workload]
         line = fn(args)
         line["n_gpus"] = 1
         print(json.dumps(line))

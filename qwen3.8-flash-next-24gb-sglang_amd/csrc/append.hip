@@ -22,13 +22,7 @@ using namespace kvt;
 
 namespace {
 
-constexpr int kWavesPerBlock = 4;
-// (token, head) rows per wavefront.  One row per wave gives twice as many waves as fit at once on the chip for
-// an 8192-token append, so later waves' loads overlap earlier waves' quantization (2 and 4 rows per wave, with
-// every load issued up front, measured slower).
-constexpr int kRowsPerWave = 1;
-constexpr int kRowsPerBlock = kWavesPerBlock * kRowsPerWave;
-
+constexpr int kWavesPerBlock = 4;  // one (token, KV head) row per wavefront, four per block
 struct RowIn {
   const void* base;
   int64_t stride_n;  // elements
@@ -48,37 +42,56 @@ KVT_DEV __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t bytes) {
 // The vector forms need the base and both strides to keep every 4-channel chunk aligned.
 enum LoadMode : int { kLoadElem = 0, kLoadVec = 1, kLoadVecSm = 2 };
 
-// The 4 input channels c0..c0+3 of row (t, h) as fp32, times the smoothing inverse when one is given:
-// x = f32(k) * f32(sm_inv) (patches/kv_tiers.py:332-333).
+// The 4 input channels c0..c0+3 of row (t, h), loaded (load4_raw) and later converted to fp32 times the smoothing
+// inverse when one is given: x = f32(k) * f32(sm_inv) (patches/kv_tiers.py:332-333).  Splitting the two lets the
+// kernels put the input loads first and the metadata chain behind them without waiting for the inputs.
+struct In4 {
+  uint32_t w[4];  // 16-bit types: w[0..1] hold the 4 values; fp32: w[0..3]; kLoadElem: the converted fp32 bits
+  uint2 m;        // kLoadVecSm: the 4 smoothing values (fp16)
+};
+
 template <int DT, int LM>
-KVT_DEV void load4(const RowIn& in, int64_t t, int h, int c0, const uint16_t* sm_inv, int D, float x[4]) {
+KVT_DEV In4 load4_raw(const RowIn& in, int64_t t, int h, int c0, const uint16_t* sm_inv, int D) {
   const int64_t off = t * in.stride_n + (int64_t)h * in.stride_h + c0;
+  In4 r{};
   if constexpr (LM == kLoadElem) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float v = load_in<DT>(in.base, off + i);
-      x[i] = sm_inv ? v * f16_bits_to_f32(sm_inv[h * D + c0 + i]) : v;
+      r.w[i] = __float_as_uint(sm_inv ? v * f16_bits_to_f32(sm_inv[h * D + c0 + i]) : v);
     }
   } else {
     if constexpr (DT == kF32) {
-      const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(in.base) + off);
-      x[0] = v.x;
-      x[1] = v.y;
-      x[2] = v.z;
-      x[3] = v.w;
+      const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(in.base) + off);
+      r.w[0] = v.x;
+      r.w[1] = v.y;
+      r.w[2] = v.z;
+      r.w[3] = v.w;
     } else {
       const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(in.base) + off);
-      const uint16_t e[4] = {(uint16_t)v.x, (uint16_t)(v.x >> 16), (uint16_t)v.y, (uint16_t)(v.y >> 16)};
+      r.w[0] = v.x;
+      r.w[1] = v.y;
+    }
+    if constexpr (LM == kLoadVecSm) r.m = *reinterpret_cast<const uint2*>(sm_inv + h * D + c0);
+  }
+  return r;
+}
+
+template <int DT, int LM>
+KVT_DEV void to_f32(const In4& r, float x[4]) {
+  if constexpr (LM == kLoadElem || DT == kF32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = DT == kBF16 ? bf16_to_f32(e[i]) : f16_bits_to_f32(e[i]);
-    }
-    if constexpr (LM == kLoadVecSm) {
-      const uint2 m = *reinterpret_cast<const uint2*>(sm_inv + h * D + c0);
-      x[0] *= f16_bits_to_f32((uint16_t)m.x);
-      x[1] *= f16_bits_to_f32((uint16_t)(m.x >> 16));
-      x[2] *= f16_bits_to_f32((uint16_t)m.y);
-      x[3] *= f16_bits_to_f32((uint16_t)(m.y >> 16));
-    }
+    for (int i = 0; i < 4; ++i) x[i] = __uint_as_float(r.w[i]);
+  } else {
+    const uint16_t e[4] = {(uint16_t)r.w[0], (uint16_t)(r.w[0] >> 16), (uint16_t)r.w[1], (uint16_t)(r.w[1] >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = DT == kBF16 ? bf16_to_f32(e[i]) : f16_bits_to_f32(e[i]);
+  }
+  if constexpr (LM == kLoadVecSm) {
+    x[0] *= f16_bits_to_f32((uint16_t)r.m.x);
+    x[1] *= f16_bits_to_f32((uint16_t)(r.m.x >> 16));
+    x[2] *= f16_bits_to_f32((uint16_t)r.m.y);
+    x[3] *= f16_bits_to_f32((uint16_t)(r.m.y >> 16));
   }
 }
 
@@ -228,49 +241,21 @@ KVT_DEV int64_t load_loc(const void* loc, int loc64, int64_t t) {
   return loc64 ? reinterpret_cast<const int64_t*>(loc)[t] : (int64_t) reinterpret_cast<const int32_t*>(loc)[t];
 }
 
-// load_loc without a branch on the index width: the high word of an int32 index comes from a load outside the
-// buffer (zero, no access) and is replaced by the sign extension.
-KVT_DEV int64_t load_loc_nb(const void* loc, int loc64, uint32_t t, uint32_t n) {
-  const auto rs = row_rsrc(loc, loc64 ? n * 8u : n * 4u);
-  const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(rs, loc64 ? t * 8u : t * 4u, 0, 0);
-  const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(rs, loc64 ? t * 8u + 4u : 0x80000000u, 0, 0);
-  return loc64 ? (int64_t)(((uint64_t)hi << 32) | lo) : (int64_t)(int32_t)lo;
+// Blocks are dealt to the 8 XCDs round-robin (block b runs on XCD b % 8), each XCD with its own L2.  Renumbered
+// this way, every XCD takes one contiguous range of blocks, so rows that share cache lines (scale rows, per-token
+// indices) are fetched into one L2 rather than several.
+KVT_DEV uint32_t xcd_block() {
+  const uint32_t b = blockIdx.x, n = gridDim.x;
+  const uint32_t q = n / 8, r = n % 8, x = b % 8;
+  return x * q + min(x, r) + b / 8;
 }
 
-// (token, head) of the ROWS consecutive rows from item0 (uniform across the wave); rows past NH are clamped onto
-// the last row for their loads and flagged so that they store nothing.  Row indices fit 32 bits (the launchers
-// reject larger N * H).
-template <int ROWS>
-struct RowSet {
-  uint32_t t[ROWS];
-  int h[ROWS];
-  bool ok[ROWS];
-  KVT_DEV RowSet(uint32_t item0, uint32_t NH, int H) {
-#pragma unroll
-    for (int i = 0; i < ROWS; ++i) {
-      ok[i] = item0 + i < NH;
-      const uint32_t item = ok[i] ? item0 + i : NH - 1;
-      t[i] = item / (uint32_t)H;
-      h[i] = (int)(item - t[i] * (uint32_t)H);
-    }
-  }
-};
-
-// First row of this wavefront; lane l < ROWS also gets the token of row first + l (clamped) in *lane_t, so that the
-// per-row metadata loads of the wave are one vector load each.
-KVT_DEV uint32_t wave_rows(int rows, uint32_t NH, int H, int lane, uint32_t* lane_t) {
-  const uint32_t item0 =
-      ((uint32_t)blockIdx.x * kWavesPerBlock + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * rows;
-  uint32_t it = item0 + (uint32_t)(lane < rows ? lane : rows - 1);
-  it = it < NH ? it : NH - 1;
-  *lane_t = it / (uint32_t)H;
-  return item0;
-}
-
-KVT_DEV int64_t readlane64(int64_t v, int l) {
-  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)v, l);
-  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
-  return (int64_t)(((uint64_t)hi << 32) | lo);
+// This wavefront's (token, head) row, or false past the last one.
+KVT_DEV bool wave_row(uint32_t NH, int H, uint32_t* t, int* h) {
+  const uint32_t item = xcd_block() * kWavesPerBlock + (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  *t = item / (uint32_t)H;
+  *h = (int)(item - *t * (uint32_t)H);
+  return item < NH;
 }
 
 __global__ void __launch_bounds__(256) stamp_owner_kernel(const void* loc, int loc64, int64_t N, int32_t* owner,
@@ -281,55 +266,45 @@ __global__ void __launch_bounds__(256) stamp_owner_kernel(const void* loc, int l
   owner[slot & ring_mask] = (int32_t)slot;  // one winner per contested ring row (patches/kv_tiers.py:272-280)
 }
 
-// MODE 0: tiered dual write; 1: INT8 only (ring buffers are the pool); 2: INT4 only.  Each wavefront handles
-// kRowsPerWave rows: their slot indices (one per lane) and inputs are loaded first, then (MODE 0) the owner words.
+// MODE 0: tiered dual write; 1: INT8 only (ring buffers are the pool); 2: INT4 only.  The row's slot index (and
+// in MODE 0 the owner word of its ring row) are wave-uniform scalar loads, issued behind the input loads; the
+// scheduling barriers keep the compiler from interleaving input-dependent arithmetic into that chain.
 template <int DT, int D, int G8, int MODE, int LM>
 __global__ void __launch_bounds__(256) quant_store_kernel(
     RowIn kin, RowIn vin, const void* loc, int loc64, uint32_t NH, int H, uint8_t* k4, uint8_t* v4, uint16_t* ks4,
     uint16_t* vs4, int8_t* rk, int8_t* rv, uint16_t* rks, uint16_t* rvs, const int32_t* owner,
     const uint16_t* sm_k_inv, const uint16_t* sm_v_inv, int64_t ring_mask) {
-  constexpr int R = kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  uint32_t lt;
-  const uint32_t item0 = wave_rows(R, NH, H, lane, &lt);
-  if (item0 >= NH || lane >= D / 4) return;
-  const int64_t lslot = load_loc_nb(loc, loc64, lt, NH / (uint32_t)H);
-  const RowSet<R> rs(item0, NH, H);
+  uint32_t t;
+  int h;
+  if (!wave_row(NH, H, &t, &h) || lane >= D / 4) return;
   const int c0 = 4 * lane;
-  float xk[R][4], xv[R][4];
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    load4<DT, LM>(kin, rs.t[i], rs.h[i], c0, sm_k_inv, D, xk[i]);
-    load4<DT, LM>(vin, rs.t[i], rs.h[i], c0, sm_v_inv, D, xv[i]);
-  }
+  const In4 rk_in = load4_raw<DT, LM>(kin, t, h, c0, sm_k_inv, D);
+  const In4 rv_in = load4_raw<DT, LM>(vin, t, h, c0, sm_v_inv, D);
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t slot = load_loc(loc, loc64, t);
+  bool hot = false;
   if constexpr (MODE == 0) {
-    const bool lhot = (int64_t)owner[lslot & ring_mask] == lslot;  // stamped by the preceding launch
-    const uint64_t hot = __ballot(lhot);
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      if (!rs.ok[i]) continue;
-      const int64_t slot = readlane64(lslot, i);
-      if ((hot >> i) & 1) {  // the whole row belongs to one token
-        const int64_t r = slot & ring_mask;
-        store_ring_row<D, G8>(rk, rks, r, H, rs.h[i], lane, xk[i]);
-        store_ring_row<D, G8>(rv, rvs, r, H, rs.h[i], lane, xv[i]);
-      }
-      store_pool_row<D>(k4, ks4, slot, H, rs.h[i], lane, xk[i]);
-      store_pool_row<D>(v4, vs4, slot, H, rs.h[i], lane, xv[i]);
+    __builtin_amdgcn_sched_barrier(0);
+    hot = (int64_t)owner[slot & ring_mask] == slot;  // stamped by the preceding launch
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float xk[4], xv[4];
+  to_f32<DT, LM>(rk_in, xk);
+  to_f32<DT, LM>(rv_in, xv);
+  if constexpr (MODE == 0) {
+    if (hot) {  // wave-uniform: the whole row belongs to one token
+      store_ring_row<D, G8>(rk, rks, slot & ring_mask, H, h, lane, xk);
+      store_ring_row<D, G8>(rv, rvs, slot & ring_mask, H, h, lane, xv);
     }
+    store_pool_row<D>(k4, ks4, slot, H, h, lane, xk);
+    store_pool_row<D>(v4, vs4, slot, H, h, lane, xv);
+  } else if constexpr (MODE == 1) {
+    store_ring_row<D, G8>(rk, rks, slot, H, h, lane, xk);
+    store_ring_row<D, G8>(rv, rvs, slot, H, h, lane, xv);
   } else {
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      if (!rs.ok[i]) continue;
-      const int64_t slot = readlane64(lslot, i);
-      if constexpr (MODE == 1) {
-        store_ring_row<D, G8>(rk, rks, slot, H, rs.h[i], lane, xk[i]);
-        store_ring_row<D, G8>(rv, rvs, slot, H, rs.h[i], lane, xv[i]);
-      } else {
-        store_pool_row<D>(k4, ks4, slot, H, rs.h[i], lane, xk[i]);
-        store_pool_row<D>(v4, vs4, slot, H, rs.h[i], lane, xv[i]);
-      }
-    }
+    store_pool_row<D>(k4, ks4, slot, H, h, lane, xk);
+    store_pool_row<D>(v4, vs4, slot, H, h, lane, xv);
   }
 }
 
@@ -366,11 +341,12 @@ KVT_DEV void store_pool_requant(uint8_t* pbuf, uint16_t* pscale, int64_t row, in
   if ((lane & 7) == 0) pscale[(row * H + h) * NG4 + lane / 8] = sb;
 }
 
-// Position-indexed ring append with eviction.  Each wavefront handles kRowsPerWave rows, lane l < kRowsPerWave
-// loading the metadata of row l, in three dependent rounds: (1) sequence id and position, with the new K/V inputs
-// of every row right behind; (2) the sequence's ring placement; (3) the page-table entry, with the ring rows being
-// overwritten.  Then per row: the new token's INT8 row takes the ring row's place and the evicted row, held in
-// registers, is requantized into its INT4 page.
+// Position-indexed ring append with eviction, one (token, head) row per wavefront.  The new K/V inputs are
+// loaded first; the row's metadata is wave-uniform and read with scalar loads (their counter is separate from the
+// vector loads', so the chain does not wait for the inputs), in dependency levels held apart by scheduling
+// barriers: sequence id and position; the sequence's ring placement; then the ring row being overwritten (vector
+// loads, none when nothing is evicted) and its page-table entry.  The new token's INT8 row then takes the ring
+// row's place and the evicted row, held in registers, is requantized into its INT4 page.
 template <int DT, int G8, int LM>
 __global__ void __launch_bounds__(256) append_evict_kernel(
     RowIn kin, RowIn vin, const int32_t* seq_ids, const int64_t* positions, uint32_t NH, int H, uint8_t* k4,
@@ -378,46 +354,37 @@ __global__ void __launch_bounds__(256) append_evict_kernel(
     const int64_t* ring_base, const int32_t* ring_len, const int64_t* ring_start, const int32_t* page_table,
     int64_t pt_stride, const uint16_t* sm_k_inv, const uint16_t* sm_v_inv) {
   constexpr int D = 256;
-  constexpr int R = kRowsPerWave;
   const int lane = threadIdx.x & 63;
-  uint32_t lt;
-  const uint32_t item0 = wave_rows(R, NH, H, lane, &lt);
-  if (item0 >= NH) return;
-  const int lsq = seq_ids[lt];
-  const int64_t lp = positions[lt];
-  const RowSet<R> rs(item0, NH, H);
+  uint32_t t;
+  int h;
+  if (!wave_row(NH, H, &t, &h)) return;
   const int c0 = 4 * lane;
-  float xk[R][4], xv[R][4];
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    load4<DT, LM>(kin, rs.t[i], rs.h[i], c0, sm_k_inv, D, xk[i]);
-    load4<DT, LM>(vin, rs.t[i], rs.h[i], c0, sm_v_inv, D, xv[i]);
-  }
-  const int64_t llen = ring_len[lsq];
-  const int64_t lr = ring_base[lsq] + (lp & (llen - 1));
-  const int64_t le = lp - llen;  // the position whose ring row this token overwrites
-  const bool lev = le >= ring_start[lsq];
-  const uint64_t ev = __ballot(lev);
-  int64_t r[R];
-  RingRow old[R];
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    r[i] = readlane64(lr, i);
-    old[i] = load_ring_row<D, G8>(rk, rv, rks, rvs, r[i], H, rs.h[i], lane, (ev >> i) & 1);
-  }
-  const int pg = page_table[lsq * pt_stride + (lev ? le >> 6 : 0)];  // entry 0 of the row when unused
-  const int64_t lrow = lev && pg >= 0 ? (int64_t)pg * kPage + (le & (kPage - 1)) : -1;  // INT4 row of the evictee
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    if (!rs.ok[i]) continue;
-    // The new row goes in first: its stores alias the old row's loads, which keeps those loads up front.
-    store_ring_row<D, G8>(rk, rks, r[i], H, rs.h[i], lane, xk[i]);
-    store_ring_row<D, G8>(rv, rvs, r[i], H, rs.h[i], lane, xv[i]);
-    const int64_t row = readlane64(lrow, i);
-    if (row >= 0) {
-      store_pool_requant<D>(k4, ks4, row, H, rs.h[i], lane, old[i].ck, old[i].sk);
-      store_pool_requant<D>(v4, vs4, row, H, rs.h[i], lane, old[i].cv, old[i].sv);
-    }
+  const In4 rk_in = load4_raw<DT, LM>(kin, t, h, c0, sm_k_inv, D);
+  const In4 rv_in = load4_raw<DT, LM>(vin, t, h, c0, sm_v_inv, D);
+  __builtin_amdgcn_sched_barrier(0);
+  const int sq = seq_ids[t];
+  const int64_t p = positions[t];
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t len = ring_len[sq];
+  const int64_t base = ring_base[sq];
+  const int64_t start = ring_start[sq];
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t r = base + (p & (len - 1));
+  const int64_t e = p - len;  // the position whose ring row this token overwrites
+  const bool ev = e >= start;
+  const RingRow old = load_ring_row<D, G8>(rk, rv, rks, rvs, r, H, h, lane, ev);
+  const int pg = page_table[sq * pt_stride + (ev ? e >> 6 : 0)];  // entry 0 of the row when unused
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t row = ev && pg >= 0 ? (int64_t)pg * kPage + (e & (kPage - 1)) : -1;  // INT4 row of the evictee
+  float xk[4], xv[4];
+  to_f32<DT, LM>(rk_in, xk);
+  to_f32<DT, LM>(rv_in, xv);
+  // The new row goes in first: its stores alias the old row's loads, which keeps those loads up front.
+  store_ring_row<D, G8>(rk, rks, r, H, h, lane, xk);
+  store_ring_row<D, G8>(rv, rvs, r, H, h, lane, xv);
+  if (row >= 0) {
+    store_pool_requant<D>(k4, ks4, row, H, h, lane, old.ck, old.sk);
+    store_pool_requant<D>(v4, vs4, row, H, h, lane, old.cv, old.sv);
   }
 }
 
@@ -445,8 +412,7 @@ int launch_quant_store(const RowIn& kin, const RowIn& vin, int dtype, const void
                        int D, int group8, uint8_t* k4, uint8_t* v4, uint16_t* ks4, uint16_t* vs4, int8_t* rk,
                        int8_t* rv, uint16_t* rks, uint16_t* rvs, const int32_t* owner, const uint16_t* smk,
                        const uint16_t* smv, int64_t ring_mask, hipStream_t stream) {
-  if (N > (int64_t)(UINT32_MAX / 8)) return KVT_EINVAL;  // slot indices are read through a 32-bit buffer range
-  const dim3 grid((unsigned)((N * H + kRowsPerBlock - 1) / kRowsPerBlock));
+  const dim3 grid((unsigned)((N * H + kWavesPerBlock - 1) / kWavesPerBlock));
   const int lm = load_mode(kin, vin, dtype, smk, smv);
   const uint32_t NH = (uint32_t)(N * H);
 #define KVT_QS1(DT_, D_, G_, LM_)                                                                                  \
@@ -560,7 +526,7 @@ int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int6
                      int64_t pt_stride, const void* sm_k_inv, const void* sm_v_inv, int group8, void* stream) {
   if (N < 0 || H <= 0 || N > INT32_MAX / H) return KVT_EINVAL;
   if (N == 0) return KVT_OK;
-  const dim3 grid((unsigned)((N * H + kRowsPerBlock - 1) / kRowsPerBlock));
+  const dim3 grid((unsigned)((N * H + kWavesPerBlock - 1) / kWavesPerBlock));
   hipStream_t st = (hipStream_t)stream;
   const RowIn kin{k, sk_n, sk_h}, vin{v, sv_n, sv_h};
   const int lm = load_mode(kin, vin, dtype, sm_k_inv, sm_v_inv);

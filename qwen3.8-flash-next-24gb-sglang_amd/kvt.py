@@ -195,6 +195,14 @@ class PosTieredCache:
             tot += (self.h_len[s] - hs) * hot_b + hs * cold_b
         return tot
 
+    def append_bytes(self, n: int, n_evicted: int, in_bytes: int = 2) -> int:
+        """HBM bytes one append of n tokens moves per layer when n_evicted of them overwrite a ring row that goes
+        to an INT4 page: K and V inputs (in_bytes per element) read, INT8 rows + scales written, and per eviction
+        the INT8 row + scales read and the INT4 row + scales written; plus the sequence id and position per token."""
+        ring_row = self.H * 2 * (self.D + 2 * (self.D // self.group8))
+        pool_row = self.H * 2 * (self.D // 2 + 2 * (self.D // G4))
+        return n * (self.H * 2 * self.D * in_bytes + ring_row + 12) + n_evicted * (ring_row + pool_row)
+
 
 def _choose_chunk(max_len: int, items: int, lo: int = 64, hi: int = 512) -> int:
     """Tokens per split for the reference-precision kernel: enough work items to fill the chip (>= 512 blocks),
