@@ -212,6 +212,82 @@ def qwen_sparse_kv_extraction_compact_triton(
               out_v.data_ptr(), _lib.stream())
 
 
+def qwen_sparse_decode_attn(
+    q, k, v, req_to_token, req_indices, indices, seq_lens, cu_k, batch, topk,
+    k_scale=None, v_scale=None, sm_k=None, sm_v=None, kv_bits=None,
+    ring_k=None, ring_v=None, ring_ks=None, ring_vs=None, owner=None, ring_mask=None,
+    scale=None, out=None, workspace=None,
+):
+    """Top-k sparse decode attention fused over the quantized pool: what qwen_sparse_kv_extraction_compact_triton
+    followed by FlashAttention-2 over its bf16 scratch computes for one query row per request (flat patch
+    sglang/qwen4exp-serving-73a255206f.patch:1832-1882), in one split-K launch + the combine, with no scratch.
+
+    q: bf16 [batch, Hq, D]; the pool/ring/owner/scale arguments as the compact gather; cu_k: the valid counts'
+    prefix sum (qwen_sparse_fa2_cu_seqlens_triton).  Column c of request b is attended when c < cu_k[b+1] - cu_k[b]
+    and 0 <= indices[b, c] < seq_lens[b].  Returns out (fp32 [batch, Hq, D] unless a bf16/fp32 `out` is given);
+    a request with no attended column gives NaN.  `workspace` (a dict) keeps the partial buffers across calls."""
+    _, heads, dim = k.shape
+    if k.dtype == torch.uint8 and kv_bits == 4 and owner is not None:
+        dim = 2 * dim
+        R = _check_tier_args(heads, dim, k_scale, v_scale, ring_k, ring_v, ring_ks, ring_vs, owner, ring_mask)
+        kind, g8 = _KIND_TIERED, _group8(dim, ring_ks)
+    elif k.dtype == torch.uint8 and kv_bits == 4:
+        dim = 2 * dim
+        assert k_scale.shape[1:] == (heads, dim // KV_INT4_GROUP) and k_scale.is_contiguous() and v_scale.is_contiguous()
+        R, kind, g8 = 1, _KIND_INT4, KV_INT8_GROUP
+    elif k.dtype == torch.int8:
+        assert k_scale.is_contiguous() and v_scale.is_contiguous()
+        R, kind, g8 = 1, _KIND_INT8, _group8(dim, k_scale)
+    else:
+        raise NotImplementedError(f"pool dtype {k.dtype} / kv_bits {kv_bits}: only the int8_g64, int4_g32 and "
+                                  "int8ring_int4 pools are served by this library")
+    assert k.is_contiguous() and v.is_contiguous() and dim == 256, "the kernel is built for head_dim 256"
+    assert q.dim() == 3 and q.shape[0] >= batch and q.shape[2] == dim and q.dtype == torch.bfloat16
+    assert q.stride(2) == 1 and q.stride(1) == dim and q.stride(0) % 8 == 0
+    Hq = q.shape[1]
+    assert Hq % heads == 0 and Hq // heads <= 16
+    assert sm_k is None or sm_k.shape == (heads, dim)
+    assert sm_v is None or sm_v.shape == (heads, dim)
+    assert req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1
+    assert indices.dtype == torch.int32 and indices.stride(-1) == 1
+    assert seq_lens.dtype == torch.int32 and seq_lens.is_contiguous()
+    if out is None:
+        out = torch.empty(batch, Hq, dim, dtype=torch.float32, device=q.device)
+    assert out.shape[0] >= batch and out.shape[1:] == (Hq, dim) and out.stride(2) == 1 and out.stride(1) == dim
+    assert out.dtype in (torch.float32, torch.bfloat16)
+    if batch == 0:
+        return out
+    if topk == 0:
+        out[:batch] = float("nan")
+        return out
+    _lib.require_device(q, k, v, req_to_token, indices, out)
+    scale = float(dim ** -0.5) if scale is None else float(scale)
+    n_splits = (int(topk) + 15) // 16
+    ws = workspace if workspace is not None else {}
+    need = batch * heads * n_splits * (Hq // heads)
+    if ws.get("sparse_o") is None or ws["sparse_o"].numel() < need * dim:
+        ws["sparse_o"] = torch.empty(need * dim, dtype=torch.float32, device=q.device)
+        ws["sparse_ml"] = torch.empty(need * 2, dtype=torch.float32, device=q.device)
+    rq, rq64 = _idx_args(req_indices)
+    cu, cu64 = _idx_args(cu_k)
+    tier = kind == _KIND_TIERED
+    smk = None if sm_k is None else sm_k.contiguous()
+    smv = None if sm_v is None else sm_v.contiguous()
+    st = _lib.stream()
+    _lib.call("kvt_sparse_decode", kind, q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k_scale.data_ptr(),
+              v_scale.data_ptr(), _lib.ptr(ring_k) if tier else None, _lib.ptr(ring_v) if tier else None,
+              _lib.ptr(ring_ks) if tier else None, _lib.ptr(ring_vs) if tier else None,
+              _lib.ptr(owner) if tier else None, R - 1, _lib.ptr(smk), _lib.ptr(smv), req_to_token.data_ptr(),
+              req_to_token.stride(0), rq, rq64, indices.data_ptr(), indices.stride(0), seq_lens.data_ptr(), cu, cu64,
+              int(batch), int(topk), heads, Hq, dim, g8, scale, n_splits, ws["sparse_o"].data_ptr(),
+              ws["sparse_ml"].data_ptr(), st)
+    o32 = out.data_ptr() if out.dtype == torch.float32 else None
+    o16 = out.data_ptr() if out.dtype == torch.bfloat16 else None
+    _lib.call("kvt_decode_combine", ws["sparse_o"].data_ptr(), ws["sparse_ml"].data_ptr(), int(batch), heads, Hq, dim,
+              n_splits, 0, seq_lens.data_ptr(), None, o32, o16, out.stride(0), st)
+    return out
+
+
 def _prefix_gather(kind, k, v, k_scale, v_scale, sm_k, sm_v, req_to_token, req_indices, seq_lens, cu_k, out_k, out_v,
                    batch, max_len, dim, g8, tier=None):
     assert out_k.is_contiguous() and out_v.is_contiguous()
