@@ -296,6 +296,107 @@ def append_workload(args) -> dict:
     }
 
 
+def sparse_workload(args) -> dict:
+    """Top-k sparse decode over the tiered (slot-indexed) pool: 8 requests of 65,536 tokens on randomly allocated
+    slots, 12 layers, 2,051 selected positions per request (distinct, random), INT8-G64 ring of 8,192 rows whose
+    owner table names one slot per row.  Times one HIP graph of the 12 layers' fused top-k decode (split-K +
+    combine) and, for scale, one of the 12 layers' gathers into the bf16 scratch alone (the reference's unfused
+    path runs an attention over that scratch on top).  Synthetic random codes and scales."""
+    import kvtier  # noqa: F401
+    from kvtier import sparse_attn as sa
+    B, CTX, TOPK, R = 8, 65_536, 2051, 8192
+    slots = B * CTX
+    g = torch.Generator(device="cuda").manual_seed(41)
+    gc = torch.Generator().manual_seed(41)
+
+    def layer_pool():
+        return dict(
+            k4=torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, device="cuda", generator=g),
+            v4=torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, device="cuda", generator=g),
+            ks4=(0.05 + 0.3 * torch.rand(slots, H, D // 32, device="cuda", generator=g)).half(),
+            vs4=(0.05 + 0.3 * torch.rand(slots, H, D // 32, device="cuda", generator=g)).half(),
+            rk=torch.randint(-127, 128, (R, H, D), dtype=torch.int8, device="cuda", generator=g),
+            rv=torch.randint(-127, 128, (R, H, D), dtype=torch.int8, device="cuda", generator=g),
+            rks=(0.002 + 0.02 * torch.rand(R, H, D // 64, device="cuda", generator=g)).half(),
+            rvs=(0.002 + 0.02 * torch.rand(R, H, D // 64, device="cuda", generator=g)).half())
+
+    pools = [layer_pool() for _ in range(LAYERS)]
+    owner = (torch.arange(R, dtype=torch.int64) + R * torch.randint(0, slots // R, (R,), generator=gc)).to(torch.int32)
+    owner = owner.to("cuda")
+    r2t = torch.randperm(slots, generator=gc).to(torch.int32).reshape(B, CTX).to("cuda")
+    req_idx = torch.arange(B, dtype=torch.int64, device="cuda")
+    idx = torch.stack([torch.randperm(CTX, generator=gc)[:TOPK] for _ in range(B)]).to(torch.int32).to("cuda")
+    seq_lens = torch.full((B,), CTX, dtype=torch.int32, device="cuda")
+    counts = torch.empty(B, dtype=torch.int32, device="cuda")
+    cu_k = torch.empty(B + 1, dtype=torch.int32, device="cuda")
+    sa.qwen_sparse_fa2_cu_seqlens_triton(seq_lens, idx, counts, cu_k, B, TOPK)
+    sm = (0.5 + torch.rand(H, D, device="cuda", generator=g)).half()
+    q = [(torch.randn(B, HQ, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty(B, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
+    ws = [{} for _ in range(LAYERS)]
+    scr_k = torch.empty(B * TOPK, H, D, dtype=torch.bfloat16, device="cuda")
+    scr_v = torch.empty_like(scr_k)
+    # gathered bytes per layer: each selected position's K and V rows of both heads from its tier
+    sel = r2t.gather(1, idx.long()).long()
+    hot = (owner.long()[sel & (R - 1)] == sel)
+    n_hot = int(hot.sum())
+    n_cold = hot.numel() - n_hot
+    bytes_layer = H * 2 * (n_hot * (D + 2 * (D // 64)) + n_cold * (D // 2 + 2 * (D // 32)))
+
+    def fused():
+        for layer in range(LAYERS):
+            pl = pools[layer]
+            sa.qwen_sparse_decode_attn(q[layer], pl["k4"], pl["v4"], r2t, req_idx, idx, seq_lens, cu_k, B, TOPK,
+                                       pl["ks4"], pl["vs4"], sm, sm, 4, pl["rk"], pl["rv"], pl["rks"], pl["rvs"],
+                                       owner, R - 1, out=outs[layer], workspace=ws[layer])
+
+    def gather():
+        for layer in range(LAYERS):
+            pl = pools[layer]
+            sa.qwen_sparse_kv_extraction_compact_triton(pl["k4"], pl["v4"], r2t, req_idx, idx, seq_lens, cu_k, scr_k,
+                                                        scr_v, B, TOPK, pl["ks4"], pl["vs4"], sm, sm, 4, pl["rk"],
+                                                        pl["rv"], pl["rks"], pl["rvs"], owner, R - 1)
+
+    def graph_time(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        for _ in range(max(1, args.warmup)):
+            gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(1, args.steps)
+        e0.record()
+        for _ in range(reps):
+            gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    t_fused = graph_time(fused)
+    t_gather = graph_time(gather)
+    gbps = bytes_layer * LAYERS / t_fused / 1e9
+    return {
+        "metric": "top-k sparse decode, fused (12 layers, batch 8, topk 2051): us per step", "value":
+            round(t_fused * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
+        "warmup": args.warmup, "dtype": "bf16-mfma/f32", "data": "synthetic",
+        "config": {"workload": "8 requests x 65,536 tokens on random slots, 12 layers, 16 Q / 2 KV heads, D 256, "
+                               "2,051 selected positions each, tiered pool (INT8-G64 ring of 8,192 rows + INT4-G32)",
+                   "hot_fraction": round(n_hot / hot.numel(), 4)},
+        "gather_only_us_per_step": round(t_gather * 1e6, 1),
+        "kv_bytes_per_layer": bytes_layer,
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
+                     "kernel": "sparse_decode + combine (per layer)"},
+    }
+
+
 def decode_steps_workload(args, ragged: bool) -> dict:
     """ragged = False: one layer, 10,001-token context (ring 8192 + 1,809 paged positions), 1,000 steps of
     append-one-token + decode.  ragged = True: 8 sequences with log-uniform lengths in [1024, 65536] (seeded), 12
@@ -397,7 +498,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fused-combine", action="store_true",
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
-    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append"],
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
@@ -415,7 +516,8 @@ def main():
         sys.exit(2)
     if args.workload != "decode262k":
         fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
-              "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload}[args.workload]
+              "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload,
+              "sparse": sparse_workload}[args.workload]
         line = fn(args)
         line["n_gpus"] = 1
         print(json.dumps(line))

@@ -35,8 +35,8 @@ SIGNATURES = {
                          _P, _L, _P, _P, _I, _P],
     "kvt_compact_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P, _P, _I,
                            _I, _I, _I, _I, _I, _P, _P, _P],
-    "kvt_sparse_decode": [_I, _P, _L, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P,
-                          _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P],
+    "kvt_sparse_decode": [_I, _P, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L,
+                          _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P],
     "kvt_prefix_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _P, _I, _I, _L,
                           _I, _I, _I, _P, _P, _P],
     "kvt_decode_ref": [_I, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -245,7 +245,7 @@ def qwen_sparse_decode_attn(
     assert q.dim() == 3 and q.shape[0] >= batch and q.shape[2] == dim and q.dtype == torch.bfloat16
     assert q.stride(2) == 1 and q.stride(1) == dim and q.stride(0) % 8 == 0
     Hq = q.shape[1]
-    assert Hq % heads == 0 and Hq // heads <= 16
+    assert Hq % heads == 0 and Hq // heads <= 8
     assert sm_k is None or sm_k.shape == (heads, dim)
     assert sm_v is None or sm_v.shape == (heads, dim)
     assert req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1
@@ -262,7 +262,7 @@ def qwen_sparse_decode_attn(
         return out
     _lib.require_device(q, k, v, req_to_token, indices, out)
     scale = float(dim ** -0.5) if scale is None else float(scale)
-    n_splits = (int(topk) + 15) // 16
+    n_splits = (int(topk) + 63) // 64   # 64 selected columns per wavefront
     ws = workspace if workspace is not None else {}
     need = batch * heads * n_splits * (Hq // heads)
     if ws.get("sparse_o") is None or ws["sparse_o"].numel() < need * dim:
@@ -275,7 +275,7 @@ def qwen_sparse_decode_attn(
     smv = None if sm_v is None else sm_v.contiguous()
     st = _lib.stream()
     _lib.call("kvt_sparse_decode", kind, q.data_ptr(), q.stride(0), k.data_ptr(), v.data_ptr(), k_scale.data_ptr(),
-              v_scale.data_ptr(), _lib.ptr(ring_k) if tier else None, _lib.ptr(ring_v) if tier else None,
+              v_scale.data_ptr(), k.shape[0], _lib.ptr(ring_k) if tier else None, _lib.ptr(ring_v) if tier else None,
               _lib.ptr(ring_ks) if tier else None, _lib.ptr(ring_vs) if tier else None,
               _lib.ptr(owner) if tier else None, R - 1, _lib.ptr(smk), _lib.ptr(smv), req_to_token.data_ptr(),
               req_to_token.stride(0), rq, rq64, indices.data_ptr(), indices.stride(0), seq_lens.data_ptr(), cu, cu64,
