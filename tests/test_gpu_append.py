@@ -375,3 +375,44 @@ def test_unaligned_rows_all_writers(kvt_pkg, dt):
     assert torch.equal(dc.page_table.cpu(), oc.page_table(16))
     for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
         assert torch.equal(getattr(dc, name)[0].cpu(), getattr(oc, name)), name
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_writers_other_head_dims(kvt_pkg, d):
+    """head_dim 64 and 128 (a row uses D / 4 lanes; INT8 groups of 64 or the whole row): INT4, INT8 and tiered
+    writers bit-exact vs the oracle, aligned rows and rows of stride H * d + 1 (element loads)."""
+    from kvtier import sparse_attn as sa
+    gen = torch.Generator().manual_seed(40 + d)
+    n, slots, R = 300, 1024, 64
+    x = (torch.randn(n, H, d, generator=gen) * 3).to(torch.bfloat16)
+    smi = (0.5 + 1.5 * torch.rand(H, d, generator=gen)).half()
+    loc = torch.randperm(slots, generator=gen)[:n]
+    wide = torch.zeros(n, H * d + 1, dtype=torch.bfloat16)
+    wide[:, :H * d] = x.reshape(n, H * d)
+    for xd in (x.to(dev), wide.to(dev)[:, :H * d].view(n, H, d)):
+        k4 = torch.zeros(slots, H, d // 2, dtype=torch.uint8, device=dev); v4 = torch.zeros_like(k4)
+        ks4 = torch.zeros(slots, H, d // 32, dtype=torch.float16, device=dev); vs4 = torch.zeros_like(ks4)
+        sa.quant_store_kv_int4(xd, xd, loc.to(dev), k4, v4, ks4, vs4, smi.to(dev), smi.to(dev))
+        p4, s4 = ref.quant4(x, sm_inv=smi)
+        assert torch.equal(k4.cpu()[loc], p4) and torch.equal(ks4.cpu()[loc], s4)
+        for g8 in sorted({64, d}):
+            k8 = torch.zeros(slots, H, d, dtype=torch.int8, device=dev); v8 = torch.zeros_like(k8)
+            ks8 = torch.zeros(slots, H, d // g8, dtype=torch.float16, device=dev); vs8 = torch.zeros_like(ks8)
+            sa.quant_store_kv_int8(xd, xd, loc.to(dev), k8, v8, ks8, vs8, smi.to(dev), smi.to(dev))
+            q8, s8 = ref.quant8(x, group=g8, sm_inv=smi)
+            assert torch.equal(k8.cpu()[loc], q8) and torch.equal(ks8.cpu()[loc], s8), g8
+        # tiered: alias-free slots (distinct ring rows), so every row is hot
+        tl = (torch.randperm(slots // R, generator=gen)[:1] * R + torch.randperm(R, generator=gen)[:48])
+        b = [t.to(dev) for t in (
+            torch.zeros(slots, H, d // 2, dtype=torch.uint8), torch.zeros(slots, H, d // 2, dtype=torch.uint8),
+            torch.zeros(slots, H, d // 32, dtype=torch.float16), torch.zeros(slots, H, d // 32, dtype=torch.float16),
+            torch.zeros(R, H, d, dtype=torch.int8), torch.zeros(R, H, d, dtype=torch.int8),
+            torch.zeros(R, H, d // 64, dtype=torch.float16), torch.zeros(R, H, d // 64, dtype=torch.float16),
+            torch.full((R,), -1, dtype=torch.int32))]
+        sa.quant_store_kv_tiered(xd[:48], xd[:48], tl.to(dev), *b, smi.to(dev), smi.to(dev), R - 1)
+        q8, s8 = ref.quant8(x[:48], sm_inv=smi)
+        p4, s4 = ref.quant4(x[:48], sm_inv=smi)
+        r = tl & (R - 1)
+        assert torch.equal(b[4].cpu()[r], q8) and torch.equal(b[6].cpu()[r], s8)
+        assert torch.equal(b[0].cpu()[tl], p4) and torch.equal(b[2].cpu()[tl], s4)
+        assert torch.equal(b[8].cpu()[r].long(), tl)
