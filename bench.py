@@ -401,8 +401,9 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     """ragged = False: one layer, 10,001-token context (ring 8192 + 1,809 paged positions), 1,000 steps of
     append-one-token + decode.  ragged = True: 8 sequences with log-uniform lengths in [1024, 65536] (seeded), 12
     layers, two sequences sharing a 4,096-token prefix in common pages, 256 iterations of one decode step per
-    sequence (append + decode of every layer).  Reports us per step (wall, host planning included) and the KV GB/s of
-    the decode launches."""
+    sequence (append + decode of every layer).  Reports us per step (wall, host planning included), the KV GB/s of
+    the decode launches as timed by events around the eager calls, and the decode of the final state replayed as a
+    HIP graph (the device's own rate)."""
     import kvtier  # noqa: F401
     from kvtier.kvt import PosTieredCache, kvt_decode_attn
     layers = LAYERS if ragged else 1
@@ -477,6 +478,32 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
     dec_s = sum(a.elapsed_time(c) for a, _, c in ev) / 1e3 / steps
+    # the device's decode time: the final state's decode of every layer replayed as one HIP graph (the eager events
+    # above include the host's launch gaps whenever Python is slower than the kernels)
+    kv_last = cache.kv_bytes(seqs) * layers
+
+    def dec_only():
+        for layer in range(layers):
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dec_only()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dec_only()
+    graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for _ in range(20):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    dec_graph = g0.elapsed_time(g1) / 1e3 / 20
     name = ("ragged decode: 8 sequences, 12 layers, shared 4,096-token prefix, 256 iterations" if ragged
             else "decode with append: 10,001-token context, 1 layer, 1,000 steps")
     return {
@@ -486,6 +513,8 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         "decode_us_per_step": round(dec_s * 1e6, 1),
         "decode_kv_GBps": round(kv_bytes / dec_s / 1e9, 1),
         "kv_bytes_per_step": kv_bytes,
+        "decode_graph_us_per_step": round(dec_graph * 1e6, 1),
+        "decode_graph_kv_GBps": round(kv_last / dec_graph / 1e9, 1),
     }
 
 
