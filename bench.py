@@ -86,6 +86,73 @@ def cpu_baseline(cache, q, layer: int = 0):
                        f"({nbytes} KV bytes, {dt:.2f} s)")
 
 
+def _cpu_threads() -> int:
+    torch.set_num_threads(os.cpu_count() or 1)
+    return torch.get_num_threads()
+
+
+def cpu_baseline_append(n: int = RING, reps: int = 3) -> dict:
+    """The reference's torch write arithmetic on the host cores (oracle/ref.py, vectorized over tokens): INT8-G64
+    quantization of n new K and V rows and INT4-G32 requantization of n evicted ring rows; GB/s of the same
+    algorithmic bytes as the GPU line."""
+    from oracle import ref
+    cores = _cpu_threads()
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, H, D, generator=g).to(torch.bfloat16)
+    q8 = torch.randint(-127, 128, (n, H, D), dtype=torch.int8, generator=g)
+    s8 = (0.002 + 0.02 * torch.rand(n, H, D // 64, generator=g)).half()
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ref.quant8(k)
+        ref.quant8(v)
+        ref.requant8to4(q8, s8)
+        ref.requant8to4(q8, s8)
+        best = min(best, time.perf_counter() - t0)
+    ring_row = H * 2 * (D + 2 * (D // 64))
+    pool_row = H * 2 * (D // 2 + 2 * (D // 32))
+    nbytes = n * (H * 2 * D * 2 + ring_row + 12) + n * (ring_row + pool_row)
+    return dict(value=round(nbytes / best / 1e9, 3), unit="GB/s", cores=cores, kind="port",
+                sample=f"oracle/ref.py quant8 of {n} K and V rows + requant8to4 of {n} evicted K and V ring rows, "
+                       f"one layer ({best * 1e3:.1f} ms, best of {reps})")
+
+
+def cpu_baseline_sparse(pool: dict, owner, r2t, idx, q, R: int, sm) -> dict:
+    """The reference's CPU path for one layer of the top-k decode (oracle/ref.py): dequantize every request's
+    selected slots as the gather writes them, then fp32 attention; us per layer."""
+    from oracle import ref
+    cores = _cpu_threads()
+    cpu = {k: v.cpu() for k, v in pool.items()}
+    own, rt, ix, qc, smc = owner.cpu(), r2t.cpu(), idx.cpu(), q.cpu(), sm.cpu()
+    t0 = time.perf_counter()
+    for b in range(ix.shape[0]):
+        slots = rt[b, ix[b].long()]
+        kk, vv = ref.dequant_slots_tiered(slots, cpu["k4"], cpu["v4"], cpu["ks4"], cpu["vs4"], cpu["rk"], cpu["rv"],
+                                          cpu["rks"], cpu["rvs"], own, R - 1, smc, smc)
+        ref.attention_rows(qc[b], kk, vv, D ** -0.5)
+    dt = time.perf_counter() - t0
+    return dict(value=round(dt * 1e6, 1), unit="us per layer", cores=cores, kind="port",
+                sample=f"oracle/ref.py dequant_slots_tiered + attention_rows of {ix.shape[0]} requests x "
+                       f"{ix.shape[1]} selected positions, one layer ({dt * 1e3:.1f} ms)")
+
+
+def cpu_baseline_prefill(k_rows, v_rows, q_rows, a: int) -> dict:
+    """The reference's CPU attention form (oracle/ref.py attention_rows) for a sample of prefill queries: query j of
+    the sample sits at position a + j and attends to dequantized positions 0 .. a + j; TFLOP/s (causal flops)."""
+    from oracle import ref
+    cores = _cpu_threads()
+    n = q_rows.shape[0]
+    t0 = time.perf_counter()
+    for j in range(n):
+        ref.attention_rows(q_rows[j], k_rows[:a + j + 1], v_rows[:a + j + 1], D ** -0.5)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * HQ * D * sum(a + j + 1 for j in range(n))
+    return dict(value=round(flops / dt / 1e12, 4), unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"oracle/ref.py attention_rows of {n} queries at positions {a}..{a + n - 1} over the "
+                       f"dequantized cache of one layer ({dt * 1e3:.1f} ms)")
+
+
 CAL_BYTES = 256 * 1024 * 1024   # the calibration copy: 256 MiB read + 256 MiB written
 
 
@@ -189,9 +256,12 @@ def prefill_workload(args) -> dict:
     cus = {n: torch.tensor([0, n], dtype=torch.int32, device="cuda") for _, n in chunks}
     outs = [torch.empty(CH, HQ, D, dtype=torch.bfloat16, device="cuda") for _ in range(LAYERS)]
 
+    last = {}
+
     def run(events=None):
         cache = PosTieredCache(LAYERS, H, D, n_pages=n_pages, ring_total=RING, max_seqs=1, max_pages=n_pages + 1,
                                device="cuda", page_seed=0)
+        last["cache"] = cache
         cache.add_seq(RING)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -222,6 +292,17 @@ def prefill_workload(args) -> dict:
     t_prompt = min(times)
     t_prefill = sum(a.elapsed_time(b) for a, b in ev) / 1e3 / args.steps
     flops = 4.0 * HQ * D * (N * (N + 1) // 2) * LAYERS
+    cpu = None
+    if not args.no_cpu_baseline:   # the last 64 queries of layer 0 over its dequantized cache (oracle rows)
+        from oracle import ref
+        cache = last["cache"]
+        oc = ref.PosTieredCache.__new__(ref.PosTieredCache)
+        oc.H, oc.D, oc.group8 = H, D, cache.group8
+        for name in ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs"):
+            setattr(oc, name, getattr(cache, name)[0].cpu())
+        oc.seqs = [ref.SeqState(0, RING, 0, cache.h_len[0], list(cache.h_pages[0]))]
+        kk, vv = oc.rows(0)
+        cpu = cpu_baseline_prefill(kk, vv, qs[0][N - 64:].cpu(), N - 64)
     return {
         "metric": "chunked prefill 10,001 tokens x 12 layers: ms per prompt (append + evict + causal prefill)",
         "value": round(t_prompt * 1e3, 3), "unit": "ms", "higher_is_better": False, "steps": args.steps,
@@ -232,6 +313,7 @@ def prefill_workload(args) -> dict:
                      "unit": "TFLOP/s", "frac": round(flops / t_prefill / 2.5e15, 4), "traffic": None,
                      "kernel": "prefill (causal, all chunks and layers)", "kernel_ms": round(t_prefill * 1e3, 3),
                      "flops": flops},
+        "cpu_baseline": cpu,
     }
 
 
@@ -284,6 +366,7 @@ def append_workload(args) -> dict:
     t_launch = e0.elapsed_time(e1) / 1e3 / (reps * S * LAYERS)
     nbytes = cache.append_bytes(N, N)
     gbps = nbytes / t_launch / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_append(N)
     return {
         "metric": "quantize-append with ring eviction: GB/s of algorithmic HBM bytes (8,192 tokens per launch)",
         "value": round(gbps, 1), "unit": "GB/s", "higher_is_better": True, "steps": reps, "warmup": args.warmup,
@@ -293,6 +376,7 @@ def append_workload(args) -> dict:
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None, "kernel": "append_evict",
                      "bytes_per_launch": nbytes},
+        "cpu_baseline": cpu,
     }
 
 
@@ -382,6 +466,7 @@ def sparse_workload(args) -> dict:
     t_fused = graph_time(fused)
     t_gather = graph_time(gather)
     gbps = bytes_layer * LAYERS / t_fused / 1e9
+    cpu = None if args.no_cpu_baseline else cpu_baseline_sparse(pools[0], owner, r2t, idx, q[0], R, sm)
     return {
         "metric": "top-k sparse decode, fused (12 layers, batch 8, topk 2051): us per step", "value":
             round(t_fused * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
@@ -394,6 +479,7 @@ def sparse_workload(args) -> dict:
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
                      "kernel": "sparse_decode + combine (per layer)"},
+        "cpu_baseline": cpu,
     }
 
 
