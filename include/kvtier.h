@@ -2,11 +2,14 @@
  *
  * Conventions (every entry point):
  *   - all tensor memory is owned and allocated by the caller (device pointers of torch tensors); the library
- *     keeps no state and allocates nothing;
+ *     keeps no state and allocates nothing -- except the kvt_vmm_* arena entry points at the end, whose purpose
+ *     is to reserve device address space and back it with physical memory on demand;
  *   - work is enqueued on `stream` (a hipStream_t, e.g. torch.cuda.current_stream().cuda_stream); no entry point
  *     synchronizes the host, grid sizes depend only on the integer arguments (capture-safe);
  *   - the return value is KVT_OK (0) or a negative status: KVT_EINVAL (-1) unsupported shape / dtype / size,
- *     KVT_ELAUNCH (-2) the launch failed, KVT_ERANGE (-3) a size beyond a documented maximum.
+ *     KVT_ELAUNCH (-2) the launch failed, KVT_ERANGE (-3) a size beyond a documented maximum; the arena entry
+ *     points add KVT_ENOTSUP (-4) no virtual memory management on the device, KVT_ENOMEM (-5) no address space
+ *     or physical memory, KVT_EHIP (-6) another HIP runtime failure.
  *
  * Layouts (reference: patches/kv_int4.py:57-60, patches/kv_tiers.py:63-67):
  *   INT4 pool   k_buf/v_buf uint8 [rows, H, D/2] (low nibble = even channel, q + 8);
@@ -29,6 +32,9 @@ extern "C" {
 #define KVT_EINVAL -1
 #define KVT_ELAUNCH -2
 #define KVT_ERANGE -3
+#define KVT_ENOTSUP -4
+#define KVT_ENOMEM -5
+#define KVT_EHIP -6
 
 /* ----------------------------------------------------------------------------------------- write path */
 
@@ -191,6 +197,40 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
                      const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
                      int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
                      void* stream);
+
+/* ----------------------------------------------------------------------------- lazy backing (HIP VMM) */
+
+/* Lazily backed device memory for the KV pool (reference: patches/kv_lazy.py -- the pool is reserved as address
+ * space for the whole context and backed in steps as pages are handed out; beyond a floor the backing goes back to
+ * the driver when the pool is idle).  An arena is one reserved range on `device`; its first `backed` bytes are
+ * mapped read-write for that device, the rest is address space only -- a kernel must not touch it.  Every call is
+ * host-synchronous; calls that unmap wait for the device's queued work first (hipDeviceSynchronize).  A failed
+ * runtime call is also reported on stderr (which call, offset, size, the runtime's message). */
+
+/* Mapping granularity of the arenas: 2 MiB (a multiple of the runtime's recommended granularity): every mapping is
+ * whole granules at granule-aligned addresses.  KVT_ENOTSUP without VMM. */
+int kvt_vmm_granularity(int device, uint64_t* granularity);
+
+/* Reserve `bytes` (rounded up to the granularity) of address space; nothing is backed yet.  Returns the arena
+ * handle and its base address.  Replaces the VMM owner's reservation (SGLang's kv_vmm_backing owner, used in
+ * lazy mode by patches/kv_lazy.py:100-106). */
+int kvt_vmm_reserve(int device, uint64_t bytes, void** arena, void** base);
+
+/* Back the prefix [0, bytes) (rounded up to the granularity) -- one new physical allocation for the part not yet
+ * backed; a smaller or equal size is a no-op (commits only grow); KVT_ERANGE past the reservation, KVT_ENOMEM when
+ * the device has no physical memory for it (the arena is unchanged then).  Replaces ensure_prefix
+ * (patches/kv_lazy.py:70-75). */
+int kvt_vmm_commit(void* arena, uint64_t bytes);
+
+/* Unmap and free every mapping that starts at or beyond align_up(keep_bytes, granularity); mappings straddling
+ * that cut stay (patches/kv_lazy.py:39-63 uncommit_beyond).  *freed (may be NULL) = bytes returned. */
+int kvt_vmm_release_beyond(void* arena, uint64_t keep_bytes, uint64_t* freed);
+
+/* Backed bytes, reserved bytes and number of mappings (any pointer may be NULL). */
+int kvt_vmm_backed(void* arena, uint64_t* bytes, uint64_t* reserved, uint64_t* n_mappings);
+
+/* Unmap and free everything and give the address space back; NULL is a no-op. */
+int kvt_vmm_destroy(void* arena);
 
 #ifdef __cplusplus
 }

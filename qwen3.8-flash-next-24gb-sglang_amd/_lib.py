@@ -17,12 +17,14 @@ LIB_PATH = os.path.join(HERE, "libkvtier.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "kvtier.h")
 
 KVT_OK, KVT_EINVAL, KVT_ELAUNCH, KVT_ERANGE = 0, -1, -2, -3
+KVT_ENOTSUP, KVT_ENOMEM, KVT_EHIP = -4, -5, -6
 DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _L = ctypes.c_int64
 _F = ctypes.c_float
+_U = ctypes.c_uint64
 
 # argument types per entry point, in declaration order (must match include/kvtier.h)
 SIGNATURES = {
@@ -46,6 +48,12 @@ SIGNATURES = {
     "kvt_decode_combine": [_P, _P, _I, _I, _I, _I, _I, _L, _P, _P, _P, _P, _L, _P],
     "kvt_prefill_attn": [_P, _L, _L, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _L, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _I, _L, _L, _P],
+    "kvt_vmm_granularity": [_I, _P],
+    "kvt_vmm_reserve": [_I, _U, _P, _P],
+    "kvt_vmm_commit": [_P, _U],
+    "kvt_vmm_release_beyond": [_P, _U, _P],
+    "kvt_vmm_backed": [_P, _P, _P, _P],
+    "kvt_vmm_destroy": [_P],
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -95,4 +103,10 @@ def call(name: str, *args) -> None:
         raise ValueError(f"{name}: unsupported shape, dtype or size (status {status})")
     if status == KVT_ERANGE:
         raise ValueError(f"{name}: size beyond the supported maximum (status {status})")
+    if status == KVT_ENOTSUP:
+        raise RuntimeError(f"{name}: the device does not support virtual memory management (status {status})")
+    if status == KVT_ENOMEM:
+        raise RuntimeError(f"{name}: out of device address space or physical memory (status {status})")
+    if status == KVT_EHIP:
+        raise RuntimeError(f"{name}: HIP runtime call failed (status {status})")
     raise RuntimeError(f"{name}: kernel launch failed (status {status})")

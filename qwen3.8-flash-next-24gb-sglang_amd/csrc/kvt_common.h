@@ -100,6 +100,9 @@ KVT_DEV uint32_t pack_pair(float qe, float qo) {
 #define KVT_EINVAL -1       // a shape / size / dtype argument the kernel does not support
 #define KVT_ELAUNCH -2      // hipGetLastError after the launch
 #define KVT_ERANGE -3       // a size beyond a documented maximum
+#define KVT_ENOTSUP -4      // the device lacks a needed capability (virtual memory management)
+#define KVT_ENOMEM -5       // the HIP runtime could not provide address space or physical memory
+#define KVT_EHIP -6         // another HIP runtime call failed
 #define KVT_DECODE_DYNAMIC 1   // kvt_decode_mfma flag: tiles to wavefronts first come
 
 #define KVT_CHECK_LAUNCH()                                   \

@@ -5,13 +5,14 @@
 // values come from the cache tiers (INT4 pages below hot_start, INT8 ring above) or, for a chunk without a prefix,
 // from the chunk's own bf16 K/V (the reference attends to fresh bf16 K/V there).
 //
-// Work item = (sequence, KV head, tile of 16 queries), 4 wavefronts, heaviest (latest) query tiles first.  The block
-// walks the keys in tiles of 32 positions.  All 256 threads dequantize a tile ONCE into LDS as fp16 (K row-major,
-// V transposed), with the next tile's codes already loaded into registers during the matrix work on the current one;
-// the four wavefronts then reuse it for their 4 queries x 8 heads = 32 rows (dequantizing per query row is what made
-// the reference's fused kernel slow, docs/KV_PAGED_PREFIX_PLAN.md:188-191).
-//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 K rows x 32 channels from LDS (shared by the wavefront's two
-//   16-row blocks), B = Q (rows = 2 queries x 8 heads) held in registers, pre-multiplied by scale * log2(e).  The D
+// Work item = (sequence, KV head, tile of 16 queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
+// first.  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as fp16
+// (threads 0-255 the K tile row-major, threads 256-511 the V tile transposed), with the next tile's codes already
+// loaded into registers during the matrix work on the current one; the eight wavefronts then reuse it for their
+// 2 queries x 8 heads = 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
+// docs/KV_PAGED_PREFIX_PLAN.md:188-191).
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 K rows x 32 channels from LDS, B = Q (rows = 2 queries x 8
+//   heads) held in registers, pre-multiplied by scale * log2(e).  The D
 //   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
 //   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
 //   O += P V on the same instruction: B = V^T rows from LDS (two 8-byte reads per 16-dim column block).

@@ -4,8 +4,10 @@ Mirrors the reference's pool classes (``MHATokenToKVPoolInt8`` patches/kv_int8.p
 ``MHATokenToKVPoolInt4`` patches/kv_int4.py:81-227, ``MHATokenToKVPoolTiered`` patches/kv_tiers.py:103-229) with
 the same attributes, accessors, guards and exceptions, standalone (no SGLang base class: the upstream
 ``MHATokenToKVPool`` parts they use -- buffer lists, size/page_size/layer bookkeeping -- are restated here).
-Writes go through the HIP kernels (sparse_attn.quant_store_kv_*).  Lazy VMM backing and CPU offload are not
-provided (CPU offload raises NotImplementedError exactly like the reference).
+Writes go through the HIP kernels (sparse_attn.quant_store_kv_*).  With lazy=True (or SGLANG_KV_LAZY=1, as the
+reference's patches/kv_lazy.py:100-106) the per-slot buffers live on HIP virtual memory and are backed on demand
+(lazy_kv.LazyKVBacking; the ring and owner table stay eagerly allocated); ``PagedTokenAllocator`` mirrors the
+allocator hooks that drive it.  CPU offload is not provided (it raises NotImplementedError like the reference).
 """
 from __future__ import annotations
 
@@ -15,6 +17,7 @@ from typing import Optional, Tuple
 
 import torch
 
+from .lazy_kv import LazyKVBacking
 from .sparse_attn import KV_INT4_GROUP, KV_INT8_GROUP, quant_store_kv_int4, quant_store_kv_int8, quant_store_kv_tiered
 
 logger = logging.getLogger(__name__)
@@ -52,7 +55,9 @@ class _QuantKVPool:
 
     def __init__(self, size: int, page_size: int, dtype: torch.dtype, head_num: int, head_dim: int, layer_num: int,
                  device, enable_memory_saver: bool = False, start_layer: int = 0, v_head_dim: Optional[int] = None,
-                 **unused):
+                 lazy: Optional[bool] = None, **unused):
+        self.lazy = (os.environ.get("SGLANG_KV_LAZY") == "1") if lazy is None else bool(lazy)
+        self._lazy = None
         self.size = size
         self.page_size = page_size
         self.dtype = dtype
@@ -102,6 +107,18 @@ class _QuantKVPool:
     def _create_buffers(self):
         (ksh, vsh) = self._kv_buffer_shapes()
         ks_shape, vs_shape = self._scale_shapes()
+        if self.lazy:
+            # address space for every slot, the floor backed now (patches/kv_lazy.py:100-106)
+            lz = LazyKVBacking(self._rows(), self.size, self.page_size, self.device)
+            self.k_buffer = [lz.add(ksh, self.store_dtype) for _ in range(self.layer_num)]
+            self.v_buffer = [lz.add(vsh, self.store_dtype) for _ in range(self.layer_num)]
+            self.k_scale_buffer = [lz.add(ks_shape, torch.float16) for _ in range(self.layer_num)]
+            self.v_scale_buffer = [lz.add(vs_shape, torch.float16) for _ in range(self.layer_num)]
+            lz.ensure_prefix(lz.floor)
+            self._lazy = lz
+            logger.info("KV lazy backing: %d tokens reserved as VA, %d backed (floor), margin %d, %.1f KB/token",
+                        self.size, lz.floor, lz.margin, lz.bytes_per_token() / 1024)
+            return
         self.k_buffer = [torch.zeros(ksh, dtype=self.store_dtype, device=self.device) for _ in range(self.layer_num)]
         self.v_buffer = [torch.zeros(vsh, dtype=self.store_dtype, device=self.device) for _ in range(self.layer_num)]
         self.k_scale_buffer = [torch.zeros(ks_shape, dtype=torch.float16, device=self.device)
@@ -111,6 +128,7 @@ class _QuantKVPool:
 
     def _clear_buffers(self):
         self.k_buffer = self.v_buffer = self.k_scale_buffer = self.v_scale_buffer = None
+        self._lazy = None
 
     # -- accessors
     def get_key_buffer(self, layer_id: int) -> torch.Tensor:
@@ -159,8 +177,21 @@ class _QuantKVPool:
     def load_cpu_copy(self, kv_cache_cpu, indices, mamba_indices=None):
         raise NotImplementedError(f"{type(self).__name__}: CPU offload is not supported")
 
+    # -- lazy backing (patches/kv_lazy.py:113-175); no-ops on an eagerly allocated pool
+    @property
+    def lazy_backed_tokens(self) -> int:
+        """Slots [0, n) are backed (every slot of an eager pool)."""
+        return self._rows() if self._lazy is None else self._lazy.backed_tokens
+
+    def lazy_ensure(self, num_tokens: int) -> None:
+        """Back slots [0, num_tokens + margin) in margin steps (RuntimeError when the device cannot)."""
+        if self._lazy is not None:
+            self._lazy.ensure(num_tokens)
+
     def lazy_release(self) -> None:
-        """No lazy VMM backing here: nothing to release."""
+        """Unmap the backing beyond the floor (the pool is idle: no slot in use)."""
+        if self._lazy is not None:
+            self._lazy.release()
 
 
 class MHATokenToKVPoolInt8(_QuantKVPool):
@@ -297,7 +328,68 @@ class MHATokenToKVPoolTiered(MHATokenToKVPoolInt4):
                               self.ring_mask)
 
     def lazy_release(self) -> None:
-        """Hygiene only: reset the owner table (patches/kv_tiers.py:224-229)."""
+        """Release the lazy backing, and reset the owner table (patches/kv_tiers.py:224-229)."""
         super().lazy_release()
         if self.ring_owner is not None:
             self.ring_owner.fill_(-1)
+
+
+class PagedTokenAllocator:
+    """Page-granular slot allocator with the lazy-backing hooks of the reference (SGLang's
+    PagedTokenToKVPoolAllocator as patched by patches/kv_lazy.py:207-283): pages 1 .. size // page_size in
+    slot order; ``alloc`` backs the slots of the pages it is about to hand out (kvcache.lazy_ensure((max page + 1) *
+    page_size)) and refuses (returns None, pages stay free) when that fails; when every page is free again the list
+    returns to slot order and the pool's backing beyond the floor is released (kvcache.lazy_release())."""
+
+    def __init__(self, size: int, page_size: int, kvcache, device="cpu"):
+        if size % page_size:
+            raise ValueError(f"size {size} is not a multiple of page_size {page_size}")
+        self.size = size
+        self.page_size = page_size
+        self.num_pages = size // page_size
+        self._kvcache = kvcache
+        self.device = device
+        self.clear()
+
+    def clear(self) -> None:
+        self.free_pages = torch.arange(1, self.num_pages + 1, dtype=torch.int64)
+
+    def available_size(self) -> int:
+        return int(self.free_pages.numel()) * self.page_size
+
+    def _lazy_hook(self, pages: torch.Tensor) -> bool:
+        ensure = getattr(self._kvcache, "lazy_ensure", None)
+        if ensure is None or pages.numel() == 0:
+            return True
+        try:
+            ensure((int(pages.max()) + 1) * self.page_size)
+            return True
+        except Exception as ex:
+            logger.warning("KV lazy backing: commit failed, allocation refused (%s)", ex)
+            return False
+
+    def alloc(self, need_size: int) -> Optional[torch.Tensor]:
+        """``need_size`` slots (a multiple of page_size) as int64 slot indices, or None when the pool is full or
+        their backing cannot be committed."""
+        if need_size % self.page_size:
+            raise ValueError(f"need_size {need_size} is not a multiple of page_size {self.page_size}")
+        n = need_size // self.page_size
+        if n > self.free_pages.numel():
+            return None
+        out_pages = self.free_pages[:n]
+        if not self._lazy_hook(out_pages):
+            return None
+        self.free_pages = self.free_pages[n:]
+        idx = (out_pages[:, None] * self.page_size + torch.arange(self.page_size, dtype=torch.int64)).reshape(-1)
+        return idx.to(self.device)
+
+    def free(self, free_index: torch.Tensor) -> None:
+        if free_index.numel() == 0:
+            return
+        pages = torch.unique(free_index.to("cpu", torch.int64) // self.page_size)
+        self.free_pages = torch.cat((pages, self.free_pages))
+        if self.free_pages.numel() >= self.num_pages:   # pool idle: slot order + give the memory back
+            release = getattr(self._kvcache, "lazy_release", None)
+            self.clear()
+            if release is not None:
+                release()
