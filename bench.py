@@ -380,6 +380,30 @@ def append_workload(args) -> dict:
     }
 
 
+def _graph_time(fn, warmup: int, reps: int) -> float:
+    """Seconds per replay of a HIP graph of fn() (captured after one eager run on a side stream)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        fn()
+    for _ in range(max(1, warmup)):
+        gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(1, reps)
+    e0.record()
+    for _ in range(reps):
+        gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
 def sparse_workload(args) -> dict:
     """Top-k sparse decode over the tiered (slot-indexed) pool: 8 requests of 65,536 tokens on randomly allocated
     slots, 12 layers, 2,051 selected positions per request (distinct, random), INT8-G64 ring of 8,192 rows whose
@@ -442,26 +466,7 @@ def sparse_workload(args) -> dict:
                                                         pl["rv"], pl["rks"], pl["rvs"], owner, R - 1)
 
     def graph_time(fn):
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
-            fn()
-        for _ in range(max(1, args.warmup)):
-            gr.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = max(1, args.steps)
-        e0.record()
-        for _ in range(reps):
-            gr.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / reps
+        return _graph_time(fn, args.warmup, args.steps)
 
     t_fused = graph_time(fused)
     t_gather = graph_time(gather)
@@ -480,6 +485,117 @@ def sparse_workload(args) -> dict:
                      "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
                      "kernel": "sparse_decode + combine (per layer)"},
         "cpu_baseline": cpu,
+    }
+
+
+def lazy_workload(args) -> dict:
+    """Lazy backing of the tiered slot pool on HIP virtual memory at the full context: 262,144 slots x 12 layers
+    (2 KV heads, D 256; INT8 ring of 8,192 rows eagerly allocated).  Times, host wall with the device synchronized:
+    the pool's construction (48 reservations + the 4,096-token floor), the growth from the floor to the full pool in
+    2,048-token hand-outs of PagedTokenAllocator (each backs the next 2,048 slots of all 48 buffers and zeroes them,
+    14.2 MB), and the release back to the floor once every slot is free.  Then two readers of the pool as 12-layer
+    HIP graphs, over the lazily backed pool and over an eagerly allocated one of the same shape: the fused top-k
+    decode (8 requests x 32,768 slots, 2,051 random positions each: random rows) and the whole-prefix
+    gather-dequant (every slot, streaming).  Pool contents are the zeros of fresh backing (timing only)."""
+    import kvtier  # noqa: F401
+    from kvtier import sparse_attn as sa
+    from kvtier.tiered_kv_pool import MHATokenToKVPoolTiered, PagedTokenAllocator
+    SIZE, STEP, B, TOPK = 262_144, 2048, 8, 2051
+    CTXB = SIZE // B
+
+    def pool(lazy):
+        return MHATokenToKVPoolTiered(SIZE, PAGE, torch.uint8, H, D, LAYERS, "cuda", lazy=lazy)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    lz = pool(True)
+    torch.cuda.synchronize()
+    t_build = time.perf_counter() - t0
+    alloc = PagedTokenAllocator(SIZE, PAGE, lz, device="cuda")
+    step_s, chunks = [], []
+    while alloc.available_size() >= STEP:
+        t0 = time.perf_counter()
+        idx = alloc.alloc(STEP)
+        torch.cuda.synchronize()
+        step_s.append(time.perf_counter() - t0)
+        if idx is None:
+            raise RuntimeError(f"lazy backing refused a hand-out at {len(chunks) * STEP} slots")
+        chunks.append(idx)
+    backed_full = lz.lazy_backed_tokens
+    step_bytes = STEP * lz._lazy.bytes_per_token()
+    eager = pool(False)
+    gc = torch.Generator().manual_seed(43)
+    g = torch.Generator(device="cuda").manual_seed(43)
+    r2t = torch.cat(chunks).to(torch.int32).reshape(B, CTXB).contiguous()
+    req_idx = torch.arange(B, dtype=torch.int64, device="cuda")
+    idx = torch.stack([torch.randperm(CTXB, generator=gc)[:TOPK] for _ in range(B)]).to(torch.int32).to("cuda")
+    seq_lens = torch.full((B,), CTXB, dtype=torch.int32, device="cuda")
+    cu_k = torch.tensor([i * TOPK for i in range(B + 1)], dtype=torch.int32, device="cuda")
+    cu_p = torch.tensor([i * CTXB for i in range(B + 1)], dtype=torch.int32, device="cuda")
+    q = [(torch.randn(B, HQ, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty(B, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
+    scr_k = torch.empty(SIZE, H, D, dtype=torch.bfloat16, device="cuda")
+    scr_v = torch.empty_like(scr_k)
+
+    def readers(p):
+        ws = [{} for _ in range(LAYERS)]
+
+        def fused():
+            for layer in range(LAYERS):
+                k, v = p.get_kv_buffer(layer)
+                ks, vs = p.get_kv_scale_buffer(layer)
+                sk, sv = p.get_kv_smooth_buffer(layer)
+                rk, rv, rks, rvs = p.get_kv_ring_buffer(layer)
+                sa.qwen_sparse_decode_attn(q[layer], k, v, r2t, req_idx, idx, seq_lens, cu_k, B, TOPK, ks, vs, sk, sv,
+                                           4, rk, rv, rks, rvs, p.ring_owner, p.ring_mask, out=outs[layer],
+                                           workspace=ws[layer])
+
+        def prefix():
+            for layer in range(LAYERS):
+                k, v = p.get_kv_buffer(layer)
+                ks, vs = p.get_kv_scale_buffer(layer)
+                sk, sv = p.get_kv_smooth_buffer(layer)
+                rk, rv, rks, rvs = p.get_kv_ring_buffer(layer)
+                sa.qwen_sparse_prefix_gather_dequant_tiered(k, v, ks, vs, sk, sv, r2t, req_idx, seq_lens, cu_p, scr_k,
+                                                            scr_v, B, CTXB, rk, rv, rks, rvs, p.ring_owner,
+                                                            p.ring_mask)
+        return (_graph_time(fused, args.warmup, args.steps), _graph_time(prefix, args.warmup, args.steps))
+
+    t_fused_l, t_prefix_l = readers(lz)
+    t_fused_e, t_prefix_e = readers(eager)
+    del eager
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for c in chunks:
+        alloc.free(c)
+    t_release = time.perf_counter() - t0
+    backed_after = lz.lazy_backed_tokens
+    step_s.sort()
+    med = step_s[len(step_s) // 2]
+    fused_bytes = LAYERS * B * TOPK * H * 2 * (D // 2 + 2 * (D // 32))        # INT4 rows + scales of both heads
+    prefix_bytes = LAYERS * SIZE * H * 2 * (D // 2 + 2 * (D // 32) + 2 * D)   # + the bf16 rows written
+    gbps = fused_bytes / t_fused_l / 1e9
+    return {
+        "metric": "lazy KV backing (12-layer 262,144-slot tiered pool): us per 2,048-token commit step",
+        "value": round(med * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
+        "warmup": args.warmup, "dtype": "u8/f16 (pool)", "data": "synthetic (zeros of fresh backing)",
+        "config": {"workload": "262,144-slot tiered pool x 12 layers on HIP VMM (2 MiB granules), floor 4,096, "
+                               "margin 2,048; readers: top-k decode 8 x 2,051 of 32,768, whole-prefix gather"},
+        "commit_steps": len(step_s), "commit_bytes_per_step": step_bytes,
+        "commit_us": {"median": round(med * 1e6, 1), "min": round(step_s[0] * 1e6, 1),
+                      "max": round(step_s[-1] * 1e6, 1),
+                      "mean": round(sum(step_s) / len(step_s) * 1e6, 1)},
+        "commit_GBps_median": round(step_bytes / med / 1e9, 2),
+        "build_ms": round(t_build * 1e3, 2), "release_ms": round(t_release * 1e3, 2),
+        "backed_tokens": {"full": backed_full, "after_release": backed_after},
+        "sparse_decode_us_per_step": {"lazy": round(t_fused_l * 1e6, 1), "eager": round(t_fused_e * 1e6, 1)},
+        "prefix_gather_us_per_step": {"lazy": round(t_prefix_l * 1e6, 1), "eager": round(t_prefix_e * 1e6, 1)},
+        "prefix_gather_GBps": {"lazy": round(prefix_bytes / t_prefix_l / 1e9, 1),
+                               "eager": round(prefix_bytes / t_prefix_e / 1e9, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
+                     "kernel": "sparse_decode + combine over the lazily backed pool (per layer)"},
+        "cpu_baseline": None,
     }
 
 
@@ -613,7 +729,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fused-combine", action="store_true",
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
-    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse"],
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "lazy"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
@@ -632,7 +748,7 @@ def main():
     if args.workload != "decode262k":
         fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
               "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload,
-              "sparse": sparse_workload}[args.workload]
+              "sparse": sparse_workload, "lazy": lazy_workload}[args.workload]
         line = fn(args)
         line["n_gpus"] = 1
         print(json.dumps(line))

@@ -88,7 +88,8 @@ int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int6
  * (k/v are the int8 codes, ring arguments unused), 1 = INT4 pool, 2 = tiered (owner test per row).  Replaces
  * qwen_sparse_kv_extraction_compact_triton's int8 / int4 / tiered branches (_compact_kv_int8
  * patches/kv_int8.py:365-420, _compact_kv_int4 patches/kv_int4.py:396-460, _compact_kv_tiered
- * patches/kv_tiers.py:446-538, wrapper :688-737). */
+ * patches/kv_tiers.py:446-538, wrapper :688-737).  Pointer alignment (else KVT_EINVAL): INT4 codes 4 bytes, INT8
+ * codes and ring codes 8 bytes, out_k / out_v 16 bytes (any torch allocation or row slice of one qualifies). */
 int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_scale, const void* v_scale,
                        const void* ring_k, const void* ring_v, const void* ring_ks, const void* ring_vs,
                        const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,
@@ -118,7 +119,8 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
 
 /* Whole-prefix gather-dequant: rows [0, seq_lens[b]) of request req_indices[b] packed at cu_k[b]; rows at or
  * beyond seq_lens[b] are not written.  Replaces qwen_sparse_prefix_gather_dequant_{int8,int4,tiered}
- * (patches/kv_int8.py:469-504, patches/kv_int4.py:519-557, patches/kv_tiers.py:639-683). */
+ * (patches/kv_int8.py:469-504, patches/kv_int4.py:519-557, patches/kv_tiers.py:639-683).  Pointer alignment as
+ * kvt_compact_gather. */
 int kvt_prefix_gather(int kind, const void* k, const void* v, const void* k_scale, const void* v_scale,
                       const void* ring_k, const void* ring_v, const void* ring_ks, const void* ring_vs,
                       const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,

@@ -1,9 +1,14 @@
 // Gather-dequant kernels of the tiered KV cache (drop-in for the reference's compact and prefix gathers).
 //
-// One wavefront per (output row, KV head); lane l produces channels 4l..4l+3 as bf16 (one 8-byte store), reading
-// 2 bytes of INT4 codes or 4 bytes of INT8 codes plus its group's fp16 scale.  The tier is decided per row on the
-// device: hot = owner[slot & mask] == slot (patches/kv_tiers.py:500-504).  Only valid rows are written (store mask
-// = valid, patches/kv_tiers.py:476-480: the trtllm strided scratch relies on it).
+// A wavefront writes kRows output rows (all KV heads, K and V).  Lane l owns unit u = l (+ 64, ... while u < H D / 8):
+// KV head u / (D / 8), channels 8 (u % (D / 8)) .. + 7, whose smoothing constants it loads once.  Per row it reads
+// 4 bytes of INT4 codes (or 8 bytes of INT8 codes) and one fp16 group scale for K and for V, and stores 16 bytes of
+// bf16 for each: a row of one tensor is one contiguous read and one contiguous 1 KiB store across the wavefront.
+// All rows' loads go out before the first conversion.  The row -> slot chain (request, req_to_token, owner) is
+// wave-uniform scalar work.  The tier is decided per row on the device: hot = owner[slot & mask] == slot
+// (patches/kv_tiers.py:500-504).  Only valid rows are written (store mask = valid, patches/kv_tiers.py:476-480: the
+// trtllm strided scratch relies on it).  Values: bf16(code * s * sm) in fp32 (patches/kv_tiers.py:519-525), rounded
+// to nearest even by v_cvt_pk_bf16_f32.
 //
 //   kvt_compact_gather  top-k selection -> packed rows (patches/kv_tiers.py:446-538, :688-737;
 //                       patches/kv_int4.py:396-460; patches/kv_int8.py:365-420)
@@ -33,101 +38,173 @@ struct Pools {
   int64_t ring_mask;
 };
 
+constexpr int kRows = 4;     // rows per wavefront
+constexpr int kWaves = 4;    // wavefronts per block
+
+// bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
+KVT_DEV uint32_t bf16x2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+
+// The raw codes and scale of one unit of one row: INT4 (w.x, 8 nibbles) or INT8 (w.x, w.y, 8 bytes).
+struct Raw {
+  uint2 w;
+  uint16_t s;
+};
+
 template <int D, int G8>
-KVT_DEV void dequant_int8_lane(const int8_t* codes, const uint16_t* scales, int64_t row, int H, int h, int lane,
-                               const uint16_t* sm, uint16_t out[4]) {
+KVT_DEV Raw load_int8(const int8_t* codes, const uint16_t* scales, int64_t row, int H, int h, int cg) {
   constexpr int NG8 = D / G8;
-  const uint32_t c = reinterpret_cast<const uint32_t*>(codes + (row * H + h) * D)[lane];
-  const float s = f16_bits_to_f32(scales[(row * H + h) * NG8 + (4 * lane) / G8]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float m = f16_bits_to_f32(sm[h * D + 4 * lane + i]);
-    out[i] = bf16_rne((float)(int8_t)(c >> (8 * i)) * s * m);  // q * s * sm (patches/kv_tiers.py:525)
-  }
+  Raw r;
+  r.w = *reinterpret_cast<const uint2*>(codes + (row * H + h) * D + 8 * cg);
+  r.s = scales[(row * H + h) * NG8 + (8 * cg) / G8];
+  return r;
 }
 
 template <int D>
-KVT_DEV void dequant_int4_lane(const uint8_t* codes, const uint16_t* scales, int64_t row, int H, int h, int lane,
-                               const uint16_t* sm, uint16_t out[4]) {
-  constexpr int NG4 = D / kG4;
-  const uint32_t b = reinterpret_cast<const uint16_t*>(codes + (row * H + h) * (D / 2))[lane];
-  const float s = f16_bits_to_f32(scales[(row * H + h) * NG4 + lane / 8]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float m = f16_bits_to_f32(sm[h * D + 4 * lane + i]);
-    const int n = (int)((b >> (4 * i)) & 15u) - 8;
-    out[i] = bf16_rne((float)n * s * m);  // ((b & 15) - 8) * s * sm (patches/kv_tiers.py:519-523)
-  }
+KVT_DEV Raw load_int4(const uint8_t* codes, const uint16_t* scales, int64_t row, int H, int h, int cg) {
+  Raw r;
+  r.w.x = *reinterpret_cast<const uint32_t*>(codes + (row * H + h) * (D / 2) + 4 * cg);
+  r.w.y = 0;
+  r.s = scales[(row * H + h) * (D / kG4) + cg / 4];
+  return r;
 }
 
+KVT_DEV uint4 dequant8(const Raw& r, const float m[8]) {   // q * s * sm (patches/kv_tiers.py:525)
+  const float s = f16_bits_to_f32(r.s);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)(int8_t)((i < 4 ? r.w.x : r.w.y) >> (8 * (i & 3))) * s * m[i];
+  return make_uint4(bf16x2(x[0], x[1]), bf16x2(x[2], x[3]), bf16x2(x[4], x[5]), bf16x2(x[6], x[7]));
+}
+
+KVT_DEV uint4 dequant4(const Raw& r, const float m[8]) {   // ((b & 15) - 8) * s * sm (patches/kv_tiers.py:519-523)
+  const float s = f16_bits_to_f32(r.s);
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)((int)((r.w.x >> (4 * i)) & 15u) - 8) * s * m[i];
+  return make_uint4(bf16x2(x[0], x[1]), bf16x2(x[2], x[3]), bf16x2(x[4], x[5]), bf16x2(x[6], x[7]));
+}
+
+// kRows rows of one wavefront: slot[j] (wave-uniform; < 0 = row not written) -> output row dst[j].
 template <int KIND, int D, int G8>
-KVT_DEV void gather_row(const Pools& P, int64_t slot, int H, int h, int lane, uint16_t* out_k, uint16_t* out_v,
-                        int64_t dst) {
-  uint16_t ok[4], ov[4];
-  if constexpr (KIND == 0) {
-    dequant_int8_lane<D, G8>(reinterpret_cast<const int8_t*>(P.k), P.ks, slot, H, h, lane, P.sm_k, ok);
-    dequant_int8_lane<D, G8>(reinterpret_cast<const int8_t*>(P.v), P.vs, slot, H, h, lane, P.sm_v, ov);
-  } else {
-    bool hot = false;
-    int64_t r = 0;
+KVT_DEV void gather_rows(const Pools& P, const int64_t slot[kRows], const int64_t dst[kRows], int H, int lane,
+                         uint16_t* out_k, uint16_t* out_v) {
+  bool hot[kRows];
+  int64_t ring[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    hot[j] = KIND == 0;
+    ring[j] = 0;
     if constexpr (KIND == 2) {
-      r = slot & P.ring_mask;
-      hot = (int64_t)P.owner[r] == slot;
-    }
-    if (hot) {
-      dequant_int8_lane<D, G8>(P.rk, P.rks, r, H, h, lane, P.sm_k, ok);
-      dequant_int8_lane<D, G8>(P.rv, P.rvs, r, H, h, lane, P.sm_v, ov);
-    } else {
-      dequant_int4_lane<D>(P.k, P.ks, slot, H, h, lane, P.sm_k, ok);
-      dequant_int4_lane<D>(P.v, P.vs, slot, H, h, lane, P.sm_v, ov);
+      if (slot[j] >= 0) {
+        ring[j] = slot[j] & P.ring_mask;
+        hot[j] = (int64_t)P.owner[ring[j]] == slot[j];
+      }
     }
   }
-  const uint2 wk = make_uint2((uint32_t)ok[0] | ((uint32_t)ok[1] << 16), (uint32_t)ok[2] | ((uint32_t)ok[3] << 16));
-  const uint2 wv = make_uint2((uint32_t)ov[0] | ((uint32_t)ov[1] << 16), (uint32_t)ov[2] | ((uint32_t)ov[3] << 16));
-  reinterpret_cast<uint2*>(out_k + (dst * H + h) * D)[lane] = wk;
-  reinterpret_cast<uint2*>(out_v + (dst * H + h) * D)[lane] = wv;
+  constexpr int CG = D / 8;
+  const int U = H * CG;
+  for (int u = lane; u < U; u += 64) {
+    const int h = u / CG, cg = u - h * CG;
+    float mk[8], mv[8];   // once per unit (element loads: the constants need only 2-byte alignment)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      mk[i] = f16_bits_to_f32(P.sm_k[h * D + 8 * cg + i]);
+      mv[i] = f16_bits_to_f32(P.sm_v[h * D + 8 * cg + i]);
+    }
+    Raw rk[kRows], rv[kRows];
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      if (slot[j] < 0) continue;
+      if constexpr (KIND == 0) {
+        rk[j] = load_int8<D, G8>(reinterpret_cast<const int8_t*>(P.k), P.ks, slot[j], H, h, cg);
+        rv[j] = load_int8<D, G8>(reinterpret_cast<const int8_t*>(P.v), P.vs, slot[j], H, h, cg);
+      } else {
+        if (hot[j]) {
+          rk[j] = load_int8<D, G8>(P.rk, P.rks, ring[j], H, h, cg);
+          rv[j] = load_int8<D, G8>(P.rv, P.rvs, ring[j], H, h, cg);
+        } else {
+          rk[j] = load_int4<D>(P.k, P.ks, slot[j], H, h, cg);
+          rv[j] = load_int4<D>(P.v, P.vs, slot[j], H, h, cg);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRows; ++j) {
+      if (slot[j] < 0) continue;
+      const uint4 ok = hot[j] ? dequant8(rk[j], mk) : dequant4(rk[j], mk);
+      const uint4 ov = hot[j] ? dequant8(rv[j], mv) : dequant4(rv[j], mv);
+      *reinterpret_cast<uint4*>(out_k + (dst[j] * H + h) * D + 8 * cg) = ok;
+      *reinterpret_cast<uint4*>(out_v + (dst[j] * H + h) * D + 8 * cg) = ov;
+    }
+  }
 }
 
 KVT_DEV int64_t ld_idx(const void* p, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t) reinterpret_cast<const int32_t*>(p)[i];
 }
 
-// grid.x = column blocks of 4, grid.y = batch * H
+KVT_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// grid.x = column blocks of kWaves * kRows, grid.y = batch
 template <int KIND, int D, int G8>
-__global__ void __launch_bounds__(256) compact_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
-                                                      const void* req_indices, int req64, const int32_t* indices,
-                                                      int64_t idx_stride, const int32_t* seq_lens, const void* cu_k,
-                                                      int cu64, int topk, int H, uint16_t* out_k, uint16_t* out_v) {
+__global__ void __launch_bounds__(64 * kWaves) compact_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
+                                                              const void* req_indices, int req64,
+                                                              const int32_t* indices, int64_t idx_stride,
+                                                              const int32_t* seq_lens, const void* cu_k, int cu64,
+                                                              int topk, int H, uint16_t* out_k, uint16_t* out_v) {
   const int lane = threadIdx.x & 63;
-  const int col = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int b = blockIdx.y / H;
-  const int h = blockIdx.y - b * H;
-  if (col >= topk || lane >= D / 4) return;
+  const int64_t col0 = ((int64_t)blockIdx.x * kWaves + wave_id()) * kRows;
+  const int b = blockIdx.y;
+  if (col0 >= topk) return;
   const int64_t length = seq_lens[b];
   const int64_t start = ld_idx(cu_k, cu64, b);
   const int64_t vcount = ld_idx(cu_k, cu64, b + 1) - start;
-  const int64_t pos = indices[(int64_t)b * idx_stride + col];
-  if (!(col < vcount && pos >= 0 && pos < length)) return;  // store mask = valid
   const int64_t req = ld_idx(req_indices, req64, b);
-  const int64_t slot = req_to_token[req * req_stride + pos];
-  gather_row<KIND, D, G8>(P, slot, H, h, lane, out_k, out_v, start + col);
+  int64_t slot[kRows], dst[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int64_t col = col0 + j;
+    slot[j] = -1;
+    dst[j] = start + col;
+    if (col < topk && col < vcount) {
+      const int64_t pos = indices[(int64_t)b * idx_stride + col];
+      if (pos >= 0 && pos < length) slot[j] = req_to_token[req * req_stride + pos];   // store mask = valid
+    }
+  }
+  gather_rows<KIND, D, G8>(P, slot, dst, H, lane, out_k, out_v);
 }
 
-// grid.x = row blocks of 4, grid.y = batch * H
+// grid.x = row blocks of kWaves * kRows, grid.y = batch
 template <int KIND, int D, int G8>
-__global__ void __launch_bounds__(256) prefix_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
-                                                     const void* req_indices, int req64, const int32_t* seq_lens,
-                                                     const void* cu_k, int cu64, int H, uint16_t* out_k,
-                                                     uint16_t* out_v) {
+__global__ void __launch_bounds__(64 * kWaves) prefix_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
+                                                             const void* req_indices, int req64,
+                                                             const int32_t* seq_lens, const void* cu_k, int cu64,
+                                                             int H, uint16_t* out_k, uint16_t* out_v) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int b = blockIdx.y / H;
-  const int h = blockIdx.y - b * H;
-  if (lane >= D / 4) return;
-  if (t >= (int64_t)seq_lens[b]) return;
+  const int64_t t0 = ((int64_t)blockIdx.x * kWaves + wave_id()) * kRows;
+  const int b = blockIdx.y;
+  const int64_t length = seq_lens[b];
+  if (t0 >= length) return;
   const int64_t req = ld_idx(req_indices, req64, b);
-  const int64_t slot = req_to_token[req * req_stride + t];
-  gather_row<KIND, D, G8>(P, slot, H, h, lane, out_k, out_v, ld_idx(cu_k, cu64, b) + t);
+  const int64_t start = ld_idx(cu_k, cu64, b);
+  int64_t slot[kRows], dst[kRows];
+#pragma unroll
+  for (int j = 0; j < kRows; ++j) {
+    const int64_t t = t0 + j;
+    slot[j] = t < length ? (int64_t)req_to_token[req * req_stride + t] : -1;
+    dst[j] = start + t;
+  }
+  gather_rows<KIND, D, G8>(P, slot, dst, H, lane, out_k, out_v);
+}
+
+// Vector access widths: INT4 codes 4 bytes, INT8 codes 8 bytes, bf16 rows 16 bytes per lane.
+bool aligned_args(int kind, const void* k, const void* v, const void* rk, const void* rv, const void* ok,
+                  const void* ov) {
+  const auto al = [](const void* p, uintptr_t a) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) % a) == 0; };
+  const uintptr_t ca = kind == 0 ? 8 : 4;
+  return al(k, ca) && al(v, ca) && al(rk, 8) && al(rv, 8) && al(ok, 16) && al(ov, 16);
 }
 
 }  // namespace
@@ -156,14 +233,16 @@ int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_sca
                        int cu_is_int64, int batch, int topk, int H, int D, int group8, void* out_k, void* out_v,
                        void* stream) {
   if (batch < 0 || topk < 0 || H <= 0) return KVT_EINVAL;
+  if (!aligned_args(kind, k, v, ring_k, ring_v, out_k, out_v)) return KVT_EINVAL;
   if (batch == 0 || topk == 0) return KVT_OK;
   Pools P{(const uint8_t*)k,        (const uint8_t*)v,       (const uint16_t*)k_scale, (const uint16_t*)v_scale,
           (const int8_t*)ring_k,    (const int8_t*)ring_v,   (const uint16_t*)ring_ks, (const uint16_t*)ring_vs,
           (const int32_t*)owner,    (const uint16_t*)sm_k,   (const uint16_t*)sm_v,    ring_mask};
-  const dim3 grid((unsigned)((topk + 3) / 4), (unsigned)(batch * H));
+  constexpr int kPerBlock = kWaves * kRows;
+  const dim3 grid((unsigned)((topk + kPerBlock - 1) / kPerBlock), (unsigned)batch);
   hipStream_t st = (hipStream_t)stream;
 #define KVT_CG(KIND_, D_, G_)                                                                                   \
-  hipLaunchKernelGGL((compact_kernel<KIND_, D_, G_>), grid, dim3(256), 0, st, P, (const int32_t*)req_to_token, \
+  hipLaunchKernelGGL((compact_kernel<KIND_, D_, G_>), grid, dim3(64 * kWaves), 0, st, P, (const int32_t*)req_to_token, \
                      req_stride, req_indices, req_is_int64, (const int32_t*)indices, idx_stride,               \
                      (const int32_t*)seq_lens, cu_k, cu_is_int64, topk, H, (uint16_t*)out_k, (uint16_t*)out_v)
 #define KVT_CG0(D_, G_) KVT_CG(0, D_, G_)
@@ -193,14 +272,17 @@ int kvt_prefix_gather(int kind, const void* k, const void* v, const void* k_scal
                       const void* seq_lens, const void* cu_k, int cu_is_int64, int batch, int64_t max_len, int H,
                       int D, int group8, void* out_k, void* out_v, void* stream) {
   if (batch < 0 || max_len < 0 || H <= 0) return KVT_EINVAL;
+  if (!aligned_args(kind, k, v, ring_k, ring_v, out_k, out_v)) return KVT_EINVAL;
   if (batch == 0 || max_len == 0) return KVT_OK;
   Pools P{(const uint8_t*)k,        (const uint8_t*)v,       (const uint16_t*)k_scale, (const uint16_t*)v_scale,
           (const int8_t*)ring_k,    (const int8_t*)ring_v,   (const uint16_t*)ring_ks, (const uint16_t*)ring_vs,
           (const int32_t*)owner,    (const uint16_t*)sm_k,   (const uint16_t*)sm_v,    ring_mask};
-  const dim3 grid((unsigned)((max_len + 3) / 4), (unsigned)(batch * H));
+  constexpr int kPerBlock = kWaves * kRows;
+  if ((max_len + kPerBlock - 1) / kPerBlock > 0x7fffffffLL) return KVT_ERANGE;
+  const dim3 grid((unsigned)((max_len + kPerBlock - 1) / kPerBlock), (unsigned)batch);
   hipStream_t st = (hipStream_t)stream;
 #define KVT_PG(KIND_, D_, G_)                                                                                  \
-  hipLaunchKernelGGL((prefix_kernel<KIND_, D_, G_>), grid, dim3(256), 0, st, P, (const int32_t*)req_to_token, \
+  hipLaunchKernelGGL((prefix_kernel<KIND_, D_, G_>), grid, dim3(64 * kWaves), 0, st, P, (const int32_t*)req_to_token, \
                      req_stride, req_indices, req_is_int64, (const int32_t*)seq_lens, cu_k, cu_is_int64, H,   \
                      (uint16_t*)out_k, (uint16_t*)out_v)
 #define KVT_PG0(D_, G_) KVT_PG(0, D_, G_)
