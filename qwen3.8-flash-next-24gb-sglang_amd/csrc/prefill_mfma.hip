@@ -15,7 +15,7 @@
 //   heads) held in registers, pre-multiplied by scale * log2(e).  The D
 //   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
 //   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
-//   O += P V on the same instruction: B = V^T rows from LDS (two 8-byte reads per 16-dim column block).
+//   O += P V on the same instruction: B = V^T rows from LDS (one 16-byte read per 16-dim column block).
 // Numerics: fp16 K/V = code * scale (finer than the oracle's bf16 rows), fp16 Q * scale * log2(e) and P, fp32
 // accumulation and softmax; bf16 (as the reference) or fp32 output.
 
@@ -36,12 +36,18 @@ constexpr int kT = 32;                  // key positions per tile
 // LDS tiles, XOR-swizzled so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
 //   K: fp16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
 //      4 st + kb of 16 consecutive keys: 16 distinct chunks mod 16, i.e. all 64 banks.
-//   V^T: fp16 row per dim (64 B = 32 keys); its 8-byte chunk j (keys 4 j .. 4 j + 3) lives at chunk
-//      j ^ ((dim >> 2) & 7).  A B-operand read takes chunk j of 16 consecutive dims: (dim & 3, chunk) distinct.
+//   V^T: fp16 row per dim (64 B = 32 keys) in four 16-byte chunks; chunk q holds the keys of matrix k-group q
+//      (keys 4 q .. 4 q + 3, then 16 + 4 q .. 16 + 4 q + 3: the k order of the P operand).  Dim d is stored in row
+//      r = d ^ ((d >> 4) & 3), its chunk q at chunk q ^ ((r >> 2) & 3).  A B-operand read is one 16-byte read of
+//      chunk kb for 16 consecutive dims (every 8-lane phase: 8 distinct 4-bank groups); the transposed dword stores
+//      of the dequantizing threads (16 key pairs x 4 dim blocks per wavefront) hit 64 distinct banks.
 constexpr int kKPitch = kD * 2;         // bytes per fp16 K row
 constexpr int kVPitch = kT * 2;         // bytes per fp16 V^T row
 KVT_DEV uint32_t k_chunk(int key, int c) { return 16u * (uint32_t)(c ^ (key & 15)); }
-KVT_DEV uint32_t vt_chunk(int dim, int j) { return 8u * (uint32_t)(j ^ ((dim >> 2) & 7)); }
+KVT_DEV uint32_t vt_row_chunk(int dim, int q) {
+  const int row = dim ^ ((dim >> 4) & 3);
+  return (uint32_t)row * kVPitch + 16u * (uint32_t)(q ^ ((row >> 2) & 3));
+}
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -246,13 +252,16 @@ KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   uint32_t a[8], b[8];
   v_row16(x, 0, a);
   v_row16(x, 1, b);
+  // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
+  const int q = (tp >> 1) & 3;
+  const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
     const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
-    const int d0 = 16 * db + 2 * i, d1 = d0 + 1;   // keys 2 tp, 2 tp + 1: chunk tp >> 1, dword tp & 1
-    *reinterpret_cast<uint32_t*>(vt + d0 * kVPitch + vt_chunk(d0, tp >> 1) + 4 * (tp & 1)) = lo;
-    *reinterpret_cast<uint32_t*>(vt + d1 * kVPitch + vt_chunk(d1, tp >> 1) + 4 * (tp & 1)) = hi;
+    const int d0 = 16 * db + 2 * i, d1 = d0 + 1;
+    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d0, q) + inner) = lo;
+    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d1, q) + inner) = hi;
   }
 }
 
@@ -440,14 +449,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       pa = h8{(_Float16)s[0][0], (_Float16)s[0][1], (_Float16)s[0][2], (_Float16)s[0][3],
               (_Float16)s[1][0], (_Float16)s[1][1], (_Float16)s[1][2], (_Float16)s[1][3]};
     }
-    // ---- O += P V: B = V^T row (dim 16 c + n16), keys {4 kb .. +3, 16 + 4 kb .. +3}
+    // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const int dim = 16 * c + n16;
-      const uint8_t* vrow = lds.vt[cb] + dim * kVPitch;
-      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + vt_chunk(dim, kb));
-      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + vt_chunk(dim, 4 + kb));
-      const h8 bv = __builtin_bit_cast(h8, u4v{lo.x, lo.y, hi.x, hi.y});
+      const h8 bv = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(lds.vt[cb] + vt_row_chunk(16 * c + n16, kb)));
       acc[c] = mfma(pa, bv, acc[c]);
     }
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
