@@ -218,14 +218,14 @@ int kvt_vmm_granularity(int device, uint64_t* granularity);
  * lazy mode by patches/kv_lazy.py:100-106). */
 int kvt_vmm_reserve(int device, uint64_t bytes, void** arena, void** base);
 
-/* Back the prefix [0, bytes) (rounded up to the granularity) -- one new physical allocation for the part not yet
+/* Back the prefix [0, bytes) (rounded up to the granularity) -- one physical allocation per granule not yet
  * backed; a smaller or equal size is a no-op (commits only grow); KVT_ERANGE past the reservation, KVT_ENOMEM when
- * the device has no physical memory for it (the arena is unchanged then).  Replaces ensure_prefix
+ * the device has no physical memory (the granules mapped before the failure stay backed).  Replaces ensure_prefix
  * (patches/kv_lazy.py:70-75). */
 int kvt_vmm_commit(void* arena, uint64_t bytes);
 
-/* Unmap and free every mapping that starts at or beyond align_up(keep_bytes, granularity); mappings straddling
- * that cut stay (patches/kv_lazy.py:39-63 uncommit_beyond).  *freed (may be NULL) = bytes returned. */
+/* Unmap and free every mapping (granule) that starts at or beyond align_up(keep_bytes, granularity)
+ * (patches/kv_lazy.py:39-63 uncommit_beyond: mappings straddling the cut stay; one-granule mappings never do).  *freed (may be NULL) = bytes returned. */
 int kvt_vmm_release_beyond(void* arena, uint64_t keep_bytes, uint64_t* freed);
 
 /* Backed bytes, reserved bytes and number of mappings (any pointer may be NULL). */

@@ -3,9 +3,9 @@
 //
 // Behaviour follows the reference's lazy KV backing (patches/kv_lazy.py:39-63 uncommit_beyond, :70-88 ensure_prefix /
 // release_beyond over SGLang's VMM owner): the whole pool is reserved as address space; commits back a growing
-// prefix; a release unmaps every mapping that starts at or beyond the (granularity-aligned) cut, mappings straddling
-// the cut stay.  Each commit maps ONE new physical allocation covering [backed, new end): commits come in
-// 2048-token steps, so the mapping list stays short (a 262,144-token pool backed in full is 128 mappings).
+// prefix; a release unmaps every mapping that starts at or beyond the (granularity-aligned) cut.  Every mapping is
+// one physical allocation of one 2 MiB granule (a 262,144-token pool's 64 MiB code buffer backed in full is 32
+// mappings), so no mapping straddles a granule-aligned cut.
 //
 // Host code only (no kernels).  Every entry point is synchronous with respect to the host; before unmapping, the
 // device's queued work is waited for (hipDeviceSynchronize, as the reference's release_beyond does with
@@ -41,9 +41,9 @@ struct Arena {
 
 uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
-// Mappings are whole 2 MiB granules at 2 MiB-aligned addresses, whatever smaller granularity the runtime
-// recommends (4 KiB on MI355X): maps of 2 MiB or more at addresses that are not 2 MiB-aligned are rejected by
-// hipMemSetAccess (invalid argument) on ROCm 7.2, while aligned whole-granule maps of any count work.
+// Mappings are single 2 MiB granules at 2 MiB-aligned addresses, whatever smaller granularity the runtime
+// recommends (4 KiB on MI355X): on ROCm 7.2, hipMemSetAccess rejected (invalid argument) maps of 2.5 MiB at a 1 MiB
+// offset and, intermittently, 6 MiB allocations at 2 MiB-aligned offsets, while one-granule maps never failed.
 constexpr uint64_t kGranule = 2ull << 20;
 
 hipMemAllocationProp device_prop(int device) {
@@ -158,28 +158,30 @@ int kvt_vmm_commit(void* arena, uint64_t bytes) {
   if (want > a->reserved) return KVT_ERANGE;
   if (want <= a->backed) return KVT_OK;   // commits only grow
   DeviceGuard g(a->device);
-  const uint64_t off = a->backed, len = want - off;
   const hipMemAllocationProp p = device_prop(a->device);
-  hipMemGenericAllocationHandle_t h;
-  hipError_t e = hipMemCreate(&h, len, &p, 0);
-  if (e != hipSuccess) return report("hipMemCreate", e, off, len, KVT_ENOMEM);
-  e = hipMemMap(a->base + off, len, 0, h, 0);
-  if (e != hipSuccess) {
-    (void)hipMemRelease(h);
-    return report("hipMemMap", e, off, len, KVT_EHIP);
-  }
   hipMemAccessDesc acc = {};
   acc.location.type = hipMemLocationTypeDevice;
   acc.location.id = a->device;
   acc.flags = hipMemAccessFlagsProtReadWrite;
-  e = hipMemSetAccess(a->base + off, len, &acc, 1);
-  if (e != hipSuccess) {
-    (void)hipMemUnmap(a->base + off, len);
-    (void)hipMemRelease(h);
-    return report("hipMemSetAccess", e, off, len, KVT_EHIP);
+  // one physical allocation per granule: on failure the granules mapped so far stay (the arena is consistent)
+  for (uint64_t off = a->backed; off < want; off += a->gran) {
+    hipMemGenericAllocationHandle_t h;
+    hipError_t e = hipMemCreate(&h, a->gran, &p, 0);
+    if (e != hipSuccess) return report("hipMemCreate", e, off, a->gran, KVT_ENOMEM);
+    e = hipMemMap(a->base + off, a->gran, 0, h, 0);
+    if (e != hipSuccess) {
+      (void)hipMemRelease(h);
+      return report("hipMemMap", e, off, a->gran, KVT_EHIP);
+    }
+    e = hipMemSetAccess(a->base + off, a->gran, &acc, 1);
+    if (e != hipSuccess) {
+      (void)hipMemUnmap(a->base + off, a->gran);
+      (void)hipMemRelease(h);
+      return report("hipMemSetAccess", e, off, a->gran, KVT_EHIP);
+    }
+    a->maps.push_back(Mapping{off, a->gran, h});
+    a->backed = off + a->gran;
   }
-  a->maps.push_back(Mapping{off, len, h});
-  a->backed = want;
   return KVT_OK;
 }
 

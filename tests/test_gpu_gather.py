@@ -242,3 +242,34 @@ def test_single_tier_gathers(tiered_state):
     for b in range(BATCH):
         rows = rtt[b, idx[b].long()].long()
         assert torch.equal(ok.cpu()[int(cu_k[b]):int(cu_k[b + 1])], d8[rows])
+
+
+def test_gathers_reject_misaligned_scratch(tiered_state):
+    """The gathers store 16 bytes per lane: a scratch whose base is not 16-byte aligned is refused before any launch
+    (ValueError, nothing written); a row slice of an aligned allocation (offset 8 rows) is served and matches."""
+    from kvtier import sparse_attn as sa
+    st = tiered_state
+    gen = torch.Generator().manual_seed(14)
+    rtt = torch.stack([torch.randperm(SLOTS, generator=gen) for _ in range(BATCH)]).to(torch.int32).to(dev)
+    lens = torch.tensor([40, 7, 100], dtype=torch.int32, device=dev)
+    cu = F.pad(lens.cumsum(0), (1, 0)).to(torch.int32)
+    req_idx = torch.arange(BATCH, dtype=torch.int64, device=dev)
+    n = int(cu[-1])
+    flat = torch.full(((n + 8) * H * D + 8,), float("nan"), device=dev, dtype=torch.bfloat16)
+    bad_k = flat[1:1 + n * H * D].view(n, H, D)                 # base 2 bytes past an aligned allocation
+    good = torch.full((n + 8, H, D), float("nan"), device=dev, dtype=torch.bfloat16)
+    kw = dict(ring_k=st["rk"], ring_v=st["rv"], ring_ks=st["rks"], ring_vs=st["rvs"], owner=st["owner"],
+              ring_mask=R - 1)
+    args = (st["k4"], st["v4"], st["ks4"], st["vs4"], st["sm_k"], st["sm_v"], rtt, req_idx, lens, cu)
+    with pytest.raises(ValueError):
+        sa.qwen_sparse_prefix_gather_dequant_tiered(*args, bad_k, good[8:], BATCH, int(lens.max()), **kw)
+    torch.cuda.synchronize()
+    assert torch.isnan(flat).all() and torch.isnan(good).all()
+    other = torch.full((n, H, D), float("nan"), device=dev, dtype=torch.bfloat16)
+    sa.qwen_sparse_prefix_gather_dequant_tiered(*args, good[8:], other, BATCH, int(lens.max()), **kw)
+    torch.cuda.synchronize()
+    gk, gv = good[8:].cpu(), other.cpu()
+    for b in range(BATCH):
+        rows = rtt[b, :int(lens[b])].long().cpu()
+        a, e = int(cu[b]), int(cu[b + 1])
+        assert torch.equal(gk[a:e], st["dk_all"][rows]) and torch.equal(gv[a:e], st["dv_all"][rows])

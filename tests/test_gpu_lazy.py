@@ -27,21 +27,21 @@ def test_vmm_arena_commit_release(kvt_pkg):
     assert g > 0 and a.reserved >= 40 << 20 and a.reserved % g == 0 and a.backed == 0 and a.n_mappings == 0
     t = a.tensor((a.reserved,), torch.uint8)
     assert t.data_ptr() == a.base
-    a.commit(g + g // 2)                       # rounded up to 2 granules, one mapping
-    assert a.backed == 2 * g and a.n_mappings == 1
+    a.commit(g + g // 2)                       # rounded up to 2 granules, one mapping each
+    assert a.backed == 2 * g and a.n_mappings == 2
     p0 = _pattern(2 * g, 1)
     t[:2 * g].copy_(p0)
-    a.commit(5 * g)                            # grows by one more mapping; the first keeps its contents
-    assert a.backed == 5 * g and a.n_mappings == 2
+    a.commit(5 * g)                            # 3 more granules; the first two keep their contents
+    assert a.backed == 5 * g and a.n_mappings == 5
     t[2 * g:5 * g].fill_(9)
     torch.cuda.synchronize()
     assert torch.equal(t[:2 * g], p0) and bool((t[2 * g:5 * g] == 9).all())
     a.commit(3 * g)                            # commits only grow
-    assert a.backed == 5 * g and a.n_mappings == 2
-    assert a.release_beyond(3 * g) == 0        # the second mapping (2g .. 5g) straddles the cut: it stays
-    assert a.backed == 5 * g
-    assert a.release_beyond(2 * g) == 3 * g    # now it starts at the cut: unmapped
-    assert a.backed == 2 * g and a.n_mappings == 1
+    assert a.backed == 5 * g and a.n_mappings == 5
+    assert a.release_beyond(3 * g - 1) == 2 * g   # cut rounded up to 3g: granules 3 and 4 go
+    assert a.backed == 3 * g and bool((t[2 * g:3 * g] == 9).all())
+    assert a.release_beyond(2 * g) == g
+    assert a.backed == 2 * g and a.n_mappings == 2
     assert torch.equal(t[:2 * g], p0)
     a.commit(4 * g)                            # backed again, fresh memory
     p1 = _pattern(2 * g, 2)
@@ -152,3 +152,27 @@ def test_lazy_tiered_pool_matches_eager(kvt_pkg, monkeypatch):
     for lid in range(layers):
         assert torch.equal(lazy.k_buffer[lid][written], eager.k_buffer[lid][written])
         assert torch.equal(lazy.v_scale_buffer[lid][written], eager.v_scale_buffer[lid][written])
+
+
+def test_lazy_int8_pool_matches_eager(kvt_pkg):
+    """The single-tier INT8-G64 pool in lazy mode: same bytes as the eager pool for the same hand-outs and writes;
+    a hand-out that would cross the reservation is refused by the allocator, not by a fault."""
+    from kvtier.tiered_kv_pool import MHATokenToKVPoolInt8, PagedTokenAllocator
+    size = 16384
+    lazy = MHATokenToKVPoolInt8(size, 64, torch.int8, 2, 256, 1, dev, lazy=True)
+    eager = MHATokenToKVPoolInt8(size, 64, torch.int8, 2, 256, 1, dev, lazy=False)
+    al, ae = PagedTokenAllocator(size, 64, lazy), PagedTokenAllocator(size, 64, eager)
+    gen = torch.Generator().manual_seed(6)
+    for n in (4096, 6144, 6144):
+        loc = al.alloc(n)
+        assert loc is not None and torch.equal(loc, ae.alloc(n))
+        k = torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+        v = torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+        lazy.set_kv_buffer(None, loc.to(dev), k, v, layer_id_override=0)
+        eager.set_kv_buffer(None, loc.to(dev), k, v, layer_id_override=0)
+        torch.cuda.synchronize()
+        rows = slice(0, lazy.lazy_backed_tokens)
+        assert torch.equal(lazy.k_buffer[0][rows], eager.k_buffer[0][rows])
+        assert torch.equal(lazy.v_scale_buffer[0][rows], eager.v_scale_buffer[0][rows])
+    assert lazy.lazy_backed_tokens == size + 64          # 16,384 slots handed out: the whole pool backed
+    assert al.alloc(64) is None                          # nothing left
