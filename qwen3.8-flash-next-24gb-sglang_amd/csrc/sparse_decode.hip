@@ -140,9 +140,10 @@ KVT_DEV void issue_tile(const PoolRsrc& P, int flags, uint32_t coff, uint32_t so
 }
 
 template <int KIND, int G8>
-__global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A) {
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) sparse_decode_kernel(SparseArgs A) {
   // per wavefront: its tile's K and V rows (bf16); after the tiles, the same space holds the 4 partials' merge
-  __shared__ __align__(16) uint16_t kv[kWaves][2][kRows * kKPitch];
+  // one tile buffer per wavefront: K rows until S is formed, then V rows (LDS per block 42 KB: 3 blocks per CU)
+  __shared__ __align__(16) uint16_t kv[kWaves][kRows * kKPitch];
   __shared__ __align__(16) uint16_t qs[kHeads * kKPitch];   // the group's q heads, bf16 (zero beyond gs)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -152,8 +153,8 @@ __global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A
   const int H = A.H, gs = A.gs;
   const int64_t item = ((int64_t)b * H + h) * A.n_splits + split;
   const int n16 = lane & 15, kq = lane >> 4;
-  uint16_t* kt = kv[wave][0];
-  uint16_t* vr = kv[wave][1];
+  uint16_t* kt = kv[wave];
+  uint16_t* vr = kv[wave];   // the same rows: V is dequantized once the K reads of S are issued
 
   // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
 #pragma unroll
@@ -224,7 +225,7 @@ __global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A
     smv[3] = f16_bits_to_f32((uint16_t)(w.y >> 16));
   }
 
-  // dequantize the tile into this wavefront's LDS rows (K and V, row-major)
+  // dequantize the tile's K rows into this wavefront's LDS rows (row-major)
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
     const bool ht = (T.fl[r] & 2) != 0;
@@ -234,11 +235,6 @@ __global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = c[i] * sk * smk[i];
     *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
-    codes4(ht, T.vw[r], lane, c);
-    const float sv = f16_bits_to_f32((uint16_t)T.vs[r]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = c[i] * sv * smv[i];
-    *reinterpret_cast<uint2*>(&vr[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
   }
   __syncthreads();   // q staged (the tile rows are this wavefront's own: its LDS accesses are in order)
 
@@ -249,6 +245,18 @@ __global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A
     const uint2 ka = *reinterpret_cast<const uint2*>(&kt[n16 * kKPitch + 16 * k + 4 * kq]);
     const uint2 qb = *reinterpret_cast<const uint2*>(&qs[n16 * kKPitch + 16 * k + 4 * kq]);
     s = mfma_bf16(__builtin_bit_cast(bf4, ka), __builtin_bit_cast(bf4, qb), s);
+  }
+  // V rows into the same LDS rows: a wavefront's LDS accesses complete in order, so these stores land after the K
+  // reads above (the compiler keeps stores behind loads that may alias them)
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const bool ht = (T.fl[r] & 2) != 0;
+    float c[4], x[4];
+    codes4(ht, T.vw[r], lane, c);
+    const float sv = f16_bits_to_f32((uint16_t)T.vs[r]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = c[i] * sv * smv[i];
+    *reinterpret_cast<uint2*>(&vr[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
   }
   // softmax over the tile's rows (log2 units): rows 4 kq + i of this lane, the other 12 in lanes n16 + 16 j
   constexpr float kLog2e = 1.4426950408889634f;
@@ -290,7 +298,7 @@ __global__ void __launch_bounds__(64 * kWaves) sparse_decode_kernel(SparseArgs A
   // merge the 4 wavefronts' partials through LDS (the tile rows are done with): wavefront w stores O rows of heads
   // < gs and (m, l) per head; then thread t merges head t / 32, channels 8 (t % 32) .. + 7 over the 4
   __syncthreads();
-  float* mo = reinterpret_cast<float*>(&kv[0][0][0]);              // [wave][head < 8][256]
+  float* mo = reinterpret_cast<float*>(&kv[0][0]);                 // [wave][head < 8][256]
   float* mml = mo + kWaves * 8 * kD;                                // [wave][head][2]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
