@@ -1,6 +1,6 @@
 // Gather-dequant kernels of the tiered KV cache (drop-in for the reference's compact and prefix gathers).
 //
-// A wavefront writes kRows output rows (all KV heads, K and V).  Lane l owns unit u = l (+ 64, ... while u < H D / 8):
+// A wavefront writes 2 (top-k) or 4 (prefix) output rows (all KV heads, K and V).  Lane l owns unit u = l (+ 64, ... while u < H D / 8):
 // KV head u / (D / 8), channels 8 (u % (D / 8)) .. + 7, whose smoothing constants it loads once.  Per row it reads
 // 4 bytes of INT4 codes (or 8 bytes of INT8 codes) and one fp16 group scale for K and for V, and stores 16 bytes of
 // bf16 for each: a row of one tensor is one contiguous read and one contiguous 1 KiB store across the wavefront.
@@ -38,7 +38,10 @@ struct Pools {
   int64_t ring_mask;
 };
 
-constexpr int kRows = 4;     // rows per wavefront
+// rows per wavefront: 2 for the top-k gather (random rows: more wavefronts in flight), 4 for the whole-prefix
+// gather (streaming) -- 174.7 against 192 us and 1.55 against 1.69 ms per 12-layer step, the better of 2, 4 and 8
+constexpr int kCompactRows = 2;
+constexpr int kPrefixRows = 4;
 constexpr int kWaves = 4;    // wavefronts per block
 
 // bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
@@ -86,14 +89,14 @@ KVT_DEV uint4 dequant4(const Raw& r, const float m[8]) {   // ((b & 15) - 8) * s
   return make_uint4(bf16x2(x[0], x[1]), bf16x2(x[2], x[3]), bf16x2(x[4], x[5]), bf16x2(x[6], x[7]));
 }
 
-// kRows rows of one wavefront: slot[j] (wave-uniform; < 0 = row not written) -> output row dst[j].
-template <int KIND, int D, int G8>
-KVT_DEV void gather_rows(const Pools& P, const int64_t slot[kRows], const int64_t dst[kRows], int H, int lane,
+// ROWS rows of one wavefront: slot[j] (wave-uniform; < 0 = row not written) -> output row dst[j].
+template <int KIND, int D, int G8, int ROWS>
+KVT_DEV void gather_rows(const Pools& P, const int64_t slot[ROWS], const int64_t dst[ROWS], int H, int lane,
                          uint16_t* out_k, uint16_t* out_v) {
-  bool hot[kRows];
-  int64_t ring[kRows];
+  bool hot[ROWS];
+  int64_t ring[ROWS];
 #pragma unroll
-  for (int j = 0; j < kRows; ++j) {
+  for (int j = 0; j < ROWS; ++j) {
     hot[j] = KIND == 0;
     ring[j] = 0;
     if constexpr (KIND == 2) {
@@ -113,9 +116,9 @@ KVT_DEV void gather_rows(const Pools& P, const int64_t slot[kRows], const int64_
       mk[i] = f16_bits_to_f32(P.sm_k[h * D + 8 * cg + i]);
       mv[i] = f16_bits_to_f32(P.sm_v[h * D + 8 * cg + i]);
     }
-    Raw rk[kRows], rv[kRows];
+    Raw rk[ROWS], rv[ROWS];
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) {
+    for (int j = 0; j < ROWS; ++j) {
       if (slot[j] < 0) continue;
       if constexpr (KIND == 0) {
         rk[j] = load_int8<D, G8>(reinterpret_cast<const int8_t*>(P.k), P.ks, slot[j], H, h, cg);
@@ -131,7 +134,7 @@ KVT_DEV void gather_rows(const Pools& P, const int64_t slot[kRows], const int64_
       }
     }
 #pragma unroll
-    for (int j = 0; j < kRows; ++j) {
+    for (int j = 0; j < ROWS; ++j) {
       if (slot[j] < 0) continue;
       const uint4 ok = hot[j] ? dequant8(rk[j], mk) : dequant4(rk[j], mk);
       const uint4 ov = hot[j] ? dequant8(rv[j], mv) : dequant4(rv[j], mv);
@@ -147,7 +150,7 @@ KVT_DEV int64_t ld_idx(const void* p, int is64, int64_t i) {
 
 KVT_DEV int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
-// grid.x = column blocks of kWaves * kRows, grid.y = batch
+// grid.x = column blocks of kWaves * kCompactRows, grid.y = batch
 template <int KIND, int D, int G8>
 __global__ void __launch_bounds__(64 * kWaves) compact_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
                                                               const void* req_indices, int req64,
@@ -155,6 +158,7 @@ __global__ void __launch_bounds__(64 * kWaves) compact_kernel(Pools P, const int
                                                               const int32_t* seq_lens, const void* cu_k, int cu64,
                                                               int topk, int H, uint16_t* out_k, uint16_t* out_v) {
   const int lane = threadIdx.x & 63;
+  constexpr int kRows = kCompactRows;
   const int64_t col0 = ((int64_t)blockIdx.x * kWaves + wave_id()) * kRows;
   const int b = blockIdx.y;
   if (col0 >= topk) return;
@@ -173,16 +177,17 @@ __global__ void __launch_bounds__(64 * kWaves) compact_kernel(Pools P, const int
       if (pos >= 0 && pos < length) slot[j] = req_to_token[req * req_stride + pos];   // store mask = valid
     }
   }
-  gather_rows<KIND, D, G8>(P, slot, dst, H, lane, out_k, out_v);
+  gather_rows<KIND, D, G8, kRows>(P, slot, dst, H, lane, out_k, out_v);
 }
 
-// grid.x = row blocks of kWaves * kRows, grid.y = batch
+// grid.x = row blocks of kWaves * kPrefixRows, grid.y = batch
 template <int KIND, int D, int G8>
 __global__ void __launch_bounds__(64 * kWaves) prefix_kernel(Pools P, const int32_t* req_to_token, int64_t req_stride,
                                                              const void* req_indices, int req64,
                                                              const int32_t* seq_lens, const void* cu_k, int cu64,
                                                              int H, uint16_t* out_k, uint16_t* out_v) {
   const int lane = threadIdx.x & 63;
+  constexpr int kRows = kPrefixRows;
   const int64_t t0 = ((int64_t)blockIdx.x * kWaves + wave_id()) * kRows;
   const int b = blockIdx.y;
   const int64_t length = seq_lens[b];
@@ -196,7 +201,7 @@ __global__ void __launch_bounds__(64 * kWaves) prefix_kernel(Pools P, const int3
     slot[j] = t < length ? (int64_t)req_to_token[req * req_stride + t] : -1;
     dst[j] = start + t;
   }
-  gather_rows<KIND, D, G8>(P, slot, dst, H, lane, out_k, out_v);
+  gather_rows<KIND, D, G8, kRows>(P, slot, dst, H, lane, out_k, out_v);
 }
 
 // Vector access widths: INT4 codes 4 bytes, INT8 codes 8 bytes, bf16 rows 16 bytes per lane.
@@ -238,7 +243,7 @@ int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_sca
   Pools P{(const uint8_t*)k,        (const uint8_t*)v,       (const uint16_t*)k_scale, (const uint16_t*)v_scale,
           (const int8_t*)ring_k,    (const int8_t*)ring_v,   (const uint16_t*)ring_ks, (const uint16_t*)ring_vs,
           (const int32_t*)owner,    (const uint16_t*)sm_k,   (const uint16_t*)sm_v,    ring_mask};
-  constexpr int kPerBlock = kWaves * kRows;
+  constexpr int kPerBlock = kWaves * kCompactRows;
   const dim3 grid((unsigned)((topk + kPerBlock - 1) / kPerBlock), (unsigned)batch);
   hipStream_t st = (hipStream_t)stream;
 #define KVT_CG(KIND_, D_, G_)                                                                                   \
@@ -277,7 +282,7 @@ int kvt_prefix_gather(int kind, const void* k, const void* v, const void* k_scal
   Pools P{(const uint8_t*)k,        (const uint8_t*)v,       (const uint16_t*)k_scale, (const uint16_t*)v_scale,
           (const int8_t*)ring_k,    (const int8_t*)ring_v,   (const uint16_t*)ring_ks, (const uint16_t*)ring_vs,
           (const int32_t*)owner,    (const uint16_t*)sm_k,   (const uint16_t*)sm_v,    ring_mask};
-  constexpr int kPerBlock = kWaves * kRows;
+  constexpr int kPerBlock = kWaves * kPrefixRows;
   if ((max_len + kPerBlock - 1) / kPerBlock > 0x7fffffffLL) return KVT_ERANGE;
   const dim3 grid((unsigned)((max_len + kPerBlock - 1) / kPerBlock), (unsigned)batch);
   hipStream_t st = (hipStream_t)stream;
