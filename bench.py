@@ -367,6 +367,13 @@ def append_workload(args) -> dict:
     nbytes = cache.append_bytes(N, N)
     gbps = nbytes / t_launch / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_append(N)
+    traffic = None   # HBM bytes per launch measured by two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE)
+    tfile = os.path.join(ROOT, "profiles", "decode_262k_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as f:
+            ae = json.load(f).get("append_evict_bytes_per_launch")
+        if ae:
+            traffic = int(ae["read"]) + int(ae["write"])
     return {
         "metric": "quantize-append with ring eviction: GB/s of algorithmic HBM bytes (8,192 tokens per launch)",
         "value": round(gbps, 1), "unit": "GB/s", "higher_is_better": True, "steps": reps, "warmup": args.warmup,
@@ -374,7 +381,7 @@ def append_workload(args) -> dict:
         "config": {"workload": "append 8,192 tokens x 12 layers into a full 8,192-row ring, 2 KV heads, D 256, "
                                "INT8-G64 ring, INT4-G32 pages; 4 steps per graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None, "kernel": "append_evict",
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": traffic, "kernel": "append_evict",
                      "bytes_per_launch": nbytes},
         "cpu_baseline": cpu,
     }
