@@ -101,11 +101,11 @@ int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_sca
 /* Top-k sparse decode attention, fused: for request b (one query row, q bf16 [batch, Hq, D] with batch stride
  * q_stride_b elements, 16-byte aligned), the selected columns c < cu_k[b+1] - cu_k[b] (and < topk) whose position
  * indices[b * idx_stride + c] lies in [0, seq_lens[b]) are resolved through req_to_token[req_indices[b]] and, for
- * kind 0, the owner table, dequantized as kvt_compact_gather writes them (bf16(q * s * sm)) and attended with scale;
+ * kind 2, the owner table, dequantized as kvt_compact_gather writes them (bf16(q * s * sm)) and attended with scale;
  * bf16 matrix-core products, fp32 accumulation.  Writes one unnormalized partial per 64 columns to part_o (fp32
  * [batch * H * n_splits, Hq / H, D]) and part_ml ([..., 2]): merge with kvt_decode_combine(n_chunks = n_splits,
  * chunk = 0, split_counts = NULL); a request with no attended column comes out NaN (0/0).  n_splits >= ceil(topk /
- * 64); Hq / H <= 8, D = 256.  Kinds and buffers as kvt_compact_gather; pool_rows = rows of k / v (byte offsets
+ * 64); Hq / H <= 16, D = 256.  Kinds and buffers as kvt_compact_gather; pool_rows = rows of k / v (byte offsets
  * are 32-bit: pool_rows * H * D (INT8) or * D / 2 (INT4) < 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the
  * compact gather + FlashAttention-2 pair of the reference's decode (flat patch
  * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for top-k selections. */
@@ -116,6 +116,25 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
                       const void* indices, int64_t idx_stride, const void* seq_lens, const void* cu_k,
                       int cu_is_int64, int batch, int topk, int H, int Hq, int D, int group8, float scale,
                       int n_splits, void* part_o, void* part_ml, void* stream);
+
+/* Prefix-chunk sparse attention read straight from a quantized pool.  Chunk b owns query rows cu_q[b] ..
+ * cu_q[b+1] of q (bf16, row r / q head j at q + r sq_n + j sq_h); its context holds kv_lens[b] positions, resolved
+ * through req_to_token[req_indices[b]] (and, kind 2, the owner table) and dequantized as kvt_compact_gather writes
+ * them.  Query j of the chunk (q_len rows) attends the entries of its index row (int32, row r / KV head h / column c
+ * at indices + r si_m + h si_g + c si_n) among the first min(topk, j + kv_len - q_len + 1) that lie in [0, kv_len);
+ * the result is written normalized to out (bf16, or fp32 when out_f32; row r / q head j at out + r so_n + j so_h);
+ * a row with no attended entry gives NaN (0/0).  bf16 matrix-core products, fp32 accumulation.  Grid: max_q rows per
+ * chunk (the longest chunk).  Hq / H <= 16, D = 256; q and out 16-byte aligned with row and head strides multiples of
+ * 16 bytes (else KVT_EINVAL); pool_rows and ring sizes as kvt_sparse_decode.  Replaces sparse_gqa_fwd_interface_paged
+ * / _sparse_gqa_chunk_prefill_paged (patches/kv_paged_prefix.py:141-365). */
+int kvt_sparse_prefill(int kind, const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                       const void* kv_lens, int batch, int max_q, const void* indices, int64_t si_m, int64_t si_g,
+                       int64_t si_n, int topk, const void* k, const void* v, const void* k_scale, const void* v_scale,
+                       int64_t pool_rows, const void* ring_k, const void* ring_v, const void* ring_ks,
+                       const void* ring_vs, const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,
+                       const void* req_to_token, int64_t req_stride, const void* req_indices, int req_is_int64, int H,
+                       int Hq, int D, int group8, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
+                       void* stream);
 
 /* Whole-prefix gather-dequant: rows [0, seq_lens[b]) of request req_indices[b] packed at cu_k[b]; rows at or
  * beyond seq_lens[b] are not written.  Replaces qwen_sparse_prefix_gather_dequant_{int8,int4,tiered}

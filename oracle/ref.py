@@ -12,11 +12,12 @@ forms follow the reference's own torch references (``gemv/test_kv_tiers.py:56-87
 * fp32 scale math, IEEE fp32 division, ``torch.round`` (round-half-to-even), RNE conversions to fp16/bf16;
 * the fp16-max clamp of every stored scale (``patches/kv_tiers.py:336-337``, ``patches/kv_int4.py:330-333``).
 
-How each part is pinned (checks in ``tests/test_oracle.py``): the reference tests' special cases and constants
-(0x88, 0x01|0xF0, 65504, 127*65504 and 7*65504 in bf16, the -7..7 row), an independent scalar restatement in
-pure Python on small random inputs (``tests/golden/scalar_model.py``), brute force over all 225 nibble pairs,
-invariants of the owner table (last writer of each residue class, the s/s+R boundary flip), the closed form of
-softmax attention at a single position (returns exactly that V row) and a float64 softmax.
+How each part is pinned (every function has a named check in ``tests/test_oracle.py``): the reference tests'
+special cases and constants (0x88, 0x01|0xF0, 65504, 127*65504 and 7*65504 in bf16, the -7..7 row), an independent
+scalar restatement in pure Python (``tests/golden/scalar_model.py``: golden vectors, per-slot tier loops), brute force
+(all 225 nibble pairs, per-element valid counts, the token-by-token evict model against its closed form), invariants
+of the owner table (last writer of each residue class, the s/s+R boundary flip, one winner per collision), the closed
+form of softmax attention at a single position (returns exactly that V row) and a float64 softmax.
 Parts with no such check: none.
 """
 from __future__ import annotations
@@ -143,19 +144,6 @@ def quant_store_tiered(k, v, loc, k_buf, v_buf, k_scale, v_scale, rk, rv, rks, r
     v_scale[sl] = sv
 
 
-def quant_store_int8(k, v, loc, k_buf, v_buf, k_scale, v_scale, sm_k_inv, sm_v_inv, group8: int = G8) -> None:
-    """INT8-G quant + scatter at loc (patches/kv_int8.py:281-362, with the fp16-max clamp)."""
-    if k.shape[0] == 0:
-        return
-    sl = loc.long()
-    q, s = quant8(k, group8, sm_k_inv)
-    k_buf[sl] = q
-    k_scale[sl] = s
-    q, s = quant8(v, group8, sm_v_inv)
-    v_buf[sl] = q
-    v_scale[sl] = s
-
-
 def quant_store_int4(k, v, loc, k_buf, v_buf, k_scale, v_scale, sm_k_inv, sm_v_inv) -> None:
     """INT4-G32 quant + nibble pack + scatter at loc (patches/kv_int4.py:289-393)."""
     if k.shape[0] == 0:
@@ -198,38 +186,6 @@ def cu_seqlens_valid(seq_lens, indices, topk):
     return torch.cat([torch.zeros(1, dtype=torch.long), counts.cumsum(0)]).to(torch.int32)
 
 
-def compact_gather(rows_fn, req_to_token, req_indices, indices, seq_lens, cu_k, out_k, out_v, batch, topk):
-    """Top-k gather into the bf16 scratch (patches/kv_tiers.py:446-538): column c of request b is valid when
-    c < cu_k[b+1] - cu_k[b] and 0 <= pos < seq_len; valid columns are written at row cu_k[b] + c, nothing else is
-    touched (store mask = valid).  rows_fn(slots) -> (K rows, V rows) bf16."""
-    for b in range(batch):
-        length = int(seq_lens[b])
-        req = int(req_indices[b])
-        start = int(cu_k[b])
-        vcount = int(cu_k[b + 1]) - start
-        for c in range(topk):
-            pos = int(indices[b, c])
-            if not (c < vcount and 0 <= pos < length):
-                continue
-            slot = req_to_token[req, pos].reshape(1)
-            kk, vv = rows_fn(slot)
-            out_k[start + c] = kk[0]
-            out_v[start + c] = vv[0]
-
-
-def prefix_gather(rows_fn, req_to_token, req_indices, seq_lens, cu_k, out_k, out_v, batch):
-    """Whole-prefix gather-dequant: rows [0, seq_len) of request b packed at cu_k[b] (patches/kv_tiers.py:568-619)."""
-    for b in range(batch):
-        length = int(seq_lens[b])
-        if length == 0:
-            continue
-        slots = req_to_token[int(req_indices[b]), :length]
-        kk, vv = rows_fn(slots)
-        a = int(cu_k[b])
-        out_k[a:a + length] = kk
-        out_v[a:a + length] = vv
-
-
 # ----------------------------------------------------------------------------------------------- attention
 def attention_rows(q: torch.Tensor, k_rows: torch.Tensor, v_rows: torch.Tensor, scale: float) -> torch.Tensor:
     """fp32 softmax attention of one query over bf16-dequantized rows (gemv/test_kv_paged_prefix.py:520-528).
@@ -256,7 +212,7 @@ def prefill_selected_positions(idx_row: torch.Tensor, visible: int, kv_len: int,
     """Positions a prefill query attends to (patches/kv_paged_prefix.py:200-229, test oracle
     gemv/test_kv_paged_prefix.py:515-519): the first min(topk, visible) entries of its index row with
     0 <= idx < kv_len; visible = j + kv_len - q_len + 1 for query j of its chunk."""
-    n = min(topk, visible)
+    n = max(0, min(topk, visible))          # a query with no visible position (kv_len < q_len) selects nothing
     pos = idx_row[:n].long()
     return pos[(pos >= 0) & (pos < kv_len)]
 
@@ -378,6 +334,27 @@ class PosTieredCache:
         return pt
 
 
+def evict_closed_form(xk: torch.Tensor, xv: torch.Tensor, ring_len: int, ring_start: int = 0, group8: int = G8,
+                      sm_k_inv=None, sm_v_inv=None) -> dict:
+    """State of one sequence of the evict-mode cache after positions ring_start .. ring_start + n - 1 were appended
+    (in any chunking), as closed forms over all tokens at once: positions p >= hot_start = max(ring_start,
+    length - R) hold quant8(x[p]) in ring row p & (R - 1) (patches/kv_tiers.py:325-351); every older appended
+    position holds requant8to4 of its INT8 row (docs/KV_TIERS_PLAN.md:53, :82), in page order.  xk / xv: the
+    appended rows [n, H, D] (row i = position ring_start + i).  Returns the hot codes / scales in position order
+    with their ring rows, the cold INT4 codes / scales in position order and hot_start."""
+    n = xk.shape[0]
+    length = ring_start + n
+    hs = max(ring_start, length - ring_len)
+    q8k, s8k = quant8(xk, group8, sm_k_inv)
+    q8v, s8v = quant8(xv, group8, sm_v_inv)
+    c = hs - ring_start                       # appended rows that left the ring
+    pk, sk = requant8to4(q8k[:c], s8k[:c], group8)
+    pv, sv = requant8to4(q8v[:c], s8v[:c], group8)
+    pos_hot = torch.arange(hs, length)
+    return dict(hot_start=hs, ring_rows=pos_hot & (ring_len - 1), rk=q8k[c:], rks=s8k[c:], rv=q8v[c:], rvs=s8v[c:],
+                k4=pk, ks4=sk, v4=pv, vs4=sv)
+
+
 # ----------------------------------------------------------------------------------------------- synthetic inputs
 def make_kv(n: int, H: int, D: int, gen: torch.Generator, outlier_ch: torch.Tensor, outlier_mul: float = 8.0):
     """K ~ N(0,1) with the given channels (per head) scaled x8 as outliers, V ~ N(0,1); bf16 on the CPU
@@ -398,7 +375,3 @@ def outlier_channels(H: int, D: int, n_out: int, gen: torch.Generator) -> torch.
 def make_q(Hq: int, D: int, gen: torch.Generator, n: int = 1) -> torch.Tensor:
     """Q ~ N(0,1) / 16 in bf16."""
     return (torch.randn(n, Hq, D, generator=gen) / 16).to(torch.bfloat16)
-
-
-def softmax_scale(D: int) -> float:
-    return 1.0 / math.sqrt(D)

@@ -1,20 +1,27 @@
-// Top-k sparse decode attention over the quantized pools, fused: the selected positions of each request are
-// resolved (position -> slot through req_to_token -> tier through the owner table), dequantized exactly as the
+// Sparse attention over selected positions of the quantized pools, fused: the selected positions of each query row
+// are resolved (position -> slot through req_to_token -> tier through the owner table), dequantized exactly as the
 // reference's compact gather does (bf16(q * s * sm), patches/kv_tiers.py:446-538) and attended in one pass, with no
-// bf16 scratch.  The reference's decode gathers into that scratch and runs FlashAttention-2 over it
-// (sglang/qwen4exp-serving-73a255206f.patch:1832-1882); this kernel replaces both launches' work, and its partials
-// go through the same combine as the dense decode.
+// bf16 scratch.  Two entry points share the kernel:
+//   * kvt_sparse_decode (one query row per request): the reference's decode gathers the top-k positions into that
+//     scratch and runs FlashAttention-2 over it (sglang/qwen4exp-serving-73a255206f.patch:1832-1882).  A block takes
+//     64 selected columns of one (request, KV head) and writes an unnormalized partial; kvt_decode_combine merges
+//     the column splits as it merges the dense decode's.
+//   * kvt_sparse_prefill (one query row per chunk query): the reference's paged prefix-chunk attention
+//     sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:141-365).  A block takes every selected column of
+//     one (query, KV head): query j of a chunk of q_len queries over a context of kv_len attends the valid entries
+//     (0 <= idx < kv_len) among the first min(topk, j + kv_len - q_len + 1) of its index row
+//     (patches/kv_paged_prefix.py:199-229) and writes its normalized output (0/0 = NaN when nothing is attended).
 //
-// One block of 4 wavefronts per (request, KV head, 64 selected columns), a wavefront per tile of 16: the tile's
-// K and V rows are dequantized into LDS as bf16, then QK^T and P.V run as bf16 16x16x16 matrix-core steps with
-// fp32 accumulation:
+// Inside a block, 4 wavefronts take 16-column tiles in turn.  A tile's K and V rows are dequantized into the
+// wavefront's LDS rows as bf16, then QK^T and P.V run as bf16 16x16x16 matrix-core steps with fp32 accumulation:
 //   S^T[row][head] = K[row][:] . Q[head][:]   (A = K tile, B = Q^T; 16 steps over the 256 channels)
 //   O[head][ch]   += P[head][row] V[row][ch]  (A = P straight from S^T's accumulator layout as bf16 high part
 //                                               + bf16 remainder, B = V tile by the transposing LDS read)
-// The 4 wavefronts merge through LDS and the block writes an unnormalized partial (m, l, o) per q head (m in
-// natural-log units, as the dense decode's); kvt_decode_combine merges the column splits.  Columns c of request b attend when c < the request's
-// valid count (cu_k[b + 1] - cu_k[b]) and 0 <= indices[b][c] < seq_lens[b] - the columns the reference's gather
-// writes and its attention reads when the valid positions come first (the indexer pads with -1 at the end).
+// with an online softmax across a wavefront's tiles.  The 16 accumulator rows hold up to 16 q heads per KV head
+// (GQA 8 of the configurations, 12 of the served model).  The 4 wavefronts merge through LDS, 8 heads per pass.
+// In decode, columns c of request b attend when c < the request's valid count (cu_k[b + 1] - cu_k[b]) and
+// 0 <= indices[b][c] < seq_lens[b] - the columns the reference's gather writes and its attention reads when the
+// valid positions come first (the indexer pads with -1 at the end).
 //
 // Kinds (the compact gather's codes): 0 INT8-G pool, 1 INT4-G32 pool, 2 tiered (INT8-G ring over INT4-G32 rows,
 // owner test).
@@ -65,10 +72,18 @@ struct SparseArgs {
   uint32_t rows8;        // rows of the INT8 tensors (ring R when tiered, the pool otherwise)
   uint32_t rows4;        // rows of the INT4 pool
   float scale;
-  const uint16_t* q;       // bf16 [batch, Hq, D] with batch stride q_stride_b
-  int64_t q_stride_b;
-  float* part_o;           // [(b H + h) n_splits + split][gs][D]
-  float* part_ml;          // [(b H + h) n_splits + split][gs][2]
+  const uint16_t* q;       // bf16 query rows: row r, q head j at q + r sq_n + j sq_h
+  int64_t sq_n, sq_h;
+  int64_t si_m, si_g, si_n;  // indices of row r, KV head h, column c at indices + r si_m + h si_g + c si_n
+  float* part_o;           // decode: [(b H + h) n_splits + split][gs][D]
+  float* part_ml;          // decode: [(b H + h) n_splits + split][gs][2]
+  // prefill rows: chunk b holds rows cu_q[b] .. cu_q[b + 1] over a context of kv_lens[b] positions
+  const void* cu_q;
+  int cuq64;
+  const int32_t* kv_lens;
+  void* out;               // bf16 or fp32 (out_f32) rows: row r, q head j at out + r so_n + j so_h
+  int out_f32;
+  int64_t so_n, so_h;
 };
 
 KVT_DEV int64_t load_idx(const void* p, int is64, int64_t i) {
@@ -139,41 +154,21 @@ KVT_DEV void issue_tile(const PoolRsrc& P, int flags, uint32_t coff, uint32_t so
   }
 }
 
+// One 16-column tile of a wavefront, folded into its running softmax state (m, l per q head n16 of this lane, o):
+// resolve the columns, load and dequantize K into the wavefront's LDS rows, S^T = K Q^T, dequantize V into the same
+// rows, online softmax, O += P V.
 template <int KIND, int G8>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) sparse_decode_kernel(SparseArgs A) {
-  // per wavefront: its tile's K and V rows (bf16); after the tiles, the same space holds the 4 partials' merge
-  // one tile buffer per wavefront: K rows until S is formed, then V rows (LDS per block 42 KB: 3 blocks per CU)
-  __shared__ __align__(16) uint16_t kv[kWaves][kRows * kKPitch];
-  __shared__ __align__(16) uint16_t qs[kHeads * kKPitch];   // the group's q heads, bf16 (zero beyond gs)
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int split = blockIdx.x;
-  const int b = blockIdx.y / A.H;
-  const int h = blockIdx.y - b * A.H;
-  const int H = A.H, gs = A.gs;
-  const int64_t item = ((int64_t)b * H + h) * A.n_splits + split;
+KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt, int64_t c0,
+                         int64_t c_end, const int32_t* idx_row, int64_t L, int64_t req, int h, int lane,
+                         const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16]) {
+  const int H = A.H;
   const int n16 = lane & 15, kq = lane >> 4;
-  uint16_t* kt = kv[wave];
-  uint16_t* vr = kv[wave];   // the same rows: V is dequantized once the K reads of S are issued
-
-  // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
-#pragma unroll
-  for (int i = threadIdx.x; i < kHeads * kD / 8; i += 64 * kWaves) {
-    const int hq = i / (kD / 8), ch = i - hq * (kD / 8);
-    uint4 w = {0u, 0u, 0u, 0u};
-    if (hq < gs) w = *reinterpret_cast<const uint4*>(A.q + b * A.q_stride_b + (int64_t)(h * gs + hq) * kD + 8 * ch);
-    *reinterpret_cast<uint4*>(&qs[hq * kKPitch + 8 * ch]) = w;
-  }
-
-  // resolve: lane r < 16 of wavefront w resolves column split * 64 + 16 w + r to (valid, hot, row)
-  const int64_t vcount = load_idx(A.cu_k, A.cu64, b + 1) - load_idx(A.cu_k, A.cu64, b);
-  const int64_t L = A.seq_lens[b];
-  const int64_t req = load_idx(A.req_indices, A.req64, b);
-  const int64_t col = (int64_t)split * kCols + kRows * wave + n16;
+  // lane r < 16 resolves column c0 + r to (valid, hot, row)
+  const int64_t col = c0 + n16;
   bool valid = false, hot = KIND == 0;
   int64_t row = 0;
-  if (lane < kRows && col < vcount && col < A.topk) {
-    const int64_t pos = A.indices[(int64_t)b * A.idx_stride + col];
+  if (lane < kRows && col < c_end) {
+    const int64_t pos = idx_row[col * A.si_n];
     if (pos >= 0 && pos < L) {
       valid = true;
       const int64_t slot = A.req_to_token[req * A.req_stride + pos];
@@ -192,6 +187,132 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   const int64_t rh = row * H + h;
   const uint32_t coff = !valid ? kNoRow : (uint32_t)(hot ? rh * kD : rh * (kD / 2));
   const uint32_t soff = !valid ? kNoRow : (uint32_t)(hot ? rh * (kD / G8) * 2 : rh * (kD / kG4) * 2);
+  TileLoads T;
+  issue_tile<G8>(P, flags, coff, soff, lane, T);
+
+  // K rows into this wavefront's LDS rows (row-major); a wavefront's LDS accesses complete in order, so these
+  // stores land after the previous tile's V reads
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const bool ht = (T.fl[r] & 2) != 0;
+    float c[4], x[4];
+    codes4(ht, T.kw[r], lane, c);
+    const float sk = f16_bits_to_f32((uint16_t)T.ks[r]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = c[i] * sk * smk[i];
+    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
+  }
+  // S^T = K Q^T: lane l holds rows 4 (l >> 4) + i of q head l & 15
+  f4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const uint2 ka = *reinterpret_cast<const uint2*>(&kt[n16 * kKPitch + 16 * k + 4 * kq]);
+    const uint2 qb = *reinterpret_cast<const uint2*>(&qs[n16 * kKPitch + 16 * k + 4 * kq]);
+    s = mfma_bf16(__builtin_bit_cast(bf4, ka), __builtin_bit_cast(bf4, qb), s);
+  }
+  // V rows into the same LDS rows (the stores stay behind the K reads above, which may alias them)
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const bool ht = (T.fl[r] & 2) != 0;
+    float c[4], x[4];
+    codes4(ht, T.vw[r], lane, c);
+    const float sv = f16_bits_to_f32((uint16_t)T.vs[r]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = c[i] * sv * smv[i];
+    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
+  }
+  // online softmax (log2 units): rows 4 kq + i of this lane's head, the other 12 rows in lanes n16 + 16 j
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float cs = A.scale * kLog2e;
+  float tv[4], mloc = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = __shfl(flags, 4 * kq + i, 64);   // the row's resolve lane
+    tv[i] = (f & 1) ? s[i] * cs : -INFINITY;
+    mloc = fmaxf(mloc, tv[i]);
+  }
+  const float m_new = fmaxf(m_run, max_xor16_32(mloc));
+  const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+  float p[4], lsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    p[i] = m_new == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(tv[i] - m_new);
+    lsum += p[i];
+  }
+  l_run = l_run * alpha + sum_xor16_32(lsum);
+  m_run = m_new;
+  // o[n][i] is head 4 kq + i: its rescale factor lives in lane 4 kq + i
+  float ai[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, 4 * kq + i, 64);
+  // P as bf16 high part + bf16 remainder (two products per step): P keeps ~16 significant bits, against 8 for a
+  // plain bf16 cast, so a peaked softmax stays within the fp32 reference's tolerance
+  const uint32_t h01 = bf16x2(p[0], p[1]), h23 = bf16x2(p[2], p[3]);
+  const uint32_t l01 = bf16x2(p[0] - __uint_as_float(h01 << 16), p[1] - __uint_as_float(h01 & 0xffff0000u));
+  const uint32_t l23 = bf16x2(p[2] - __uint_as_float(h23 << 16), p[3] - __uint_as_float(h23 & 0xffff0000u));
+  const bf4 pa = __builtin_bit_cast(bf4, uint2{h01, h23});
+  const bf4 pb = __builtin_bit_cast(bf4, uint2{l01, l23});
+  // O = P V.  B = V[rows 4 kq + k][channel 16 n + n16] by the transposing read: in each 16-lane group, lane L's
+  // element k comes from element L & 3 of the 8 bytes lane 4 k + (L >> 2) addresses, so lane m addresses
+  // V[4 kq + (m >> 2)][16 n + 4 (m & 3)]
+  const uint32_t vbase = (uint32_t)(uintptr_t)&kt[(4 * kq + (n16 >> 2)) * kKPitch + 4 * (n16 & 3)];
+#pragma unroll
+  for (int n = 0; n < 16; ++n) {
+    const bf4 vop = __builtin_bit_cast(
+        bf4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vbase + 32u * (uint32_t)n)));
+    f4 acc = o[n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= ai[i];
+    o[n] = mfma_bf16(pb, vop, mfma_bf16(pa, vop, acc));
+  }
+}
+
+// LDS of a block: one tile buffer per wavefront (K rows until S is formed, then V rows; 42 KB per block), after the
+// tiles the same space holds the merge of the 4 wavefronts; and the group's q heads, bf16 (zero beyond gs)
+struct BlockLds {
+  uint16_t kv[kWaves][kRows * kKPitch];
+  uint16_t qs[kHeads * kKPitch];
+};
+
+template <int KIND, int G8, bool ROWS>
+KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
+  auto& kv = S.kv;
+  uint16_t* qs = S.qs;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = A.H, gs = A.gs;
+  const int b = blockIdx.y / H;
+  const int h = blockIdx.y - b * H;
+  // the block's query row, context length and column range
+  int64_t qrow, L, c_begin, c_end;
+  if constexpr (ROWS) {
+    const int64_t q0 = load_idx(A.cu_q, A.cuq64, b), q1 = load_idx(A.cu_q, A.cuq64, b + 1);
+    const int64_t j = blockIdx.x;
+    if (q0 + j >= q1) return;   // block-uniform: the chunk is shorter than the grid
+    qrow = q0 + j;
+    L = A.kv_lens[b];
+    const int64_t visible = j + L - (q1 - q0) + 1;
+    c_begin = 0;
+    c_end = visible < (int64_t)A.topk ? (visible > 0 ? visible : 0) : (int64_t)A.topk;
+  } else {
+    qrow = b;
+    L = A.seq_lens[b];
+    const int64_t vcount = load_idx(A.cu_k, A.cu64, b + 1) - load_idx(A.cu_k, A.cu64, b);
+    c_begin = (int64_t)blockIdx.x * kCols;
+    const int64_t lim = vcount < (int64_t)A.topk ? vcount : (int64_t)A.topk;
+    c_end = c_begin + kCols < lim ? c_begin + kCols : lim;
+  }
+
+  // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
+#pragma unroll
+  for (int i = threadIdx.x; i < kHeads * kD / 8; i += 64 * kWaves) {
+    const int hq = i / (kD / 8), ch = i - hq * (kD / 8);
+    uint4 w = {0u, 0u, 0u, 0u};
+    if (hq < gs) w = *reinterpret_cast<const uint4*>(A.q + qrow * A.sq_n + (int64_t)(h * gs + hq) * A.sq_h + 8 * ch);
+    *reinterpret_cast<uint4*>(&qs[hq * kKPitch + 8 * ch]) = w;
+  }
+  const int64_t req = load_idx(A.req_indices, A.req64, b);
+  const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
   PoolRsrc P;
   {
     const uint32_t n8 = A.rows8 * (uint32_t)H * kD, n4 = A.rows4 * (uint32_t)H * (kD / 2);
@@ -205,9 +326,6 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     P.ks4 = rsrc(A.ks, KIND == 0 ? 0u : s4);
     P.vs4 = rsrc(A.vs, KIND == 0 ? 0u : s4);
   }
-  TileLoads T;
-  issue_tile<G8>(P, flags, coff, soff, lane, T);
-
   // smoothing factors of this lane's channels 4 lane .. 4 lane + 3
   float smk[4] = {1.f, 1.f, 1.f, 1.f}, smv[4] = {1.f, 1.f, 1.f, 1.f};
   if (A.sm_k != nullptr) {
@@ -224,111 +342,58 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     smv[2] = f16_bits_to_f32((uint16_t)w.y);
     smv[3] = f16_bits_to_f32((uint16_t)(w.y >> 16));
   }
+  __syncthreads();   // q staged
 
-  // dequantize the tile's K rows into this wavefront's LDS rows (row-major)
+  float m_run = -INFINITY, l_run = 0.f;   // of q head lane & 15
+  f4 o[16];                               // O[head 4 (lane >> 4) + i][channel 16 n + (lane & 15)]
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const bool ht = (T.fl[r] & 2) != 0;
-    float c[4], x[4];
-    codes4(ht, T.kw[r], lane, c);
-    const float sk = f16_bits_to_f32((uint16_t)T.ks[r]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = c[i] * sk * smk[i];
-    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
-  }
-  __syncthreads();   // q staged (the tile rows are this wavefront's own: its LDS accesses are in order)
-
-  // S^T = K Q^T: lane l holds rows 4 (l >> 4) + i of q head l & 15
-  f4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const uint2 ka = *reinterpret_cast<const uint2*>(&kt[n16 * kKPitch + 16 * k + 4 * kq]);
-    const uint2 qb = *reinterpret_cast<const uint2*>(&qs[n16 * kKPitch + 16 * k + 4 * kq]);
-    s = mfma_bf16(__builtin_bit_cast(bf4, ka), __builtin_bit_cast(bf4, qb), s);
-  }
-  // V rows into the same LDS rows: a wavefront's LDS accesses complete in order, so these stores land after the K
-  // reads above (the compiler keeps stores behind loads that may alias them)
-#pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const bool ht = (T.fl[r] & 2) != 0;
-    float c[4], x[4];
-    codes4(ht, T.vw[r], lane, c);
-    const float sv = f16_bits_to_f32((uint16_t)T.vs[r]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = c[i] * sv * smv[i];
-    *reinterpret_cast<uint2*>(&vr[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
-  }
-  // softmax over the tile's rows (log2 units): rows 4 kq + i of this lane, the other 12 in lanes n16 + 16 j
-  constexpr float kLog2e = 1.4426950408889634f;
-  const float cs = A.scale * kLog2e;
-  float tv[4], mloc = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = __shfl(flags, 4 * kq + i, 64);   // the row's resolve lane
-    tv[i] = (f & 1) ? s[i] * cs : -INFINITY;
-    mloc = fmaxf(mloc, tv[i]);
-  }
-  const float m = max_xor16_32(mloc);
-  float p[4], lsum = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    p[i] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(tv[i] - m);
-    lsum += p[i];
-  }
-  const float l = sum_xor16_32(lsum);
-  // P as bf16 high part + bf16 remainder (two products per step): P keeps ~16 significant bits, against 8 for a
-  // plain bf16 cast, so a peaked softmax stays within the fp32 reference's tolerance
-  const uint32_t h01 = bf16x2(p[0], p[1]), h23 = bf16x2(p[2], p[3]);
-  const uint32_t l01 = bf16x2(p[0] - __uint_as_float(h01 << 16), p[1] - __uint_as_float(h01 & 0xffff0000u));
-  const uint32_t l23 = bf16x2(p[2] - __uint_as_float(h23 << 16), p[3] - __uint_as_float(h23 & 0xffff0000u));
-  const bf4 pa = __builtin_bit_cast(bf4, uint2{h01, h23});
-  const bf4 pb = __builtin_bit_cast(bf4, uint2{l01, l23});
-  // O = P V.  B = V[rows 4 kq + k][channel 16 n + n16] by the transposing read: in each 16-lane group, lane L's
-  // element k comes from element L & 3 of the 8 bytes lane 4 k + (L >> 2) addresses, so lane m addresses
-  // V[4 kq + (m >> 2)][16 n + 4 (m & 3)]
-  f4 o[16];   // O[head 4 kq + i][channel 16 n + n16]
-  const uint32_t vbase = (uint32_t)(uintptr_t)&vr[(4 * kq + (n16 >> 2)) * kKPitch + 4 * (n16 & 3)];
-#pragma unroll
-  for (int n = 0; n < 16; ++n) {
-    const bf4 vop = __builtin_bit_cast(
-        bf4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vbase + 32u * (uint32_t)n)));
-    o[n] = mfma_bf16(pb, vop, mfma_bf16(pa, vop, f4{0.f, 0.f, 0.f, 0.f}));
+  for (int n = 0; n < 16; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (ROWS) {
+    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols)
+      attend_tile<KIND, G8>(A, P, qs, kv[wave], c0, c_end, idx_row, L, req, h, lane, smk, smv, m_run, l_run, o);
+  } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads
+    if (c_begin + kRows * wave < c_end)
+      attend_tile<KIND, G8>(A, P, qs, kv[wave], c_begin + kRows * wave, c_end, idx_row, L, req, h, lane, smk, smv,
+                            m_run, l_run, o);
   }
 
-  // merge the 4 wavefronts' partials through LDS (the tile rows are done with): wavefront w stores O rows of heads
-  // < gs and (m, l) per head; then thread t merges head t / 32, channels 8 (t % 32) .. + 7 over the 4
-  __syncthreads();
-  float* mo = reinterpret_cast<float*>(&kv[0][0]);                 // [wave][head < 8][256]
-  float* mml = mo + kWaves * 8 * kD;                                // [wave][head][2]
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int hq = 4 * kq + i;
-    if (hq < gs) {
-#pragma unroll
-      for (int n = 0; n < 16; ++n) mo[(wave * 8 + hq) * kD + 16 * n + n16] = o[n][i];
-    }
-  }
+  // merge the 4 wavefronts through LDS, 8 q heads per pass: wavefront w stores the O rows of the pass's heads and
+  // (m, l) of every head; thread t then merges head t / 32 of the pass, channels 8 (t % 32) .. + 7, over the 4
+  __syncthreads();   // every wavefront is done with its tile rows
+  float* mo = reinterpret_cast<float*>(&kv[0][0]);   // [wave][8 heads][256]
+  float* mml = mo + kWaves * 8 * kD;                  // [wave][16 heads][2]
+  const int kq = lane >> 4, n16 = lane & 15;
   if (lane < gs) {
-    mml[(wave * 8 + lane) * 2] = m;
-    mml[(wave * 8 + lane) * 2 + 1] = l;
+    mml[(wave * kHeads + lane) * 2] = m_run;
+    mml[(wave * kHeads + lane) * 2 + 1] = l_run;
   }
-  __syncthreads();
-  {
-    const int hq = threadIdx.x >> 5, c0 = 8 * (threadIdx.x & 31);
+  for (int hh = 0; hh < gs; hh += 8) {
+    if (hh > 0) __syncthreads();   // the previous pass's reads are done
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hq = 4 * kq + i - hh;
+      if (hq >= 0 && hq < 8 && hq + hh < gs) {
+#pragma unroll
+        for (int n = 0; n < 16; ++n) mo[(wave * 8 + hq) * kD + 16 * n + n16] = o[n][i];
+      }
+    }
+    __syncthreads();
+    const int hq = hh + (threadIdx.x >> 5), c0 = 8 * (threadIdx.x & 31);
     if (hq < gs) {
       float mw[kWaves], M = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        mw[w] = mml[(w * 8 + hq) * 2];
+        mw[w] = mml[(w * kHeads + hq) * 2];
         M = fmaxf(M, mw[w]);
       }
       float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, lt = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        const float a = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
-        lt += a * mml[(w * 8 + hq) * 2 + 1];
-        const float4 o0 = *reinterpret_cast<const float4*>(&mo[(w * 8 + hq) * kD + c0]);
-        const float4 o1 = *reinterpret_cast<const float4*>(&mo[(w * 8 + hq) * kD + c0 + 4]);
+        const float a = mw[w] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[w] - M);
+        lt += a * mml[(w * kHeads + hq) * 2 + 1];
+        const float* src = &mo[(w * 8 + (hq - hh)) * kD + c0];
+        const float4 o0 = *reinterpret_cast<const float4*>(src);
+        const float4 o1 = *reinterpret_cast<const float4*>(src + 4);
         acc[0] += a * o0.x;
         acc[1] += a * o0.y;
         acc[2] += a * o0.z;
@@ -338,16 +403,87 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         acc[6] += a * o1.z;
         acc[7] += a * o1.w;
       }
-      float* dst = A.part_o + (item * gs + hq) * kD + c0;
-      *reinterpret_cast<float4*>(dst) = float4{acc[0], acc[1], acc[2], acc[3]};
-      *reinterpret_cast<float4*>(dst + 4) = float4{acc[4], acc[5], acc[6], acc[7]};
-      if (c0 == 0) {   // (m, l) of the block's partial, m in natural-log units
-        constexpr float kLn2 = 0.6931471805599453f;
-        A.part_ml[(item * gs + hq) * 2 + 0] = M == -INFINITY ? -INFINITY : M * kLn2;
-        A.part_ml[(item * gs + hq) * 2 + 1] = lt;
+      if constexpr (ROWS) {
+        // normalized output; nothing attended gives 0 / 0 = NaN (patches/kv_paged_prefix.py:259)
+        const int64_t off = qrow * A.so_n + (int64_t)(h * gs + hq) * A.so_h + c0;
+        if (A.out_f32) {
+          float* dst = reinterpret_cast<float*>(A.out) + off;
+          *reinterpret_cast<float4*>(dst) = float4{acc[0] / lt, acc[1] / lt, acc[2] / lt, acc[3] / lt};
+          *reinterpret_cast<float4*>(dst + 4) = float4{acc[4] / lt, acc[5] / lt, acc[6] / lt, acc[7] / lt};
+        } else {
+          uint16_t* dst = reinterpret_cast<uint16_t*>(A.out) + off;
+          *reinterpret_cast<uint4*>(dst) = uint4{bf16x2(acc[0] / lt, acc[1] / lt), bf16x2(acc[2] / lt, acc[3] / lt),
+                                                 bf16x2(acc[4] / lt, acc[5] / lt), bf16x2(acc[6] / lt, acc[7] / lt)};
+        }
+      } else {
+        const int64_t item = ((int64_t)b * H + h) * A.n_splits + blockIdx.x;
+        float* dst = A.part_o + (item * gs + hq) * kD + c0;
+        *reinterpret_cast<float4*>(dst) = float4{acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<float4*>(dst + 4) = float4{acc[4], acc[5], acc[6], acc[7]};
+        if (c0 == 0) {   // (m, l) of the block's partial, m in natural-log units
+          constexpr float kLn2 = 0.6931471805599453f;
+          A.part_ml[(item * gs + hq) * 2 + 0] = M == -INFINITY ? -INFINITY : M * kLn2;
+          A.part_ml[(item * gs + hq) * 2 + 1] = lt;
+        }
       }
     }
   }
+}
+
+// decode: one tile per wavefront, 3 blocks per CU
+template <int KIND, int G8>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) sparse_decode_kernel(SparseArgs A) {
+  __shared__ __align__(16) BlockLds S;
+  sparse_attn_block<KIND, G8, false>(A, S);
+}
+
+// prefill rows: a wavefront loops over its row's tiles with the accumulators live, 2 blocks per CU
+template <int KIND, int G8>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) sparse_prefill_kernel(SparseArgs A) {
+  __shared__ __align__(16) BlockLds S;
+  sparse_attn_block<KIND, G8, true>(A, S);
+}
+
+// Shared argument checks and pool resources of both entry points; returns KVT_OK or a status.
+int pool_args(int kind, int64_t pool_rows, const void* ring_k, const void* owner, int64_t ring_mask, int H, int Hq,
+              int D, int group8, int64_t* rows8, int64_t* rows4) {
+  if (H <= 0 || Hq % H != 0 || Hq / H > kHeads || D != kD || kind < 0 || kind > 2) return KVT_EINVAL;
+  if (kind == 2 && (owner == nullptr || ring_k == nullptr || ((ring_mask + 1) & ring_mask) != 0)) return KVT_EINVAL;
+  if (pool_rows <= 0 || (kind != 1 && group8 != 64 && group8 != 256)) return KVT_EINVAL;
+  // byte offsets are 32-bit and must stay below kNoRow (rows * H * D bytes of INT8 codes, / 2 for INT4)
+  *rows8 = kind == 2 ? ring_mask + 1 : (kind == 0 ? pool_rows : 0);
+  *rows4 = kind == 0 ? 0 : pool_rows;
+  if (*rows8 * H * kD >= (int64_t)kNoRow || *rows4 * H * (kD / 2) >= (int64_t)kNoRow) return KVT_ERANGE;
+  return KVT_OK;
+}
+
+template <bool ROWS>
+int launch(int kind, int group8, dim3 grid, hipStream_t st, const SparseArgs& A) {
+#define KVT_SD(KIND_, G_)                                                                                  \
+  do {                                                                                                     \
+    if constexpr (ROWS)                                                                                    \
+      hipLaunchKernelGGL((sparse_prefill_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);           \
+    else                                                                                                   \
+      hipLaunchKernelGGL((sparse_decode_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);            \
+  } while (0)
+  if (kind == 1) {
+    KVT_SD(1, 64);
+  } else if (group8 == 64) {
+    if (kind == 2) {
+      KVT_SD(2, 64);
+    } else {
+      KVT_SD(0, 64);
+    }
+  } else {
+    if (kind == 2) {
+      KVT_SD(2, 256);
+    } else {
+      KVT_SD(0, 256);
+    }
+  }
+#undef KVT_SD
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
 }
 
 }  // namespace
@@ -361,43 +497,54 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
                       const void* indices, int64_t idx_stride, const void* seq_lens, const void* cu_k,
                       int cu_is_int64, int batch, int topk, int H, int Hq, int D, int group8, float scale,
                       int n_splits, void* part_o, void* part_ml, void* stream) {
-  if (batch <= 0 || topk <= 0 || H <= 0 || Hq % H != 0 || Hq / H > 8 || D != kD) return KVT_EINVAL;
-  if (n_splits < (topk + kCols - 1) / kCols || kind < 0 || kind > 2) return KVT_EINVAL;
-  if (kind == 2 && (owner == nullptr || ring_k == nullptr || ((ring_mask + 1) & ring_mask) != 0)) return KVT_EINVAL;
-  if (pool_rows <= 0) return KVT_EINVAL;
-  // byte offsets are 32-bit and must stay below kNoRow (rows * H * D bytes of INT8 codes, / 2 for INT4)
-  const int64_t rows8 = kind == 2 ? ring_mask + 1 : (kind == 0 ? pool_rows : 0);
-  const int64_t rows4 = kind == 0 ? 0 : pool_rows;
-  if (rows8 * H * kD >= (int64_t)kNoRow || rows4 * H * (kD / 2) >= (int64_t)kNoRow) return KVT_ERANGE;
-  SparseArgs A{k, v, (const uint16_t*)k_scale, (const uint16_t*)v_scale, (const int8_t*)ring_k, (const int8_t*)ring_v,
-               (const uint16_t*)ring_ks, (const uint16_t*)ring_vs, (const int32_t*)owner, ring_mask,
-               (const uint16_t*)sm_k, (const uint16_t*)sm_v, (const int32_t*)req_to_token, req_stride, req_indices,
-               req_is_int64, (const int32_t*)indices, idx_stride, (const int32_t*)seq_lens, cu_k, cu_is_int64, topk,
-               H, Hq / H, n_splits, (uint32_t)rows8, (uint32_t)rows4, scale, (const uint16_t*)q, q_stride_b,
-               (float*)part_o, (float*)part_ml};
-  const dim3 grid((unsigned)n_splits, (unsigned)(batch * H));
-  hipStream_t st = (hipStream_t)stream;
-#define KVT_SD(KIND_, G_) hipLaunchKernelGGL((sparse_decode_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A)
-  if (kind == 1) {
-    KVT_SD(1, 64);
-  } else if (group8 == 64) {
-    if (kind == 2) {
-      KVT_SD(2, 64);
-    } else {
-      KVT_SD(0, 64);
-    }
-  } else if (group8 == 256) {
-    if (kind == 2) {
-      KVT_SD(2, 256);
-    } else {
-      KVT_SD(0, 256);
-    }
-  } else {
-    return KVT_EINVAL;
-  }
-#undef KVT_SD
-  KVT_CHECK_LAUNCH();
-  return KVT_OK;
+  if (batch <= 0 || topk <= 0 || n_splits < (topk + kCols - 1) / kCols) return KVT_EINVAL;
+  if ((q_stride_b & 7) != 0 || ((uintptr_t)q & 15) != 0) return KVT_EINVAL;
+  int64_t rows8 = 0, rows4 = 0;
+  const int st_ = pool_args(kind, pool_rows, ring_k, owner, ring_mask, H, Hq, D, group8, &rows8, &rows4);
+  if (st_ != KVT_OK) return st_;
+  SparseArgs A{};
+  A.k = k, A.v = v, A.ks = (const uint16_t*)k_scale, A.vs = (const uint16_t*)v_scale;
+  A.rk = (const int8_t*)ring_k, A.rv = (const int8_t*)ring_v, A.rks = (const uint16_t*)ring_ks;
+  A.rvs = (const uint16_t*)ring_vs, A.owner = (const int32_t*)owner, A.ring_mask = ring_mask;
+  A.sm_k = (const uint16_t*)sm_k, A.sm_v = (const uint16_t*)sm_v;
+  A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
+  A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.idx_stride = idx_stride;
+  A.seq_lens = (const int32_t*)seq_lens, A.cu_k = cu_k, A.cu64 = cu_is_int64, A.topk = topk;
+  A.H = H, A.gs = Hq / H, A.n_splits = n_splits, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
+  A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = q_stride_b, A.sq_h = kD;
+  A.si_m = idx_stride, A.si_g = 0, A.si_n = 1, A.part_o = (float*)part_o, A.part_ml = (float*)part_ml;
+  return launch<false>(kind, group8, dim3((unsigned)n_splits, (unsigned)(batch * H)), (hipStream_t)stream, A);
+}
+
+int kvt_sparse_prefill(int kind, const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                       const void* kv_lens, int batch, int max_q, const void* indices, int64_t si_m, int64_t si_g,
+                       int64_t si_n, int topk, const void* k, const void* v, const void* k_scale, const void* v_scale,
+                       int64_t pool_rows, const void* ring_k, const void* ring_v, const void* ring_ks,
+                       const void* ring_vs, const void* owner, int64_t ring_mask, const void* sm_k, const void* sm_v,
+                       const void* req_to_token, int64_t req_stride, const void* req_indices, int req_is_int64, int H,
+                       int Hq, int D, int group8, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
+                       void* stream) {
+  if (batch < 0 || max_q < 0 || topk < 0) return KVT_EINVAL;
+  // 16-byte q loads and output stores: row and head strides multiples of 8 elements (4 for fp32 output)
+  if ((sq_n & 7) != 0 || (sq_h & 7) != 0 || ((uintptr_t)q & 15) != 0) return KVT_EINVAL;
+  if (((uintptr_t)out & 15) != 0 || (so_n & (out_f32 ? 3 : 7)) != 0 || (so_h & (out_f32 ? 3 : 7)) != 0) return KVT_EINVAL;
+  int64_t rows8 = 0, rows4 = 0;
+  const int st_ = pool_args(kind, pool_rows, ring_k, owner, ring_mask, H, Hq, D, group8, &rows8, &rows4);
+  if (st_ != KVT_OK) return st_;
+  if (batch == 0 || max_q == 0) return KVT_OK;
+  SparseArgs A{};
+  A.k = k, A.v = v, A.ks = (const uint16_t*)k_scale, A.vs = (const uint16_t*)v_scale;
+  A.rk = (const int8_t*)ring_k, A.rv = (const int8_t*)ring_v, A.rks = (const uint16_t*)ring_ks;
+  A.rvs = (const uint16_t*)ring_vs, A.owner = (const int32_t*)owner, A.ring_mask = ring_mask;
+  A.sm_k = (const uint16_t*)sm_k, A.sm_v = (const uint16_t*)sm_v;
+  A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
+  A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.topk = topk;
+  A.H = H, A.gs = Hq / H, A.n_splits = 1, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
+  A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = sq_n, A.sq_h = sq_h;
+  A.si_m = si_m, A.si_g = si_g, A.si_n = si_n;
+  A.cu_q = cu_q, A.cuq64 = cu_q_is_int64, A.kv_lens = (const int32_t*)kv_lens;
+  A.out = out, A.out_f32 = out_f32, A.so_n = so_n, A.so_h = so_h;
+  return launch<true>(kind, group8, dim3((unsigned)max_q, (unsigned)(batch * H)), (hipStream_t)stream, A);
 }
 
 }  // extern "C"

@@ -245,7 +245,7 @@ def qwen_sparse_decode_attn(
     assert q.dim() == 3 and q.shape[0] >= batch and q.shape[2] == dim and q.dtype == torch.bfloat16
     assert q.stride(2) == 1 and q.stride(1) == dim and q.stride(0) % 8 == 0
     Hq = q.shape[1]
-    assert Hq % heads == 0 and Hq // heads <= 8
+    assert Hq % heads == 0 and Hq // heads <= 16, "at most 16 q heads per KV head"
     assert sm_k is None or sm_k.shape == (heads, dim)
     assert sm_v is None or sm_v.shape == (heads, dim)
     assert req_to_token.dtype == torch.int32 and req_to_token.stride(1) == 1
@@ -285,6 +285,87 @@ def qwen_sparse_decode_attn(
     o16 = out.data_ptr() if out.dtype == torch.bfloat16 else None
     _lib.call("kvt_decode_combine", ws["sparse_o"].data_ptr(), ws["sparse_ml"].data_ptr(), int(batch), heads, Hq, dim,
               n_splits, 0, seq_lens.data_ptr(), None, o32, o16, out.stride(0), st)
+    return out
+
+
+def sparse_gqa_fwd_interface_paged(
+    q, indices, cu_q, kv_lens, req_to_token, req_indices, k_buf, v_buf, k_scale, v_scale, sm_k, sm_v, scale,
+    max_q, kv_bits, ring_k=None, ring_v=None, ring_ks=None, ring_vs=None, owner=None, ring_mask=None, config=None,
+    out=None,
+):
+    """Prefix-chunk sparse attention read straight from a quantized pool (patches/kv_paged_prefix.py:267-365).
+
+    q: bf16 [total_q, Hq, D]; indices: int32 [total_q, topk] or [total_q, H, topk] (selected positions per query,
+    per KV head in the 3-d form); cu_q: int32 / int64 [batch + 1] (chunk b owns rows cu_q[b] .. cu_q[b + 1]);
+    kv_lens: int32 [batch], the full context lengths (prefix + chunk); req_to_token int32 [reqs, ctx] and
+    req_indices [batch] map positions to slots; k_buf / v_buf + k_scale / v_scale: the pool (int8 [rows, H, D] +
+    fp16 [rows, H, D / 64] for kv_bits 8, uint8 [rows, H, D / 2] + fp16 [rows, H, D / 32] for kv_bits 4); sm_k / sm_v
+    [H, D]; the ring arguments select the tiered pool.  Query j of chunk b attends the entries of its index row
+    among the first min(topk, j + kv_len - q_len + 1) that lie in [0, kv_len); an entry outside is ignored, and a row
+    with none comes out NaN (0/0), as the reference.  K/V rows are dequantized exactly as the gathers write them,
+    QK^T and P.V on bf16 matrix cores with fp32 accumulation.  max_q = the longest chunk (host int).  `config` is the
+    reference's Triton tile configuration and has no meaning here (accepted and ignored).  Returns a new bf16 tensor
+    shaped like q, as the reference; `out` (an addition: bf16 or fp32, shaped like q, unit last stride) receives the
+    result instead, the bf16 form being the fp32 one rounded to nearest even.
+    """
+    total_q, num_q_heads, head_dim = q.shape
+    _, heads, last = k_buf.shape
+    assert q.dtype == torch.bfloat16 and q.stride(2) == 1, "paged prefix attention needs bf16 queries"
+    assert k_buf.is_contiguous() and v_buf.is_contiguous() and v_buf.shape == k_buf.shape
+    assert indices.dtype == torch.int32 and kv_lens.dtype == torch.int32 and kv_lens.is_contiguous()
+    assert indices.dim() in (2, 3) and indices.shape[0] >= total_q
+    assert cu_q.dtype in (torch.int32, torch.int64) and cu_q.is_contiguous(), cu_q.dtype
+    assert req_to_token.dtype == torch.int32 and req_to_token.dim() == 2 and req_to_token.stride(1) == 1
+    if owner is not None:                                   # tiered: INT8 ring over INT4 rows
+        dim = 2 * last
+        assert kv_bits == 4 and k_buf.dtype == torch.uint8 and v_buf.dtype == torch.uint8
+        R = _check_tier_args(heads, dim, k_scale, v_scale, ring_k, ring_v, ring_ks, ring_vs, owner, ring_mask)
+        kind, g8 = _KIND_TIERED, _group8(dim, ring_ks)
+    elif kv_bits == 4:                                      # int4_g32 pool
+        dim = 2 * last
+        assert k_buf.dtype == torch.uint8 and v_buf.dtype == torch.uint8
+        assert dim % KV_INT4_GROUP == 0 and _pow2(dim)
+        for t in (k_scale, v_scale):
+            assert t.dtype == torch.float16 and t.shape[1:] == (heads, dim // KV_INT4_GROUP) and t.is_contiguous()
+        R, kind, g8 = 1, _KIND_INT4, KV_INT8_GROUP
+    else:                                                   # int8_g64 pool
+        dim = last
+        assert k_buf.dtype == torch.int8 and v_buf.dtype == torch.int8
+        assert dim % KV_INT8_GROUP == 0 and _pow2(dim)
+        g8 = _group8(dim, k_scale)
+        for t in (k_scale, v_scale):
+            assert t.dtype == torch.float16 and t.shape[1:] == (heads, dim // g8) and t.is_contiguous()
+        R, kind = 1, _KIND_INT8
+    assert dim == head_dim, f"pool head_dim {dim} != query head_dim {head_dim}"
+    assert dim == 256, "the kernel is built for head_dim 256"
+    assert sm_k.shape == (heads, dim) and sm_v.shape == (heads, dim)
+    assert num_q_heads % heads == 0 and num_q_heads // heads <= 16, "at most 16 q heads per KV head"
+    if indices.dim() == 3:
+        assert indices.shape[1] == heads
+    assert config is None or len(config) == 3
+    batch = cu_q.shape[0] - 1
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    assert out.shape == q.shape and out.dtype in (torch.bfloat16, torch.float32) and out.stride(2) == 1
+    if batch == 0 or int(max_q) == 0:
+        return out
+    _lib.require_device(q, indices, cu_q, kv_lens, req_to_token, k_buf, v_buf, out)
+    if q.stride(0) % 8 or q.stride(1) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    topk = indices.shape[-1]
+    si_g = indices.stride(1) if indices.dim() == 3 else 0
+    rq, rq64 = _idx_args(req_indices)
+    tier = kind == _KIND_TIERED
+    smk, smv = sm_k.contiguous(), sm_v.contiguous()
+    _lib.call("kvt_sparse_prefill", kind, q.data_ptr(), q.stride(0), q.stride(1), cu_q.data_ptr(),
+              int(cu_q.dtype == torch.int64), kv_lens.data_ptr(), batch, int(max_q), indices.data_ptr(),
+              indices.stride(0), si_g, indices.stride(-1), int(topk), k_buf.data_ptr(), v_buf.data_ptr(),
+              k_scale.data_ptr(), v_scale.data_ptr(), k_buf.shape[0], _lib.ptr(ring_k) if tier else None,
+              _lib.ptr(ring_v) if tier else None, _lib.ptr(ring_ks) if tier else None,
+              _lib.ptr(ring_vs) if tier else None, _lib.ptr(owner) if tier else None, R - 1, smk.data_ptr(),
+              smv.data_ptr(), req_to_token.data_ptr(), req_to_token.stride(0), rq, rq64, heads, num_q_heads, dim,
+              g8, float(scale), out.data_ptr(), int(out.dtype == torch.float32), out.stride(0), out.stride(1),
+              _lib.stream())
     return out
 
 

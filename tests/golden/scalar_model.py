@@ -70,8 +70,23 @@ def pack_row(codes: List[int]) -> List[int]:
     return [((codes[2 * j] + 8) | ((codes[2 * j + 1] + 8) << 4)) & 0xFF for j in range(len(codes) // 2)]
 
 
-def dequant_row_bits(codes: List[int], scales: List[float], group: int) -> List[int]:
-    return [bf16_round_bits(F32(F32(c) * F32(scales[i // group]))) for i, c in enumerate(codes)]
+def dequant_row_bits(codes: List[int], scales: List[float], group: int, sm: List[float] = None) -> List[int]:
+    """bf16 bits of f32(c) * f32(s) (* f32(sm) per channel when given), products in fp32 left to right."""
+    out = []
+    for i, c in enumerate(codes):
+        x = F32(F32(c) * F32(scales[i // group]))
+        if sm is not None:
+            x = F32(x * F32(sm[i]))
+        out.append(bf16_round_bits(x))
+    return out
+
+
+def unpack_row(packed: List[int]) -> List[int]:
+    """INT4 bytes -> codes: low nibble the even channel, high nibble the odd one, each minus 8."""
+    codes = []
+    for b in packed:
+        codes += [(b & 15) - 8, (b >> 4) - 8]
+    return codes
 
 
 def requant_row(codes8: List[int], scales8: List[float], group8: int):

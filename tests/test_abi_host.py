@@ -101,10 +101,99 @@ def test_wrapper_contracts_cpu(kvt_pkg):
 
 
 def test_page_allocator_order(kvt_pkg):
-    """The device page allocator hands out pages in the same seeded order as the oracle's."""
+    """The page allocator hands out every page exactly once, in the order of torch.randperm under the seed (the
+    permutation the configurations ask for), and refuses a pop from an empty pool."""
     from kvtier.kvt import PageAllocator
-    from oracle.ref import PageAllocator as RefAlloc
-    a, b = PageAllocator(100, seed=3), RefAlloc(100, seed=3)
-    assert [a.pop() for _ in range(100)] == [b.pop() for _ in range(100)]
+    a = PageAllocator(100, seed=3)
+    got = [a.pop() for _ in range(100)]
+    assert sorted(got) == list(range(100)) and got != list(range(100))
+    assert got == torch.randperm(100, generator=torch.Generator().manual_seed(3)).tolist()
     with pytest.raises(RuntimeError):
         a.pop()
+
+
+def test_kv_buffer_descs(kvt_pkg):
+    """Descriptor names and row sizes of the per-slot buffers (gemv/test_kv_int4.py:311-313): k0.., v0.., ks0..,
+    vs0..; payload rows heads * D / 2 bytes (INT4) or heads * D (INT8); scale rows heads * groups * 2 bytes viewed as
+    (rows, row_bytes); the tiered pool's descriptors equal the INT4 pool's (the ring is not a per-slot buffer)."""
+    from kvtier.tiered_kv_pool import MHATokenToKVPoolInt4, MHATokenToKVPoolInt8, MHATokenToKVPoolTiered
+    size, page, H, D = 1024, 64, 2, 256
+    rows = size + page
+    mk = dict(size=size, page_size=page, head_num=H, head_dim=D, layer_num=2, device="cpu")
+    p4 = MHATokenToKVPoolInt4(dtype=torch.uint8, **mk)
+    d4 = p4._kv_buffer_descs
+    assert [d.name for d in d4] == ["k0", "k1", "v0", "v1", "ks0", "ks1", "vs0", "vs1"]
+    assert all(d.row_bytes == H * D // 2 and d.shape == (rows, H, D // 2) and d.tokens_per_row == 1 for d in d4[:4])
+    assert all(d.row_bytes == 32 and d.shape == (rows, 32) for d in d4[4:])
+    p8 = MHATokenToKVPoolInt8(dtype=torch.int8, **mk)
+    d8 = p8._kv_buffer_descs
+    assert [d.name for d in d8] == [d.name for d in d4]
+    assert all(d.row_bytes == H * D and d.shape == (rows, H, D) for d in d8[:4])
+    assert all(d.row_bytes == H * (D // 64) * 2 and d.shape == (rows, H * (D // 64) * 2) for d in d8[4:])
+    # the descriptor sizes account for every byte of the per-slot buffers
+    kb, vb = p8.get_kv_size_bytes()
+    assert kb + vb == sum(rows * d.row_bytes for d in d8)
+    import os
+    os.environ["SGLANG_KV_TIERS_W"] = "64"
+    try:
+        pt = MHATokenToKVPoolTiered(dtype=torch.uint8, **mk)
+    finally:
+        del os.environ["SGLANG_KV_TIERS_W"]
+    assert pt._kv_buffer_descs == d4
+    with pytest.raises(ValueError):
+        MHATokenToKVPoolInt4(dtype=torch.int8, **mk)
+    with pytest.raises(ValueError):
+        MHATokenToKVPoolInt8(dtype=torch.uint8, **mk)
+
+
+def test_hybrid_forwarders_and_backend_kwargs(kvt_pkg, monkeypatch):
+    """HybridLinearKVPool translates global layer ids of the full-attention layers to the pool's local ids and
+    forwards the quantized pools' accessors (patches/kv_tiers.py:787-808); the backend's dispatch helpers
+    (flat patch 1789-1827) return exactly the keyword arguments the gathers and the paged prefill accept."""
+    import inspect
+    from types import SimpleNamespace
+    from kvtier import sparse_attn as sa
+    from kvtier.backend_glue import KVDispatch
+    from kvtier.tiered_kv_pool import (HybridLinearKVPool, MHATokenToKVPoolInt4, MHATokenToKVPoolInt8,
+                                       MHATokenToKVPoolTiered)
+    monkeypatch.setenv("SGLANG_KV_TIERS_W", "64")
+    mk = dict(size=1024, page_size=64, head_num=2, head_dim=256, layer_num=3, device="cpu")
+    tiered = MHATokenToKVPoolTiered(dtype=torch.uint8, **mk)
+    hyb = HybridLinearKVPool(tiered, full_attention_layer_ids=[3, 7, 11])
+    lay = SimpleNamespace(layer_id=7)
+    assert hyb.get_key_buffer(7) is tiered.k_buffer[1] and hyb.get_value_buffer(11) is tiered.v_buffer[2]
+    assert [t.data_ptr() for t in hyb.get_kv_ring_buffer(7)] == [t.data_ptr() for t in tiered.get_kv_ring_buffer(1)]
+    assert hyb.get_kv_ring_owner() is tiered.ring_owner
+    assert hyb.get_kv_scale_buffer(3)[0] is tiered.k_scale_buffer[0]
+    assert hyb.get_kv_smooth_buffer(11)[1].data_ptr() == tiered.sm_v[2].data_ptr()
+    with pytest.raises(ValueError):
+        hyb.get_key_buffer(5)                     # a linear-attention layer has no KV here
+    glue = KVDispatch(hyb)
+    kb = hyb.get_key_buffer(7)
+    assert glue._kv_bits() == 4 and glue._kv_head_dim(kb) == 256 and glue._kv_scratch_dtype(kb) == torch.bfloat16
+    kw = glue._int8_gather_kwargs(kb, lay)
+    assert set(kw) == {"k_scale", "v_scale", "sm_k", "sm_v", "kv_bits", "ring_k", "ring_v", "ring_ks", "ring_vs",
+                       "owner", "ring_mask"}
+    assert kw["ring_mask"] == 63 and kw["owner"] is tiered.ring_owner and kw["k_scale"] is tiered.k_scale_buffer[1]
+    assert kw["ring_ks"] is tiered.ring_ks[1]
+    for fn in (sa.qwen_sparse_kv_extraction_compact_triton, sa.sparse_gqa_fwd_interface_paged):
+        params = inspect.signature(fn).parameters
+        assert set(kw) <= set(params), (fn.__name__, set(kw) - set(params))
+    tier_only = glue._kv_tier_kwargs(lay)
+    assert set(tier_only) <= set(inspect.signature(sa.qwen_sparse_prefix_gather_dequant_tiered).parameters)
+    # single-tier pools: no ring arguments; an unquantized stand-in gets none at all
+    p4 = MHATokenToKVPoolInt4(dtype=torch.uint8, **mk)
+    g4 = KVDispatch(p4)
+    assert g4._kv_tier_kwargs(SimpleNamespace(layer_id=0)) == {}
+    assert set(g4._int8_gather_kwargs(p4.k_buffer[0], SimpleNamespace(layer_id=0))) == {
+        "k_scale", "v_scale", "sm_k", "sm_v", "kv_bits"}
+    p8 = MHATokenToKVPoolInt8(dtype=torch.int8, **mk)
+    g8 = KVDispatch(p8)
+    assert g8._kv_bits() == 8 and g8._kv_head_dim(p8.k_buffer[0]) == 256
+    kw8 = g8._int8_gather_kwargs(p8.k_buffer[0], SimpleNamespace(layer_id=2))
+    assert kw8["kv_bits"] == 8 and kw8["sm_k"].data_ptr() == p8.sm_k[2].data_ptr()
+    plain = SimpleNamespace(kv_bits=None)
+    gp = KVDispatch(plain)
+    bf = torch.zeros(4, 2, 256, dtype=torch.bfloat16)
+    assert gp._int8_gather_kwargs(bf, lay) == {} and gp._kv_scratch_dtype(bf) == torch.bfloat16
+    assert gp._kv_scratch_dtype(torch.zeros(4, 2, 256, dtype=torch.float16)) == torch.float16

@@ -158,3 +158,16 @@ def test_sparse_decode_invalid_columns_inside_the_count(kvt_pkg):
     q = (torch.randn(2, HQ, D, generator=gen) / 4).to(torch.bfloat16)
     got = _call("tiered", p, q, r2t, req_idx, idx, sl, cu_k, 2, 96, R).cpu()
     _close(got, _oracle("tiered", p, q, r2t, req_idx, idx, sl, cu_k, 96, R, 64, skip_invalid=True))
+
+
+def test_sparse_decode_gqa12(kvt_pkg):
+    """24 q heads over 2 KV heads (GQA 12, the served model's shape, tools/probe_trtllm_sm120.py:4): the 16-row
+    accumulator tile holds 12 heads and the block merges them in two passes of 8."""
+    gen = torch.Generator().manual_seed(34)
+    slots, R = 4096, 64
+    p = _pools(slots, R, 64, gen)
+    r2t, req_idx, idx, sl, cu_k = _case(gen, [3000, 700, 9], 2051, slots)
+    q = (torch.randn(3, 24, D, generator=gen) / 4).to(torch.bfloat16)
+    for kind in ("tiered", "int8"):
+        got = _call(kind, p, q, r2t, req_idx, idx, sl, cu_k, 3, 2051, R).cpu()
+        _close(got, _oracle(kind, p, q, r2t, req_idx, idx, sl, cu_k, 2051, R, 64))

@@ -302,3 +302,154 @@ def test_prefill_selection_rule():
     assert pos.tolist() == [3, 0, 7, 5]          # first min(topk, visible) = 5 entries, -1 dropped, < kv_len
     pos = ref.prefill_selected_positions(idx, visible=9, kv_len=8, topk=7)
     assert pos.tolist() == [3, 0, 7, 5, 2]       # 9 >= kv_len dropped
+    pos = ref.prefill_selected_positions(idx, visible=9, kv_len=8, topk=3)
+    assert pos.tolist() == [3, 0, 7]             # only the first topk entries
+    for visible in (0, -5):                      # kv_len < q_len: the early queries see nothing
+        assert ref.prefill_selected_positions(idx, visible=visible, kv_len=8, topk=7).numel() == 0
+
+
+# ---------------------------------------------------------------------------------------------- gathers' building blocks
+def test_cu_seqlens_valid_brute_force():
+    """cu_k = prefix sum of the per-request counts of columns c < topk with 0 <= indices[b][c] < seq_lens[b], counted
+    element by element (indices with -1 padding, entries >= seq_len and columns past topk that must not count)."""
+    gen = torch.Generator().manual_seed(11)
+    for batch, topk, width in ((1, 5, 5), (4, 37, 40), (7, 200, 260)):
+        seq = torch.randint(0, 300, (batch,), generator=gen).to(torch.int32)
+        idx = torch.randint(-2, 330, (batch, width), generator=gen).to(torch.int32)
+        idx[0, : min(3, width)] = -1
+        cu = ref.cu_seqlens_valid(seq, idx, topk)
+        want = [0]
+        for b in range(batch):
+            n = 0
+            for c in range(topk):
+                v = int(idx[b, c])
+                if 0 <= v < int(seq[b]):
+                    n += 1
+            want.append(want[-1] + n)
+        assert cu.dtype == torch.int32 and cu.tolist() == want
+
+
+def test_dequant_slots_tiered_scalar_loop():
+    """Tiered rows of given slots against a per-slot scalar loop (tests/golden/scalar_model.py): the ring row
+    r = slot & mask when owner[r] == slot, else the INT4 row; unowned ring rows are poisoned (NaN / inf scales,
+    0x77 codes) and a stale owner (another slot of the class) must send its slot to INT4
+    (gemv/test_kv_tiers.py:259-262, :320, :370-378)."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import scalar_model as sm
+    gen = torch.Generator().manual_seed(12)
+    H, D, R, slots = 2, 256, 16, 256
+    k4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, generator=gen)
+    v4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, generator=gen)
+    ks4 = (0.05 + torch.rand(slots, H, D // 32, generator=gen)).half()
+    vs4 = (0.05 + torch.rand(slots, H, D // 32, generator=gen)).half()
+    rk = torch.full((R, H, D), 0x77, dtype=torch.int8)
+    rv = torch.full((R, H, D), 0x77, dtype=torch.int8)
+    rks = torch.full((R, H, D // 64), float("nan"), dtype=torch.float16)
+    rvs = torch.full((R, H, D // 64), float("inf"), dtype=torch.float16)
+    owner = torch.full((R,), -1, dtype=torch.int32)
+    owned = [0, 3, 5, 6, 9, 12, 15]
+    for r in owned:
+        owner[r] = r + R * int(torch.randint(0, slots // R, (1,), generator=gen))
+        rk[r] = torch.randint(-127, 128, (H, D), dtype=torch.int8, generator=gen)
+        rv[r] = torch.randint(-127, 128, (H, D), dtype=torch.int8, generator=gen)
+        rks[r] = (0.001 + 0.01 * torch.rand(H, D // 64, generator=gen)).half()
+        rvs[r] = (0.001 + 0.01 * torch.rand(H, D // 64, generator=gen)).half()
+    smk = (0.5 + torch.rand(H, D, generator=gen)).half()
+    smv = (0.5 + torch.rand(H, D, generator=gen)).half()
+    # every owner slot, its stale neighbours of the same class, and random slots
+    query = [int(owner[r]) for r in owned] + [int(owner[r]) + R for r in owned if int(owner[r]) + R < slots]
+    query += torch.randint(0, slots, (40,), generator=gen).tolist()
+    sl = torch.tensor(query)
+    dk, dv = ref.dequant_slots_tiered(sl, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, R - 1, smk, smv)
+    assert torch.isfinite(dk.float()).all() and torch.isfinite(dv.float()).all()
+    n_hot = 0
+    for i, s_ in enumerate(query):
+        r = s_ & (R - 1)
+        hot = int(owner[r]) == s_
+        n_hot += hot
+        for h in range(H):
+            for got, cod8, sc8, cod4, sc4, smf in ((dk, rk, rks, k4, ks4, smk), (dv, rv, rvs, v4, vs4, smv)):
+                if hot:
+                    codes, scales, g = cod8[r, h].tolist(), sc8[r, h].float().tolist(), 64
+                else:
+                    codes, scales, g = sm.unpack_row(cod4[s_, h].tolist()), sc4[s_, h].float().tolist(), 32
+                want = sm.dequant_row_bits(codes, scales, g, smf[h].float().tolist())
+                assert got[i, h].view(torch.int16).tolist() == [w - 65536 if w >= 32768 else w for w in want]
+    assert 0 < n_hot < len(query)
+
+
+def test_quant_store_int4_scatter():
+    """quant_store_int4 writes quant4(k) / quant4(v) at the given slots of the K and V tensors and nothing else."""
+    gen = torch.Generator().manual_seed(13)
+    H, D, slots = 2, 256, 64
+    k = (torch.randn(10, H, D, generator=gen) * 3).to(torch.bfloat16)
+    v = (torch.randn(10, H, D, generator=gen) * 3).to(torch.bfloat16)
+    loc = torch.randperm(slots, generator=gen)[:10]
+    kb = torch.full((slots, H, D // 2), 0x55, dtype=torch.uint8)
+    vb = torch.full((slots, H, D // 2), 0x66, dtype=torch.uint8)
+    ksb = torch.full((slots, H, 8), 3.0, dtype=torch.float16)
+    vsb = torch.full((slots, H, 8), 5.0, dtype=torch.float16)
+    ref.quant_store_int4(k, v, loc, kb, vb, ksb, vsb, None, None)
+    pk, sk = ref.quant4(k)
+    pv, sv = ref.quant4(v)
+    assert torch.equal(kb[loc], pk) and torch.equal(ksb[loc], sk) and torch.equal(vb[loc], pv) and torch.equal(vsb[loc], sv)
+    rest = torch.ones(slots, dtype=torch.bool)
+    rest[loc] = False
+    assert (kb[rest] == 0x55).all() and (vb[rest] == 0x66).all() and (ksb[rest] == 3).all() and (vsb[rest] == 5).all()
+
+
+def test_evict_closed_form_matches_token_model():
+    """The closed form of the evict-mode state (all tokens at once) equals the token-by-token model
+    (PosTieredCache.append), for a ring of 64 over 500 positions and for a sequence that starts at a shared
+    prefix (ring_start 128) with group 256."""
+    gen = torch.Generator().manual_seed(14)
+    H, D = 2, 256
+    for R, start, n, g8 in ((64, 0, 500, 64), (128, 128, 300, 256), (64, 0, 40, 64)):
+        xk = (torch.randn(n, H, D, generator=gen) * 2).to(torch.bfloat16)
+        xv = (torch.randn(n, H, D, generator=gen) * 2).to(torch.bfloat16)
+        c = ref.PosTieredCache(H, D, n_pages=16, ring_total=R, group8=g8)
+        alloc = ref.PageAllocator(16, seed=3)
+        shared = [alloc.pop() for _ in range(start // 64)]
+        s = c.add_seq(0, R, start, shared)
+        for a in range(0, n, 37):
+            m = min(37, n - a)
+            c.plan_pages(s, m, alloc)
+            c.append(s, xk[a:a + m], xv[a:a + m])
+        f = ref.evict_closed_form(xk, xv, R, start, g8)
+        st = c.seqs[s]
+        assert f["hot_start"] == st.hot_start
+        assert torch.equal(c.rk[f["ring_rows"]], f["rk"]) and torch.equal(c.rks[f["ring_rows"]], f["rks"])
+        assert torch.equal(c.rv[f["ring_rows"]], f["rv"]) and torch.equal(c.rvs[f["ring_rows"]], f["rvs"])
+        cold = torch.arange(start, st.hot_start)
+        pt = torch.tensor(st.pages, dtype=torch.long)
+        rows = pt[cold // 64] * 64 + cold % 64 if cold.numel() else cold
+        assert torch.equal(c.k4[rows], f["k4"]) and torch.equal(c.ks4[rows], f["ks4"])
+        assert torch.equal(c.v4[rows], f["v4"]) and torch.equal(c.vs4[rows], f["vs4"])
+
+
+def test_page_allocator_is_the_seeded_permutation():
+    """The oracle's allocator hands out torch.randperm(n, seed) in order, each page once, then refuses."""
+    a = ref.PageAllocator(50, seed=7)
+    got = [a.pop() for _ in range(50)]
+    assert got == torch.randperm(50, generator=torch.Generator().manual_seed(7)).tolist() and sorted(got) == list(range(50))
+    with pytest.raises(RuntimeError):
+        a.pop()
+
+
+def test_synthetic_inputs():
+    """make_kv: V ~ N(0, 1), K ~ N(0, 1) with the 8 outlier channels of each head scaled x8 (distinct channels per
+    head from outlier_channels); make_q: N(0, 1) / 16; all bf16."""
+    gen = torch.Generator().manual_seed(15)
+    och = ref.outlier_channels(2, 256, 8, gen)
+    assert och.shape == (2, 8) and all(len(set(r.tolist())) == 8 for r in och)
+    k, v = ref.make_kv(20000, 2, 256, gen, och)
+    assert k.dtype == v.dtype == torch.bfloat16
+    std_k = k.float().std(0)
+    for h in range(2):
+        mask = torch.zeros(256, dtype=torch.bool)
+        mask[och[h]] = True
+        assert float((std_k[h, mask] - 8).abs().max()) < 0.3 and float((std_k[h, ~mask] - 1).abs().max()) < 0.05
+    assert abs(float(v.float().std()) - 1) < 0.01 and abs(float(v.float().mean())) < 0.01
+    q = ref.make_q(16, 256, gen, n=500)
+    assert q.shape == (500, 16, 256) and abs(float(q.float().std()) - 1 / 16) < 0.002
