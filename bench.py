@@ -32,7 +32,37 @@ PAGE = 64
 PEAK_HBM = 8.0e12
 
 
+def _headline_streams(layer: int, seed: int = 0):
+    """The seeded input stream of one layer of the headline cache: a device generator (seed * 1000 + layer) and the
+    x8 multiplier of the layer's 8 outlier K channels per head (drawn on the CPU from the same seed)."""
+    g = torch.Generator(device="cuda").manual_seed(seed * 1000 + layer)
+    gc = torch.Generator().manual_seed(seed * 1000 + layer)
+    ch = torch.stack([torch.randperm(D, generator=gc)[:8] for _ in range(H)])
+    mul = torch.ones(H, D)
+    for h in range(H):
+        mul[h, ch[h]] = 8.0
+    return g, mul.to("cuda")
+
+
+def _headline_chunk(g, mul):
+    """The next RING tokens of a layer's stream: K ~ N(0, 1) with the outlier channels x8, V ~ N(0, 1), bf16."""
+    k = (torch.randn(RING, H, D, device="cuda", generator=g) * mul).to(torch.bfloat16)
+    v = torch.randn(RING, H, D, device="cuda", generator=g).to(torch.bfloat16)
+    return k, v
+
+
+def headline_inputs(layer: int, seed: int = 0):
+    """All CTX tokens of one layer's K and V exactly as build_cache appended them (the same draws in the same
+    order), on the device."""
+    g, mul = _headline_streams(layer, seed)
+    parts = [_headline_chunk(g, mul) for _ in range(0, CTX, RING)]
+    return torch.cat([k for k, _ in parts]), torch.cat([v for _, v in parts])
+
+
 def build_cache(seed: int = 0):
+    """The headline cache: CTX positions x LAYERS layers appended through the write path in RING-token chunks (the
+    oldest ring rows requantized into INT4 pages once the ring is full), pages from a permutation seeded with
+    `seed`; and one seeded query per layer (N(0, 1) / 16, bf16)."""
     import kvtier  # noqa: F401
     from kvtier.kvt import PosTieredCache
     n_cold = CTX - RING
@@ -40,22 +70,11 @@ def build_cache(seed: int = 0):
     cache = PosTieredCache(LAYERS, H, D, n_pages=n_pages, ring_total=RING, max_seqs=1, max_pages=n_pages + 1,
                            device="cuda", page_seed=seed)
     cache.add_seq(RING)
-    gens = []
-    outl = []
-    for layer in range(LAYERS):
-        g = torch.Generator(device="cuda").manual_seed(seed * 1000 + layer)
-        gens.append(g)
-        gc = torch.Generator().manual_seed(seed * 1000 + layer)
-        ch = torch.stack([torch.randperm(D, generator=gc)[:8] for _ in range(H)])
-        mul = torch.ones(H, D)
-        for h in range(H):
-            mul[h, ch[h]] = 8.0
-        outl.append(mul.to("cuda"))
+    streams = [_headline_streams(layer, seed) for layer in range(LAYERS)]
     for a in range(0, CTX, RING):
         plan = cache.plan_append([0], [RING])
         for layer in range(LAYERS):
-            k = (torch.randn(RING, H, D, device="cuda", generator=gens[layer]) * outl[layer]).to(torch.bfloat16)
-            v = torch.randn(RING, H, D, device="cuda", generator=gens[layer]).to(torch.bfloat16)
+            k, v = _headline_chunk(*streams[layer])
             cache.append(layer, plan, k, v)
         cache.commit(plan)
     torch.cuda.synchronize()
@@ -78,12 +97,12 @@ def cpu_baseline(cache, q, layer: int = 0):
     qc = q[layer, 0].cpu()
     t0 = time.perf_counter()
     kk, vv = oc.rows(0)
-    ref.attention_rows(qc, kk, vv, D ** -0.5)
+    exp = ref.attention_rows(qc, kk, vv, D ** -0.5)
     dt = time.perf_counter() - t0
     nbytes = cache.kv_bytes()
     return dict(value=round(nbytes / dt / 1e9, 3), unit="GB/s", cores=torch.get_num_threads(), kind="port",
                 sample=f"oracle/ref.py dequant + fp32 attention of 1 of {LAYERS} layers at {CTX} tokens "
-                       f"({nbytes} KV bytes, {dt:.2f} s)")
+                       f"({nbytes} KV bytes, {dt:.2f} s)"), exp
 
 
 def _cpu_threads() -> int:
@@ -810,7 +829,17 @@ def main():
             t = json.load(f)
         if t.get("impl") == args.impl:
             traffic = t.get("hbm_bytes_per_launch")
-    cpu = None if args.no_cpu_baseline else cpu_baseline(cache, q)
+    cpu = parity = None
+    if not args.no_cpu_baseline:
+        # the CPU leg's oracle output doubles as a correctness check of the timed path at its own shape: layer 0's
+        # output of the last graph replay against the oracle's fp32 attention over the cache's rows
+        cpu, exp = cpu_baseline(cache, q)
+        err = (outs[0][0].cpu() - exp).abs()
+        parity = {"layer": 0, "max_abs": float(err.max()), "mean_abs": float(err.mean()),
+                  "tolerance": [2e-3, 1e-3], "ok": bool(float(err.max()) <= 2e-3 and float(err.mean()) <= 1e-3)}
+        if not parity["ok"]:
+            print(f"bench.py: the measured decode differs from the oracle beyond tolerance ({parity}); the line is "
+                  "invalid", file=sys.stderr)
     line = {
         "metric": "decode-attn KV GB/s and % HBM peak at 256k ctx; us/token all layers",
         "value": round(value, 2),
@@ -846,8 +875,13 @@ def main():
             "combine_avg_us": round(comb_avg_us, 2),
         },
         "cpu_baseline": cpu,
+        "parity": parity,
     }
+    if parity is not None and not parity["ok"]:
+        line["invalid"] = "decode output outside the oracle tolerance"
     print(json.dumps(line))
+    if parity is not None and not parity["ok"]:
+        sys.exit(1)
 
 
 if __name__ == "__main__":

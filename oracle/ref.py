@@ -40,7 +40,7 @@ def _scaled(x: torch.Tensor, sm_inv: Optional[torch.Tensor]) -> torch.Tensor:
     xf = x.float()
     if sm_inv is not None:
         xf = xf * sm_inv.float()
-    return xf
+    return xf if xf.is_contiguous() else xf.contiguous()
 
 
 def quant_groups(x: torch.Tensor, group: int, qmax: float, sm_inv: Optional[torch.Tensor] = None):
@@ -51,11 +51,19 @@ def quant_groups(x: torch.Tensor, group: int, qmax: float, sm_inv: Optional[torc
     gemv/test_kv_tiers.py:65-83).  Returns (q float tensor shaped like x, s fp16 [..., D // group]).
     """
     xf = _scaled(x, sm_inv)
-    xg = xf.reshape(*xf.shape[:-1], xf.shape[-1] // group, group)
+    if xf.data_ptr() == x.data_ptr():      # an fp32 input: work on a copy (the steps below are in place)
+        xf = xf.clone()
+    return _quant_fp32_inplace(xf, group, qmax)
+
+
+def _quant_fp32_inplace(xf: torch.Tensor, group: int, qmax: float):
+    """quant_groups' arithmetic on a contiguous fp32 tensor that it may overwrite with the codes."""
+    xg = xf.view(*xf.shape[:-1], xf.shape[-1] // group, group)
     a = xg.abs().amax(-1)
-    s = torch.where(a > 0, a / qmax, torch.ones_like(a)).clamp(max=FP16_MAX).half()
-    q = torch.clamp(torch.round(xg / s.float()[..., None]), -qmax, qmax)
-    return q.reshape(xf.shape), s
+    s = torch.where(a > 0, a / qmax, torch.ones_like(a)).clamp_(max=FP16_MAX).half()
+    # q = clamp(rne(x / f32(s)), -qmax, qmax): the same IEEE division, rounding and clamp, in place over x's copy
+    xg.div_(s.float()[..., None]).round_().clamp_(-qmax, qmax)
+    return xf, s
 
 
 def quant8(x: torch.Tensor, group: int = G8, sm_inv: Optional[torch.Tensor] = None):
@@ -105,8 +113,10 @@ def dequant4(p: torch.Tensor, s: torch.Tensor, sm: Optional[torch.Tensor] = None
 def requant8to4(q8: torch.Tensor, s8: torch.Tensor, group8: int = G8):
     """Ring-eviction requantization: x = f32(q8) * f32(s8) (exact in fp32), then INT4-G32 with fresh 32-channel
     scales (docs/KV_TIERS_PLAN.md:53, torch reference at :82; "do NOT reuse s8*127/7")."""
-    x = q8.float() * s8.float().repeat_interleave(group8, dim=-1)
-    return quant4(x)
+    D = q8.shape[-1]
+    x = (q8.float().view(*q8.shape[:-1], D // group8, group8) * s8.float()[..., None]).view(q8.shape)
+    q, s = _quant_fp32_inplace(x, G4, 7.0)
+    return pack4(q), s
 
 
 # ----------------------------------------------------------------------------------------------- dual-write (slot ring)
