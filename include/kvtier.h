@@ -201,6 +201,24 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
                        int64_t chunk, const void* seq_lens, const void* split_counts, void* out_f32, void* out_bf16,
                        int64_t out_stride_b, void* stream);
 
+/* kvt_decode_mfma followed by kvt_decode_combine(n_chunks = n_splits, chunk = 0, split_counts), with the split
+ * partials in a scratch array that the library holds on each GPU (8 MiB, a file-scope device array kept until the
+ * process ends) instead of caller-provided part_o / part_ml: the entry point allocates nothing.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The partials need batch * H * n_splits * (Hq / H) * (D + 2) * 4 bytes
+ * (the o part rounded up to 256 bytes); more than 8 MiB returns KVT_ERANGE before anything is launched (the
+ * 262,144-position headline at 128 splits per KV head needs 2.0 MiB).  split_map and split_counts (int32 [batch],
+ * the splits of each sequence) go together, as for the pair of calls this replaces; out_f32 and / or out_bf16 as
+ * kvt_decode_combine.  Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent
+ * streams, other threads) race and must be serialized by the caller. */
+int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
+                            int group8, const void* k4, const void* v4, const void* ks4, const void* vs4,
+                            const void* rk, const void* rv, const void* rks, const void* rvs, const void* ring_base,
+                            const void* ring_len, const void* ring_start, const void* page_table, int64_t pt_stride,
+                            int64_t pool_rows, float scale, int n_splits, const void* split_map, int n_map,
+                            const void* split_counts, int flags, void* out_f32, void* out_bf16, int64_t out_stride_b,
+                            void* stream);
+
 /* Causal prefill attention of a chunk of queries over the position-indexed tiered cache on the matrix cores
  * (v_mfma_f32_16x16x32_f16, K/V tiles dequantized once per 16 queries into LDS).  Sequence b's queries are rows
  * cu_q[b] .. cu_q[b+1] of q (bf16 [total_q, Hq, D], strides sq_n / sq_h) at positions kv_lens[b] - q_len .. ;

@@ -39,8 +39,17 @@
 // position returns exactly code * scale.
 
 #include "kvt_common.h"
+#include "kvtier.h"
+
+#include <mutex>
 
 using namespace kvt;
+
+// Split partials of kvt_decode_mfma_noalloc: a file-scope device array (each GPU the library runs on holds its own
+// copy until the process ends).  Host code never uses this name as an address: scratch_base() resolves the device
+// address per GPU with hipGetSymbolAddress.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -1188,6 +1197,48 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
   }
   KVT_CHECK_LAUNCH();
   return KVT_OK;
+}
+
+// Device address of `scratch` on the current device: resolved once per device (hipGetSymbolAddress with that device
+// current), then kept.  Returns KVT_OK or KVT_EHIP.
+static int scratch_base(float** base) {
+  static std::mutex mu;
+  static float* addr[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return KVT_EHIP;
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return KVT_EHIP;
+    addr[dev] = static_cast<float*>(p);
+  }
+  *base = addr[dev];
+  return KVT_OK;
+}
+
+int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
+                            int group8, const void* k4, const void* v4, const void* ks4, const void* vs4,
+                            const void* rk, const void* rv, const void* rks, const void* rvs, const void* ring_base,
+                            const void* ring_len, const void* ring_start, const void* page_table, int64_t pt_stride,
+                            int64_t pool_rows, float scale, int n_splits, const void* split_map, int n_map,
+                            const void* split_counts, int flags, void* out_f32, void* out_bf16, int64_t out_stride_b,
+                            void* stream) {
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || n_splits <= 0) return KVT_EINVAL;
+  if (out_f32 == nullptr && out_bf16 == nullptr) return KVT_EINVAL;
+  if ((split_map == nullptr) != (split_counts == nullptr)) return KVT_EINVAL;
+  // partials: o fp32 [batch H n_splits][Hq / H][D], then (m, l) [..][Hq / H][2] at a 256-byte boundary
+  const int64_t rows = (int64_t)batch * H * n_splits * (Hq / H);
+  const int64_t o_floats = (rows * kD + 63) & ~(int64_t)63;
+  if ((o_floats + rows * 2) * (int64_t)sizeof(float) > (int64_t)kScratchBytes) return KVT_ERANGE;
+  float* base = nullptr;
+  const int st = scratch_base(&base);
+  if (st != KVT_OK) return st;
+  const int s1 = kvt_decode_mfma(q, q_stride_b, seq_lens, batch, H, Hq, D, group8, k4, v4, ks4, vs4, rk, rv, rks, rvs,
+                                 ring_base, ring_len, ring_start, page_table, pt_stride, pool_rows, scale, n_splits,
+                                 split_map, n_map, base, base + o_floats, flags, nullptr, nullptr, nullptr, 0, stream);
+  if (s1 != KVT_OK) return s1;
+  return kvt_decode_combine(base, base + o_floats, batch, H, Hq, D, n_splits, 0, seq_lens, split_counts, out_f32,
+                            out_bf16, out_stride_b, stream);
 }
 
 }  // extern "C"

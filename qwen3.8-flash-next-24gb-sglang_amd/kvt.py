@@ -354,6 +354,47 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     return out
 
 
+def kvt_decode_attn_noalloc(cache: PosTieredCache, layer: int, q: torch.Tensor, out: torch.Tensor,
+                            splits: Optional[int] = None, split_map: Optional[torch.Tensor] = None,
+                            split_counts: Optional[torch.Tensor] = None, deterministic: bool = False) -> torch.Tensor:
+    """kvt_decode_attn(impl="mfma") through the library's no-allocation entry point: the split partials live in the
+    library's per-GPU scratch array, the caller passes q, out and (for ragged batches) the split map and per-sequence
+    split counts it prepared beforehand; nothing is allocated by the call.  Calls on one GPU must not overlap (they
+    share the scratch).  A workload whose partials exceed the scratch raises ValueError before any launch."""
+    S = cache.n_seqs
+    H, D = cache.H, cache.D
+    assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == D and q.dtype == torch.bfloat16
+    assert q.stride(2) == 1 and q.stride(1) == D
+    Hq = q.shape[1]
+    assert out.shape == (S, Hq, D) and out.is_contiguous() and out.dtype in (torch.float32, torch.bfloat16)
+    assert (split_map is None) == (split_counts is None), "split_map and split_counts go together"
+    if split_map is not None:
+        n_map = split_map.numel() // 3
+        n_chunks = int(splits) if splits is not None else n_map
+        assert split_counts.dtype == torch.int32 and split_counts.numel() >= S
+    else:
+        n_map = 0
+        n_chunks = splits if splits is not None else _choose_splits_mfma(max(cache.h_len) if S else 0, S * H)
+    _lib.require_device(q, out)
+    rows = S * H * n_chunks * (Hq // H)
+    need = ((rows * D + 63) // 64 * 64 + rows * 2) * 4
+    status = _lib.lib().kvt_decode_mfma_noalloc(
+        q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8, cache.k4[layer].data_ptr(),
+        cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(), cache.vs4[layer].data_ptr(),
+        cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(), cache.rks[layer].data_ptr(),
+        cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(), cache.ring_len.data_ptr(),
+        cache.ring_start.data_ptr(), cache.page_table.data_ptr(), cache.page_table.stride(0),
+        cache.k4[layer].shape[0], 1.0 / math.sqrt(D), n_chunks, _lib.ptr(split_map), n_map, _lib.ptr(split_counts),
+        0 if deterministic else 1, out.data_ptr() if out.dtype == torch.float32 else None,
+        out.data_ptr() if out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
+    if status == _lib.KVT_ERANGE:
+        raise ValueError(f"kvt_decode_mfma_noalloc: the split partials need {need} bytes, more than the library's "
+                         f"{8 << 20}-byte scratch (fewer splits or a smaller batch)")
+    if status != _lib.KVT_OK:
+        raise RuntimeError(f"kvt_decode_mfma_noalloc: status {status}")
+    return out
+
+
 def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, ring_mask,
                       sm_k=None, sm_v=None, out_dtype=torch.float32, chunk: Optional[int] = None,
                       max_len: Optional[int] = None) -> torch.Tensor:
