@@ -177,12 +177,13 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
  * aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 <
  * 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the compact gather + FA2 pair (flat patch
  * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode.
- * counters non-NULL (int32 [batch * H * 4], zero before the first call; every call leaves them zero): the kernel
- * also merges its partials into out_f32 and/or out_bf16 ([batch, Hq, D], batch stride out_stride_b elements), so no
- * kvt_decode_combine is needed.  Every block writes its partial (the slot of its split) and counts itself; the last
- * min(16, splits, CUs / 2) arrivals of a (sequence, KV head) wait until every partial is written (each waits for
- * blocks that have arrived or can still run on the CUs no waiter holds) and merge (q head, 32-dim) slices over all
- * partials.  The summation order follows the arrival order.  Calls sharing counters must not run concurrently. */
+ * counters non-NULL (int32 [batch * H * 4], zero before the first call; every call leaves them zero): the launch
+ * also merges the partials into out_f32 and/or out_bf16 ([batch, Hq, D], batch stride out_stride_b elements), so no
+ * kvt_decode_combine is needed: after the work blocks the grid holds 8 fixup blocks per (sequence, KV head); a work
+ * block writes its partial with device-coherent stores and counts itself, a fixup block waits (bounded poll) for its
+ * item's count and merges 1/8 of the item's output over all partials in a fixed order (deterministic with the fixed
+ * tile order).  Fixup blocks start only on CUs that work blocks have left (every work block is dispatched first).
+ * Calls sharing counters must not run concurrently. */
 #define KVT_DECODE_DYNAMIC 1
 int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,

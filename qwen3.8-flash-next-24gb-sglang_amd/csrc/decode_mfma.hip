@@ -158,9 +158,13 @@ struct MergeArea {
   float o[kWaves][kMergePitch];
 };
 
-// A merging block's per-wavefront weights of one chunk of 128 partials (in-kernel merge).
-struct MergeWeights {
-  float w[kWaves][128];
+// A fixup block's per-wavefront merge of 64 output float4s (in-kernel merge of the splits).
+struct FixArea {
+  float m[kWaves][64];
+  float l[kWaves][64];
+  float o[kWaves][64][4];
+  int ok;
+  int n_b;
 };
 
 // Block-wide data: the group's q heads (copied once; rows beyond the group read as zero) and the work handed out
@@ -176,7 +180,7 @@ struct Lds {
   union {
     WaveArea w[kWaves];
     MergeArea merge;
-    MergeWeights mw;
+    FixArea fix;
   };
   BlockQueue q;
 };
@@ -867,16 +871,19 @@ KVT_DEV void hot_block(const HotCtx& C, WaveArea& W, int32_t* next, bool dyn, in
   }
 }
 
-// ---- split merge inside the kernel (optional; counters != nullptr).  Every block writes its partial (the slot of
-// its split, as for the combine kernel), counts itself flushed and takes an arrival ticket per (sequence, KV head).
-// The last K arrivals (K = min(kmerge, n_b), kmerge <= kMergers and at most half the CUs) wait until all n_b
-// partials are flushed -- fewer than half the CUs wait, each for blocks that have arrived or can still be
-// dispatched onto the other CUs -- and merge the output in slices of (q head, 32 dims) over all partials, one
-// slice per wavefront: reading the partials is spread over K CUs.  The last merger to finish resets the counters.
-constexpr int kMergers = 16;
+// ---- split merge inside the kernel (counters != nullptr): fixup blocks.  The grid holds, after every work block in
+// dispatch order, kFixPerItem fixup blocks per (sequence, KV head).  A work block writes its partial (the slot of its
+// split, as for the combine kernel) and counts itself on its (sequence, KV head) counter.  Fixup blocks start on the
+// CUs that work blocks leave (a work block takes a whole CU's LDS, so they start as the first work blocks finish and
+// never hold a CU a work block still needs: all work blocks were dispatched first), wait until their item's count
+// reaches its split count (a bounded poll), and each merges one slice of the output -- 1 / kFixPerItem of the item's
+// q heads x 256 dims -- over all partials in a fixed order, so the result does not depend on the arrival order.  The
+// last fixup block of an item resets its counters for the next call.
+constexpr int kFixPerItem = 8;       // fixup blocks per (sequence, KV head)
 constexpr int kSc1 = 16;             // cache-policy operand of the raw buffer builtins: sc1 (device-coherent)
-constexpr int kSpinLimit = 1 << 22;  // polls of a waiting merger (each ~1 us)
-constexpr int kCounterStride = 4;    // counter words per (sequence, KV head): arrivals, flushed, mergers done, -
+constexpr int kSpinLimit = 1 << 20;  // polls of a waiting fixup block (each ~1 us)
+constexpr int kCounterStride = 4;    // counter words per (sequence, KV head): partials written, fixups done, -, -
+constexpr int kFixLoads = 16;        // partials a lane has in flight at once
 
 KVT_DEV __amdgpu_buffer_rsrc_t rsrc_dev(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -894,66 +901,93 @@ KVT_DEV int add_dev_i32(int32_t* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-KVT_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-// One wavefront merges q head hh, dims d0 .. d0 + 31, over the n partial slots sbase .. sbase + n - 1, in chunks of
-// 128 partials (online rescaling between chunks).  In a chunk, lanes l and l + 64 hold (m, l) of parts l and
-// l + 64; lane l reads dims d0 + 4 (l & 7) .. + 3 of parts 8 k + (l >> 3), k < 16 -- all 18 loads in flight at once
-// -- and the 8 lane groups are summed at the end.  out[hh][d] = o / l; an empty whole gives 0 / 0 = NaN (as the
-// combine kernel).
-KVT_DEV void merge_head(const float* part_o, const float* part_ml, int64_t sbase, int n, int gs, int hh, int d0,
-                        float* wbuf, bool valid, float* out_f32, uint16_t* out_bf16, int64_t row0) {
-  const int lane = threadIdx.x & 63;
-  const uint32_t rows = (uint32_t)n * gs;
+// Fixup block `part` of item (b, h): waits for the item's n_b partials (slots sbase ..), then merges output float4s
+// [f0, f1) of its gs x 64 (float4 j = q head j / 64, dims 4 (j % 64) ..): wavefront w merges partials w, w + 8, ...
+// (kFixLoads in flight per lane), the 8 wavefronts' results merge through LDS in wavefront order.  out = o / l;
+// an empty whole gives 0 / 0 = NaN (as the combine kernel); a poll that runs out leaves NaN as well.
+KVT_DEV void fixup_block(FixArea& F, const float* part_o, const float* part_ml, int32_t* ctr, int64_t sbase, int n_b,
+                         int gs, int part, float* out_f32, uint16_t* out_bf16, int64_t row0) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) {
+    int ok = 0;
+    for (int it = 0; it < kSpinLimit; ++it) {
+      if (ld_dev_i32(&ctr[0]) >= n_b) {
+        ok = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    F.ok = ok;
+  }
+  __syncthreads();
+  const bool ok = F.ok != 0;
+  const uint32_t rows = (uint32_t)n_b * gs;
   const auto rml = rsrc_dev(part_ml + sbase * gs * 2, rows * 8u);
   const auto ro = rsrc_dev(part_o + sbase * gs * kD, rows * (uint32_t)(kD * 4));
   const uint32_t none = 0x80000000u;   // beyond the range: the load returns zeros
-  float M = -INFINITY, L = 0.f;
-  f4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < n; c0 += 128) {
-    f4 v[16];
+  const int nf4 = gs * (kD / 4);
+  const int f0 = nf4 * part / kFixPerItem, f1 = nf4 * (part + 1) / kFixPerItem;
+  for (int j0 = f0; j0 < f1; j0 += 64) {
+    const int j = j0 + lane;
+    const bool act = j < f1;
+    const int hq = act ? j / (kD / 4) : 0, d4 = act ? j % (kD / 4) : 0;
+    float M = -INFINITY, Ls = 0.f;
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = wave; c0 < n_b; c0 += kWaves * kFixLoads) {
+      v2i ml[kFixLoads];
+      f4 ov[kFixLoads];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int p = c0 + 8 * k + (lane >> 3);
-      const uint32_t off = p < n ? (uint32_t)(((p * gs + hh) * kD + d0 + 4 * (lane & 7)) * 4) : none;
-      v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(ro, off, 0, kSc1));
+      for (int k = 0; k < kFixLoads; ++k) {
+        const int c = c0 + kWaves * k;
+        const bool in = act && c < n_b;
+        ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, in ? (uint32_t)((c * gs + hq) * 8) : none, 0, kSc1);
+        ov[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           ro, in ? (uint32_t)(((c * gs + hq) * kD + 4 * d4) * 4) : none, 0, kSc1));
+      }
+#pragma unroll
+      for (int k = 0; k < kFixLoads; ++k) {
+        const int c = c0 + kWaves * k;
+        const float mc = (act && c < n_b) ? __int_as_float(ml[k].x) : -INFINITY;
+        if (mc == -INFINITY) continue;
+        const float Mn = fmaxf(M, mc);
+        const float a = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((M - Mn) * kLog2e);
+        const float wc = __builtin_amdgcn_exp2f((mc - Mn) * kLog2e);
+        o = o * a + ov[k] * wc;
+        Ls = Ls * a + __int_as_float(ml[k].y) * wc;
+        M = Mn;
+      }
     }
-    const int p0 = c0 + lane, p1 = c0 + 64 + lane;
-    const v2i a0 = __builtin_amdgcn_raw_buffer_load_b64(rml, p0 < n ? (uint32_t)((p0 * gs + hh) * 8) : none, 0, kSc1);
-    const v2i a1 = __builtin_amdgcn_raw_buffer_load_b64(rml, p1 < n ? (uint32_t)((p1 * gs + hh) * 8) : none, 0, kSc1);
-    const float m0 = p0 < n ? __int_as_float(a0.x) : -INFINITY;
-    const float m1 = p1 < n ? __int_as_float(a1.x) : -INFINITY;
-    const float Mn = fmaxf(M, group_max<64>(fmaxf(m0, m1)));
-    const float alpha = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((M - Mn) * kLog2e);
-    M = Mn;
-    const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m0 - M) * kLog2e);
-    const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m1 - M) * kLog2e);
-    L = L * alpha + wave_sum(w0 * __int_as_float(a0.y) + w1 * __int_as_float(a1.y));
-    o *= alpha;
-    wbuf[lane] = w0;
-    wbuf[64 + lane] = w1;
-    __builtin_amdgcn_wave_barrier();
+    F.m[wave][lane] = M;
+    F.l[wave][lane] = Ls;
+    *reinterpret_cast<f4*>(&F.o[wave][lane][0]) = o;
+    __syncthreads();
+    if (wave == 0 && act) {
+      float Mt = -INFINITY, Lt = 0.f;
+      f4 ot = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 16; ++k) o += wbuf[8 * k + (lane >> 3)] * v[k];
-    __builtin_amdgcn_wave_barrier();
-  }
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = F.m[w][lane];
+        if (mw == -INFINITY) continue;
+        const float Mn = fmaxf(Mt, mw);
+        const float a = Mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((Mt - Mn) * kLog2e);
+        const float wc = __builtin_amdgcn_exp2f((mw - Mn) * kLog2e);
+        ot = ot * a + *reinterpret_cast<const f4*>(&F.o[w][lane][0]) * wc;
+        Lt = Lt * a + F.l[w][lane] * wc;
+        Mt = Mn;
+      }
+      const int64_t row = row0 + (int64_t)hq * kD + 4 * d4;
 #pragma unroll
-  for (int x = 8; x < 64; x <<= 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] += __shfl_xor(o[i], x, 64);
-  }
-  if (lane < 8) {
-    const int64_t row = row0 + (int64_t)hh * kD + d0 + 4 * lane;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float r = valid ? o[i] / L : __builtin_nanf("");
-      if (out_f32 != nullptr) out_f32[row + i] = r;
-      if (out_bf16 != nullptr) out_bf16[row + i] = bf16_rne(r);
+      for (int i = 0; i < 4; ++i) {
+        const float r = ok ? ot[i] / Lt : __builtin_nanf("");
+        if (out_f32 != nullptr) out_f32[row + i] = r;
+        if (out_bf16 != nullptr) out_bf16[row + i] = bf16_rne(r);
+      }
     }
+    __syncthreads();
+  }
+  if (tid == 0 && add_dev_i32(&ctr[1], 1) == kFixPerItem - 1) {   // the item's last fixup: every count was read
+    st_dev_i32(&ctr[0], 0);
+    st_dev_i32(&ctr[1], 0);
   }
 }
 
@@ -964,11 +998,31 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
                    int gs, int flags, const uint16_t* q, int64_t q_stride_b, const int64_t* ring_base,
                    const uint8_t* k4, const uint8_t* v4, const uint16_t* ks4, const uint16_t* vs4, const int8_t* rk,
                    const int8_t* rv, const uint16_t* rks, const uint16_t* rvs, float scale, float* part_o,
-                   float* part_ml, uint32_t pool_rows, int32_t* counters, int kmerge, float* out_f32,
-                   uint16_t* out_bf16, int64_t out_stride_b) {
+                   float* part_ml, uint32_t pool_rows, int32_t* counters, float* out_f32,
+                   uint16_t* out_bf16, int64_t out_stride_b, int work_rows, int batch, int n_map) {
   // (the arguments the start-up chain needs come first: the first 16 dwords are preloaded into SGPRs)
   const PosArgs A{k4, v4, ks4, vs4, rk, rv, rks, rvs, ring_base, ring_len, ring_start, page_table, pt_stride};
   __shared__ __align__(128) Lds lds;
+  // 1-D grid: work block i = (row i / gx, split i % gx) for i < work_rows * gx, then the fixup blocks
+  const int gx = split_map != nullptr ? n_map : n_splits;
+  const int bid = (int)blockIdx.x;
+  if (bid >= work_rows * gx) {   // a fixup block (counters != nullptr): after every work block
+    const int f = bid - work_rows * gx;
+    const int item = f / kFixPerItem;
+    const int fb = item / H, fh = item - fb * H;
+    int fn = n_splits;
+    if (split_map != nullptr) {   // the sequence's split count, from any of its split map entries
+      if (threadIdx.x == 0) lds.fix.n_b = 0;
+      __syncthreads();
+      for (int i = threadIdx.x; i < n_map; i += 64 * kWaves)
+        if (split_map[3 * i] == fb) lds.fix.n_b = split_map[3 * i + 2];
+      __syncthreads();
+      fn = lds.fix.n_b;
+    }
+    fixup_block(lds.fix, part_o, part_ml, counters + (int64_t)item * kCounterStride, (int64_t)item * n_splits, fn,
+                gs, f - item * kFixPerItem, out_f32, out_bf16, (int64_t)fb * out_stride_b + (int64_t)fh * gs * kD);
+    return;
+  }
   const bool dyn = (flags & KVT_DECODE_DYNAMIC) != 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -976,15 +1030,16 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
   // split c of n_b for sequence b: uniform (grid.x = n_splits, grid.y = batch x H) or from the split map
   // (grid.x = total splits, grid.y = H; entry = {b, c, n_b})
   int b, c, h, n_b;
+  const int bx = bid % gx, by = bid / gx;
   if (split_map != nullptr) {
-    b = split_map[3 * blockIdx.x];
-    c = split_map[3 * blockIdx.x + 1];
-    n_b = split_map[3 * blockIdx.x + 2];
-    h = blockIdx.y;
+    b = split_map[3 * bx];
+    c = split_map[3 * bx + 1];
+    n_b = split_map[3 * bx + 2];
+    h = by;
   } else {
-    c = blockIdx.x;
-    b = blockIdx.y / H;
-    h = blockIdx.y - b * H;
+    c = bx;
+    b = by / H;
+    h = by - b * H;
     n_b = n_splits;
   }
   const int64_t item = ((int64_t)b * H + h) * n_splits + c;   // partial slots: n_splits per (sequence, head)
@@ -1059,9 +1114,6 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
   __syncthreads();                        // every wavefront is done with its staging area
   const int tid = threadIdx.x;
   const bool fused = counters != nullptr;
-  int32_t* ctr = fused ? counters + ((int64_t)b * H + h) * kCounterStride : nullptr;
-  int ticket_raw = 0;
-  if (fused && tid == 0) ticket_raw = add_dev_i32(&ctr[0], 1);   // arrival ticket, in flight during the merge
   if (kb == 0 && n16 < 8) {
     lds.merge.m[wave][n16] = m_run;
     lds.merge.l[wave][n16] = l_run;
@@ -1114,44 +1166,10 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
     st_dev(&part_ml[(item * gs + tid) * 2 + 1], lb);
   }
   if (!fused) return;
-  // ---- in-kernel merge of the splits (see merge_head)
-  int* lds_word = &lds.q.hot_next;                         // (the block's tile counters are no longer used)
+  // ---- count the partial for the fixup blocks (see fixup_block)
   wait_vmcnt<0>();                                         // the partial has reached the coherence point
   __syncthreads();
-  if (tid == 0) {
-    add_dev_i32(&ctr[1], 1);                               // flushed
-    *lds_word = ticket_raw;
-  }
-  __syncthreads();
-  const int ticket = *lds_word;
-  const int K = min(kmerge, n_b);
-  if (ticket < n_b - K) return;
-  // one of the last K arrivals: wait until all n_b partials are flushed
-  __syncthreads();                                         // (everyone has read the ticket word)
-  if (tid == 0) {
-    int ok = 0;
-    for (int it = 0; it < kSpinLimit; ++it) {
-      if (ld_dev_i32(&ctr[1]) >= n_b) {
-        ok = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(10);
-    }
-    *lds_word = ok;
-  }
-  __syncthreads();
-  const bool ok = *lds_word != 0;                          // (a poll limit that ran out leaves NaN in the output)
-  const int64_t sbase = ((int64_t)b * H + h) * n_splits;   // this (sequence, KV head)'s first partial slot
-  const int64_t out_row0 = (int64_t)b * out_stride_b + (int64_t)h * gs * kD;
-  for (int j = ticket - (n_b - K) + K * wave; j < gs * 8; j += K * kWaves)   // slice j: q head j / 8, dims 32 (j % 8)
-    merge_head(part_o, part_ml, sbase, n_b, gs, j >> 3, 32 * (j & 7), lds.mw.w[wave], ok, out_f32, out_bf16,
-               out_row0);
-  __syncthreads();
-  if (tid == 0 && add_dev_i32(&ctr[2], 1) == K - 1) {    // the last merger: every count has been read
-    st_dev_i32(&ctr[0], 0);
-    st_dev_i32(&ctr[1], 0);
-    st_dev_i32(&ctr[2], 0);
-  }
+  if (tid == 0) add_dev_i32(counters + ((int64_t)b * H + h) * kCounterStride, 1);
 }
 
 }  // namespace
@@ -1170,23 +1188,19 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
   const int gs = Hq / H;
   if (gs > 8 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
   if (counters != nullptr && out_f32 == nullptr && out_bf16 == nullptr) return KVT_EINVAL;
-  // mergers of the in-kernel merge: they wait for the others, so at most half the CUs may hold them
-  static int cu_count[64];   // per device, read once (a benign race: every writer stores the same value)
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return KVT_ELAUNCH;
-  if (cu_count[dev] == 0 &&
-      hipDeviceGetAttribute(&cu_count[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return KVT_ELAUNCH;
-  const int kmerge = max(1, min(kMergers, cu_count[dev] / 2));
+  // grid: the work blocks (rows 0 .. work_rows - 1), then, with counters, rows of fixup blocks
+  const unsigned gx = split_map != nullptr ? (unsigned)n_map : (unsigned)n_splits;
+  const int work_rows = split_map != nullptr ? H : batch * H;
+  const int64_t n_blocks = (int64_t)work_rows * gx + (counters == nullptr ? 0 : (int64_t)batch * H * kFixPerItem);
+  if (n_blocks > 0x7fffffff) return KVT_ERANGE;
 #define KVT_DECODE_ARGS                                                                                          \
   (const int32_t*)seq_lens, (const int32_t*)ring_len, (const int64_t*)ring_start, (const int32_t*)page_table,       \
       pt_stride, (const int32_t*)split_map, H, n_splits, gs, flags, (const uint16_t*)q, q_stride_b,                \
       (const int64_t*)ring_base, (const uint8_t*)k4, (const uint8_t*)v4, (const uint16_t*)ks4, (const uint16_t*)vs4, \
       (const int8_t*)rk, (const int8_t*)rv, (const uint16_t*)rks, (const uint16_t*)rvs, scale, (float*)part_o,     \
-      (float*)part_ml, (uint32_t)pool_rows, (int32_t*)counters, kmerge, (float*)out_f32, (uint16_t*)out_bf16,      \
-      out_stride_b
-  const dim3 grid = split_map != nullptr ? dim3((unsigned)n_map, (unsigned)H)
-                                         : dim3((unsigned)n_splits, (unsigned)(batch * H));
+      (float*)part_ml, (uint32_t)pool_rows, (int32_t*)counters, (float*)out_f32, (uint16_t*)out_bf16,             \
+      out_stride_b, work_rows, batch, n_map
+  const dim3 grid((unsigned)n_blocks);
   hipStream_t st = (hipStream_t)stream;
   if (group8 == 64) {
     hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);

@@ -257,13 +257,12 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     a fixed order and the combine kernel merges the splits.  By default tiles go first come (the block's wavefronts
     finish together, about 4 % faster at 262,144 positions) and the fp32 summation order varies in the last bits.
     tile_order ("fixed" / "dynamic", impl "mfma"): overrides the tile order alone.
-    fused_combine (impl "mfma", not deterministic): the split-K kernel merges its own partials and writes `out`
-    (every block writes its partial and counts itself; the last 16 arrivals wait for all partials and each merges
-    (q head, 32-dim) slices over all of them); otherwise kvt_decode_combine runs after it.  One launch instead of
-    two: faster when launches are not in a graph (262,144 positions: 44.6 against 46.5 us per layer), slower in a
-    graph (42.9 against 41.9 us), hence off by default.  The merged sum's order follows the arrival order, so
-    deterministic calls always use the combine kernel.  The merge counters live in the workspace and return to zero
-    after every call; concurrent calls must not share a workspace.
+    fused_combine (impl "mfma"): the split-K launch merges its own partials and writes `out`: fixup blocks queued
+    after the work blocks wait for every partial of their (sequence, KV head) and each merges 1/8 of its output in a
+    fixed order.  One launch instead of two, but the cross-XCD handshake (coherent stores, counter, poll, coherent
+    loads) costs more than the kernel boundary and the combine launch: at 262,144 positions 47.5 against 39.0 + 4.3
+    us per layer, hence off by default.  The merge counters live in the workspace and return to zero after every
+    call; concurrent calls must not share a workspace.
     """
     S = cache.n_seqs
     assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == cache.D and q.dtype == torch.bfloat16
@@ -289,7 +288,7 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         if chunk is None:
             chunk = _choose_chunk(max_len, S * H)
         n_chunks = max(1, -(-max_len // chunk))
-    fused = impl == "mfma" and fused_combine and not deterministic and n_chunks <= 1024
+    fused = impl == "mfma" and fused_combine
     n_slots = n_chunks   # partial slots per (sequence, KV head)
     need_o = S * H * n_slots * gs * D
     po = ws.get("part_o")
@@ -321,7 +320,7 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         fixed_order = (tile_order or ("fixed" if deterministic else "dynamic")) == "fixed"
         ctr = None
         if fused:
-            # 4 words per (sequence, KV head): arrivals, flushed partials, finished mergers (zero between calls)
+            # 4 words per (sequence, KV head): partials written, fixup blocks done (zero between calls)
             ctr = ws.get("merge_counters")
             if ctr is None or ctr.numel() < S * H * 4 or ctr.device != q.device:
                 ctr = torch.zeros(max(S * H * 4, 64), dtype=torch.int32, device=q.device)

@@ -88,20 +88,25 @@ def test_decode_mfma_splits(kvt_pkg, splits):
 
 @pytest.mark.parametrize("splits", [1, 2, 16, 17, 40, 200])
 def test_decode_fused_merge(kvt_pkg, splits):
-    """The in-kernel merge of the split partials (the last min(16, splits) arrivals each merging (q head, 32-dim)
-    slices over all partials) against the separate combine kernel (same math, another fp32
+    """The in-kernel merge of the split partials (fixup blocks after the work blocks, each merging 1/8 of the
+    output over all partials in a fixed order) against the separate combine kernel (same math, another fp32
     summation order: 1e-5; both with the fixed tile order) and the oracle, over several calls: after each, the merge
-    counters are back to zero; bf16 output = the fp32 result rounded (up to that order)."""
+    counters are back to zero and, with the fixed tile order, the output is bit-identical from call to call; bf16
+    output = the fp32 result rounded (up to that order)."""
     from kvtier.kvt import kvt_decode_attn
     dc, oc, q = _build([5000, 2100], [2048, 1024], seed=31)
     qd = q.to(dev)
     ws = {}
     sep = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, deterministic=True)
+    first = None
     for rep in range(3):
         fused = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, workspace=ws, tile_order="fixed",
                                 fused_combine=True)
         assert int(ws["merge_counters"].abs().sum()) == 0, rep
         assert float((fused - sep).abs().max()) < 1e-5, (splits, rep)
+        if first is None:
+            first = fused.clone()
+        assert torch.equal(fused, first), (splits, rep)
     fb = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, workspace=ws, out_dtype=torch.bfloat16,
                          tile_order="fixed", fused_combine=True)
     assert bool(((fb.float() - fused).abs() <= fused.abs() * 2.0 ** -8 + 1e-6).all())
@@ -110,9 +115,9 @@ def test_decode_fused_merge(kvt_pkg, splits):
 
 
 def test_decode_fused_merge_ragged(kvt_pkg):
-    """Ragged batch through the split map: per-sequence split counts from 1 up (fewer splits than mergers: one
-    merger per split), in the fused merge against the combine kernel and the oracle; the same workspace then serves
-    a call with another split layout."""
+    """Ragged batch through the split map: per-sequence split counts from 1 up (the fixup blocks read each
+    sequence's count from the map), in the fused merge against the combine kernel and the oracle; the same workspace
+    then serves a call with another split layout."""
     from kvtier.kvt import kvt_decode_attn
     lens = [40000, 300, 9000, 2500]
     dc, oc, q = _build(lens, [2048, 256, 1024, 1024], seed=37)
