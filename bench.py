@@ -647,8 +647,10 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     S = len(lens)
     rings = [min(RING, 1 << (max(1, L) - 1).bit_length()) for L in lens]
     shared = 4096 if ragged else 0
-    n_pages = sum(max(0, L + steps - r) // PAGE + 2 for L, r in zip(lens, rings)) + shared // PAGE
-    max_pages = max(lens) // PAGE + steps // PAGE + 4
+    n_host = min(100, steps // 4)              # host-planned eager steps, timed for reference
+    extra = args.warmup + n_host + 4           # tokens appended besides the timed steps (warm-ups, capture)
+    n_pages = sum(max(0, L + steps + extra - r) // PAGE + 2 for L, r in zip(lens, rings)) + shared // PAGE
+    max_pages = max(lens) // PAGE + (steps + extra) // PAGE + 4
     cache = PosTieredCache(layers, H, D, n_pages=n_pages, ring_total=sum(rings), max_seqs=S, max_pages=max_pages,
                            device="cuda", page_seed=5)
     # the shared prefix: 64 pages taken from the allocator and written once with the INT4 writer (positions 0..4095),
@@ -686,61 +688,89 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     knew, vnew = _layer_kv(S, 0, seed=11)
     ws = {}
     out = torch.empty(n_all, HQ, D, dtype=torch.float32, device="cuda")
-    ev = []
 
-    def step(events=None):
+    # eager steps through the host planner (plan_append: a Python loop, page pops, host-to-device copies)
+    def host_step():
         plan = cache.plan_append(seqs, [1] * S)
         for layer in range(layers):
             cache.append(layer, plan, knew, vnew)
         cache.commit(plan)
         for layer in range(layers):
-            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, events=events)
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
 
     for _ in range(args.warmup):
-        step()
+        host_step()
     torch.cuda.synchronize()
-    kv_bytes = cache.kv_bytes(seqs) * layers
     t0 = time.perf_counter()
+    for _ in range(n_host):
+        host_step()
+    torch.cuda.synchronize()
+    wall_host = (time.perf_counter() - t0) / n_host
+
+    # the timed steps: the device plan (positions, page pops, lengths on the device), every layer's append and decode
+    # captured once as one HIP graph and replayed once per step -- no host work per step
+    dplan = cache.plan_device(seqs, [1] * S)
+
+    def dev_step():
+        cache.launch_plan(dplan)
+        for layer in range(layers):
+            cache.append(layer, dplan, knew, vnew)
+        for layer in range(layers):
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
+
+    dev_step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dev_step()
+    graph.replay()
+    torch.cuda.synchronize()
+    cache.sync_host()
+    kv_first = cache.kv_bytes(seqs) * layers
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    g0.record()
     for _ in range(steps):
-        step(ev)
+        graph.replay()
+    g1.record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
-    dec_s = sum(a.elapsed_time(c) for a, _, c in ev) / 1e3 / steps
-    # the device's decode time: the final state's decode of every layer replayed as one HIP graph (the eager events
-    # above include the host's launch gaps whenever Python is slower than the kernels)
+    dev_s = g0.elapsed_time(g1) / 1e3 / steps
+    cache.sync_host()
     kv_last = cache.kv_bytes(seqs) * layers
+    kv_avg = (kv_first + kv_last) / 2
 
+    # decode alone over the final state (every layer, one graph): the device's decode rate
     def dec_only():
         for layer in range(layers):
             kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
 
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        dec_only()
-    torch.cuda.current_stream().wait_stream(side)
+    dec_only()   # (eagerly first: the split map of the final lengths)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    dgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(dgraph):
         dec_only()
-    graph.replay()
+    dgraph.replay()
     torch.cuda.synchronize()
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    g0.record()
+    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    d0.record()
     for _ in range(20):
-        graph.replay()
-    g1.record()
+        dgraph.replay()
+    d1.record()
     torch.cuda.synchronize()
-    dec_graph = g0.elapsed_time(g1) / 1e3 / 20
+    dec_graph = d0.elapsed_time(d1) / 1e3 / 20
     name = ("ragged decode: 8 sequences, 12 layers, shared 4,096-token prefix, 256 iterations" if ragged
             else "decode with append: 10,001-token context, 1 layer, 1,000 steps")
     return {
         "metric": name + ": us per step", "value": round(wall * 1e6, 1), "unit": "us", "higher_is_better": False,
         "steps": steps, "warmup": args.warmup, "dtype": "f16-mfma/f32", "data": "synthetic",
-        "config": {"workload": name, "lens": lens, "rings": rings, "impl": args.impl},
-        "decode_us_per_step": round(dec_s * 1e6, 1),
-        "decode_kv_GBps": round(kv_bytes / dec_s / 1e9, 1),
-        "kv_bytes_per_step": kv_bytes,
+        "config": {"workload": name, "lens": lens, "rings": rings, "impl": args.impl,
+                   "step": "device plan + append of every layer + decode of every layer, one HIP graph per step"},
+        "device_us_per_step": round(dev_s * 1e6, 1),
+        "wall_over_device": round(wall / dev_s, 3),
+        "host_planned_eager_us_per_step": round(wall_host * 1e6, 1),
+        "kv_GBps_per_step": round(kv_avg / dev_s / 1e9, 1),
+        "kv_bytes_per_step": int(kv_avg),
         "decode_graph_us_per_step": round(dec_graph * 1e6, 1),
         "decode_graph_kv_GBps": round(kv_last / dec_graph / 1e9, 1),
     }

@@ -69,6 +69,21 @@ int kvt_quant_store_int4(const void* k, const void* v, int dtype, int64_t sk_n, 
 int kvt_page_table_update(void* page_table, int64_t pt_stride, int64_t n, const void* seq, const void* lpage,
                           const void* ppage, void* stream);
 
+/* Device-side plan of an evicting append, so that a whole append (+ decode) step needs no host work and captures
+ * into a HIP graph.  Sequence seqs[j] (j < n, distinct, n <= 1024) appends cu[j+1] - cu[j] tokens (cu int32 [n+1],
+ * cu[0] = 0) at positions L0 .. L0 + cnt - 1, L0 = seq_lens[seqs[j]] when the plan runs.  Writes seq_ids int32 [N]
+ * and positions int64 [N] (N = cu[n]: the inputs of kvt_append_evict), gives every page that evicted positions enter
+ * for the first time (e = p - ring_len >= ring_start, e % 64 == 0) the next entry of free_list (int32 [n_pages], read
+ * from *free_head on), in call order -- sequence j before j + 1, positions ascending, the order of a host allocator
+ * walking the same plan -- writes it to page_table[s][e / 64], advances *free_head and sets seq_lens[s] = L0 + cnt.
+ * A page that cannot be given (free list exhausted: *status |= 1; logical page >= max_pages: |= 2) stays
+ * unassigned and kvt_append_evict then skips that token's requantization (no write outside the pool).  No reference
+ * counterpart: the reference's slot allocator is host code (the compactor bookkeeping of docs/KV_TIERS_PLAN.md:63-67
+ * was never built). */
+int kvt_append_plan(int n, const void* seqs, const void* cu, void* seq_lens, const void* ring_len,
+                    const void* ring_start, void* page_table, int64_t pt_stride, int max_pages, const void* free_list,
+                    int n_pages, void* free_head, void* seq_ids, void* positions, void* status, void* stream);
+
 /* Position-ring append of N tokens (seq_ids int32 [N], positions int64 [N]; per sequence ring_base int64,
  * ring_len int32 (power of two), ring_start int64): if e = p - ring_len >= ring_start, ring row
  * ring_base + (p & (ring_len - 1)) is first requantized (f32(q8) * f32(s8) -> INT4-G32) into pool row

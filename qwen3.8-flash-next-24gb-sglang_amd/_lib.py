@@ -33,6 +33,7 @@ SIGNATURES = {
     "kvt_quant_store_int8": [_P, _P, _I, _L, _L, _L, _L, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P, _I, _P],
     "kvt_quant_store_int4": [_P, _P, _I, _L, _L, _L, _L, _P, _I, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "kvt_page_table_update": [_P, _L, _L, _P, _P, _P, _P],
+    "kvt_append_plan": [_I, _P, _P, _P, _P, _P, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P],
     "kvt_append_evict": [_P, _P, _I, _L, _L, _L, _L, _P, _P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _L, _P, _P, _I, _P],
     "kvt_compact_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P, _P, _I,

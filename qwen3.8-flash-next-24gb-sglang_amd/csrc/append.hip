@@ -12,6 +12,7 @@
 //   kvt_quant_store_int8    INT8-G quant + scatter (patches/kv_int8.py:281-362, with the fp16-max clamp).
 //   kvt_quant_store_int4    INT4-G32 quant + nibble pack + scatter (patches/kv_int4.py:289-393).
 //   kvt_page_table_update   writes (seq, logical page) -> physical page entries before an evicting append.
+//   kvt_append_plan         the same plan on the device: positions, page pops from a free list, seq_lens advance.
 //   kvt_append_evict        position-indexed ring append: requantizes the ring row being overwritten into the
 //                           INT4 page of its position (docs/KV_TIERS_PLAN.md:53, :63-67), then stores the new
 //                           token's INT8 row.
@@ -388,6 +389,77 @@ __global__ void __launch_bounds__(256) append_evict_kernel(
   }
 }
 
+// Device-side plan of an evicting append (one block; see kvt_append_plan).  Sequence j of the call appends
+// cu[j + 1] - cu[j] tokens at positions L0 .. L0 + n - 1 (L0 = seq_lens[s] before the call).  Positions e that leave
+// the ring (e = p - R >= ring_start) and start a page (e % 64 == 0) take the next pages of the free list, in call
+// order (sequence j before j + 1, positions ascending): the order in which a host allocator walking the same plan
+// pops them.  Then seq_lens[s] = L0 + n.
+constexpr int kPlanThreads = 1024;
+
+__global__ void __launch_bounds__(kPlanThreads) append_plan_kernel(
+    int n, const int32_t* seqs, const int32_t* cu, int32_t* seq_lens, const int32_t* ring_len,
+    const int64_t* ring_start, int32_t* page_table, int64_t pt_stride, int max_pages, const int32_t* free_list,
+    int n_pages, int32_t* free_head, int32_t* seq_ids, int64_t* positions, int32_t* status) {
+  __shared__ int64_t s_l0[kPlanThreads];
+  __shared__ int32_t s_off[kPlanThreads + 1];
+  __shared__ int32_t s_cu[kPlanThreads + 1];
+  const int j = threadIdx.x;
+  int s = 0, np = 0;
+  int64_t L0 = 0, lp0 = 0;
+  if (j < n) {
+    s = seqs[j];
+    const int cnt = cu[j + 1] - cu[j];
+    L0 = seq_lens[s];
+    const int64_t R = ring_len[s], st = ring_start[s];
+    const int64_t e0 = max(st, L0 - R), e1 = L0 + cnt - R;
+    lp0 = (e0 + kPage - 1) >> 6;
+    if (e1 > e0) np = (int)(((e1 + kPage - 1) >> 6) - lp0);
+    s_l0[j] = L0;
+  }
+  if (j < n) s_cu[j] = cu[j];
+  if (j == 0) s_cu[n] = cu[n];
+  // exclusive scan of the new-page counts over the call's sequences (Hillis-Steele in LDS)
+  s_off[j] = np;
+  __syncthreads();
+  for (int d = 1; d < kPlanThreads; d <<= 1) {
+    const int v = j >= d ? s_off[j - d] : 0;
+    __syncthreads();
+    s_off[j] += v;
+    __syncthreads();
+  }
+  const int incl = s_off[j];
+  const int total = s_off[kPlanThreads - 1];
+  const int head0 = *free_head;
+  if (j < n) {
+    const int off = incl - np;
+    for (int k = 0; k < np; ++k) {
+      const int64_t lp = lp0 + k;
+      const int idx = head0 + off + k;
+      if (idx >= n_pages) {
+        atomicOr(status, 1);        // free list exhausted: the page stays unassigned (the requant is skipped)
+      } else if (lp >= max_pages) {
+        atomicOr(status, 2);        // page-table row full
+      } else {
+        page_table[(int64_t)s * pt_stride + lp] = free_list[idx];
+      }
+    }
+  }
+  // the tokens' sequence ids and positions (binary search of the token's sequence over cu)
+  const int N = s_cu[n];
+  for (int i = j; i < N; i += kPlanThreads) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cu[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    seq_ids[i] = seqs[lo];
+    positions[i] = s_l0[lo] + (i - s_cu[lo]);
+  }
+  __syncthreads();   // every thread has read seq_lens (L0) and the head
+  if (j < n) seq_lens[s] = (int32_t)(L0 + (s_cu[j + 1] - s_cu[j]));
+  if (j == 0) *free_head = min(head0 + total, n_pages);
+}
+
 __global__ void page_table_update_kernel(int32_t* pt, int64_t pt_stride, int64_t n, const int32_t* seq,
                                          const int32_t* lpage, const int32_t* ppage) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -515,6 +587,20 @@ int kvt_page_table_update(void* page_table, int64_t pt_stride, int64_t n, const 
   hipLaunchKernelGGL(page_table_update_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      (int32_t*)page_table, pt_stride, n, (const int32_t*)seq, (const int32_t*)lpage,
                      (const int32_t*)ppage);
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
+}
+
+int kvt_append_plan(int n, const void* seqs, const void* cu, void* seq_lens, const void* ring_len,
+                    const void* ring_start, void* page_table, int64_t pt_stride, int max_pages, const void* free_list,
+                    int n_pages, void* free_head, void* seq_ids, void* positions, void* status, void* stream) {
+  if (n < 0 || n > kPlanThreads || pt_stride <= 0 || max_pages <= 0 || max_pages > pt_stride || n_pages < 0)
+    return n > kPlanThreads ? KVT_ERANGE : KVT_EINVAL;
+  if (n == 0) return KVT_OK;
+  hipLaunchKernelGGL(append_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, n, (const int32_t*)seqs,
+                     (const int32_t*)cu, (int32_t*)seq_lens, (const int32_t*)ring_len, (const int64_t*)ring_start,
+                     (int32_t*)page_table, pt_stride, max_pages, (const int32_t*)free_list, n_pages,
+                     (int32_t*)free_head, (int32_t*)seq_ids, (int64_t*)positions, (int32_t*)status);
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }

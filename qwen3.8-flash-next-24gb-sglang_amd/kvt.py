@@ -60,6 +60,15 @@ class AppendPlan:
         return int(self.seq_ids.numel())
 
 
+@dataclass
+class DevicePlan(AppendPlan):
+    """A fixed append layout (seqs[j] appends counts[j] tokens per call) whose positions, page pops and length
+    updates are computed on the device by launch_plan: one kernel, no host work, capturable in a HIP graph.  The
+    seq_ids / positions buffers are rewritten by every launch."""
+    seqs_dev: Optional[torch.Tensor] = None    # int32 [n]
+    cu_dev: Optional[torch.Tensor] = None      # int32 [n + 1]
+
+
 class PosTieredCache:
     """Per layer: INT4 pool k4/v4 uint8 [n_pages * 64, H, D // 2] + fp16 scales [.., H, D // 32], INT8 ring rk/rv
     int8 [ring_total, H, D] + fp16 scales [ring_total, H, D // group8].  Shared by all layers: per-sequence ring
@@ -90,11 +99,19 @@ class PosTieredCache:
         self.ring_start = torch.zeros(max_seqs, dtype=torch.int64, **z)
         self.seq_lens = torch.zeros(max_seqs, dtype=torch.int32, **z)
         self.alloc = PageAllocator(n_pages, page_seed)
+        # the same free list on the device, for plans computed there (kvt_append_plan): the permutation, the index of
+        # the next free page (kept equal to alloc.next: host pops are pushed before a device plan runs) and a status
+        # word the plan kernel raises when it could not give a page (1: pool exhausted, 2: page-table row full)
+        self.free_list = torch.tensor(self.alloc.free, dtype=torch.int32, device=self.device)
+        self.free_head = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.plan_status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._dev_head = 0
         self._ring_used = 0
         # host mirror
         self.h_len: List[int] = []
         self.h_ring: List[tuple] = []       # (base, len, start)
         self.h_pages: List[List[int]] = []
+        self.h_shared: List[int] = []       # shared prefix pages per sequence
 
     # -- sequences
     @property
@@ -115,6 +132,7 @@ class PosTieredCache:
         self.h_len.append(ring_start)
         self.h_ring.append((base, ring_len, ring_start))
         self.h_pages.append(list(shared_pages))
+        self.h_shared.append(len(shared_pages))
         self.ring_base[s] = base
         self.ring_len[s] = ring_len
         self.ring_start[s] = ring_start
@@ -131,6 +149,8 @@ class PosTieredCache:
     def plan_append(self, seqs: Sequence[int], counts: Sequence[int]) -> AppendPlan:
         """Positions of the next counts[i] tokens of seqs[i]; pages the evictions of this append enter for the first
         time are popped from the allocator and written into the device page table (one small launch)."""
+        if len(set(seqs)) != len(list(seqs)):
+            raise ValueError("a plan lists each sequence once")
         sid, pos, upd_s, upd_l, upd_p = [], [], [], [], []
         for s, n in zip(seqs, counts):
             base, R, start = self.h_ring[s]
@@ -155,8 +175,92 @@ class PosTieredCache:
             upd = torch.tensor([upd_s, upd_l, upd_p], dtype=torch.int32).to(dev)
             _lib.call("kvt_page_table_update", self.page_table.data_ptr(), self.page_table.stride(0), len(upd_s),
                       upd[0].data_ptr(), upd[1].data_ptr(), upd[2].data_ptr(), _lib.stream())
+        self._push_free_head()
         return AppendPlan(torch.tensor(sid, dtype=torch.int32).to(dev), torch.tensor(pos, dtype=torch.int64).to(dev),
                           list(counts), list(seqs))
+
+    def plan_device(self, seqs: Sequence[int], counts: Sequence[int]) -> DevicePlan:
+        """A device plan of the append layout `seqs[j]` appends `counts[j]` tokens (distinct sequences, each count at
+        most its ring): built once, then launched by launch_plan every step, e.g. one token per sequence for decode."""
+        seqs, counts = list(seqs), list(counts)
+        if len(set(seqs)) != len(seqs):
+            raise ValueError("a plan lists each sequence once")
+        if len(seqs) > 1024:
+            raise ValueError("a device plan covers at most 1024 sequences")
+        for s, n in zip(seqs, counts):
+            assert 0 <= s < self.n_seqs, f"unknown sequence {s}"
+            R = self.h_ring[s][1]
+            assert 0 <= n <= R, f"{n} tokens in one append exceed the ring of {R}"
+        cu = [0]
+        for n in counts:
+            cu.append(cu[-1] + n)
+        dev = self.device
+        self._push_free_head()   # (a plan is built eagerly, before any capture that launches it)
+        return DevicePlan(torch.zeros(cu[-1], dtype=torch.int32, device=dev),
+                          torch.zeros(cu[-1], dtype=torch.int64, device=dev), counts, seqs,
+                          torch.tensor(seqs, dtype=torch.int32, device=dev), torch.tensor(cu, dtype=torch.int32, device=dev))
+
+    def _new_pages(self, s: int, n: int) -> range:
+        """Logical pages that appending n tokens to sequence s enters for the first time (closed form)."""
+        base, R, start = self.h_ring[s]
+        L0 = self.h_len[s]
+        e0, e1 = max(start, L0 - R), L0 + n - R
+        lp0 = (e0 + PAGE - 1) // PAGE
+        return range(lp0, (e1 + PAGE - 1) // PAGE) if e1 > e0 else range(lp0, lp0)
+
+    def _push_free_head(self) -> None:
+        """Make the device free-list head equal the host allocator's position (pages popped on the host)."""
+        if self._dev_head != self.alloc.next:
+            self.free_head.fill_(self.alloc.next)
+            self._dev_head = self.alloc.next
+
+    def launch_plan(self, plan: DevicePlan) -> None:
+        """Enqueue the device plan (positions, page pops into the page table, seq_lens += counts); capturable.  Run
+        eagerly, it first pushes host-side pops to the device free-list head, checks capacity (RuntimeError, as the
+        host planner) and then advances the host mirror (lengths, pages) in closed form; under graph capture the
+        mirror is left as it is -- sync_host() reads the device state back after replays."""
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not capturing:
+            need = sum(len(self._new_pages(s, n)) for s, n in zip(plan.seqs, plan.counts))
+            if need > self.alloc.n_free:
+                raise RuntimeError("INT4 page pool exhausted")
+            for s, n in zip(plan.seqs, plan.counts):
+                r = self._new_pages(s, n)
+                if len(r) and r.stop > self.max_pages:
+                    raise RuntimeError("page table row full")
+            self._push_free_head()
+        _lib.call("kvt_append_plan", len(plan.seqs), plan.seqs_dev.data_ptr(), plan.cu_dev.data_ptr(),
+                  self.seq_lens.data_ptr(), self.ring_len.data_ptr(), self.ring_start.data_ptr(),
+                  self.page_table.data_ptr(), self.page_table.stride(0), self.max_pages, self.free_list.data_ptr(),
+                  self.free_list.numel(), self.free_head.data_ptr(), plan.seq_ids.data_ptr(),
+                  plan.positions.data_ptr(), self.plan_status.data_ptr(), _lib.stream())
+        if not capturing:
+            for s, n in zip(plan.seqs, plan.counts):
+                for lp in self._new_pages(s, n):
+                    assert lp == len(self.h_pages[s]), "page table out of order"
+                    self.h_pages[s].append(self.alloc.pop())
+                self.h_len[s] += n
+            self._dev_head = self.alloc.next
+
+    def sync_host(self) -> None:
+        """Rebuild the host mirror (lengths, page lists, allocator position) from the device after graph replays of
+        launch_plan (synchronizes the device).  Raises RuntimeError if a device plan could not give a page."""
+        status = int(self.plan_status.item())
+        if status:
+            raise RuntimeError(f"a device append plan could not give a page (status {status}: 1 = pool exhausted, "
+                               "2 = page-table row full)")
+        lens = self.seq_lens[:self.n_seqs].tolist()
+        pt = self.page_table[:self.n_seqs].tolist()
+        for s in range(self.n_seqs):
+            self.h_len[s] = int(lens[s])
+            self.h_pages[s] = [int(p) for p in pt[s][:self._page_count(s)]]
+        self.alloc.next = int(self.free_head.item())
+        self._dev_head = self.alloc.next
+
+    def _page_count(self, s: int) -> int:
+        """Entries of sequence s's page-table row: its shared prefix pages, or every page an evicted position has
+        entered (positions below hot_start), whichever is more."""
+        return max(self.h_shared[s], -(-self.hot_start(s) // PAGE))
 
     def append(self, layer: int, plan: AppendPlan, k: torch.Tensor, v: torch.Tensor) -> None:
         """Quantize-append the plan's tokens (k, v: [N, H, D] bf16/fp16/fp32) into layer `layer`."""
@@ -175,7 +279,9 @@ class PosTieredCache:
                   self.page_table.stride(0), None, None, self.group8, _lib.stream())
 
     def commit(self, plan: AppendPlan) -> None:
-        """Advance the sequence lengths after every layer has been written."""
+        """Advance the sequence lengths after every layer has been written (a device plan advanced them already)."""
+        if isinstance(plan, DevicePlan):
+            return
         for s, n in zip(plan.seqs, plan.counts):
             self.h_len[s] += n
         idx = torch.tensor(plan.seqs, dtype=torch.int64)
@@ -227,17 +333,21 @@ def _split_counts_mfma(lens: Sequence[int], H: int, blocks: int = 256) -> List[i
     return [int(max(1, min(-(-L // 256), round(per_head * L / tot)))) for L in lens]
 
 
-def _split_map(counts: List[int], ws: dict, device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Device split map {sequence, index, count} per split and the per-sequence counts, cached in the workspace
-    while the counts stay the same (lengths grow by one per step; the counts change rarely)."""
+def _split_map(counts: List[int], ws: dict, device) -> Tuple[torch.Tensor, torch.Tensor, List[int]]:
+    """Device split map {sequence, index, count} per split, the per-sequence counts on the device and as a list,
+    cached in the workspace while the counts stay the same (lengths grow by one per step; the counts change rarely).
+    Under graph capture a cached map is kept even if the lengths now suggest other counts: the kernel reads the
+    current lengths, so any split map gives the same result (the counts only steer the balance)."""
     key = ("split_map", tuple(counts))
     hit = ws.get("split_map_key")
+    if hit is not None and hit != key and torch.cuda.is_current_stream_capturing():
+        return ws["split_map"], ws["split_counts"], list(hit[1])
     if hit != key:
         rows = [(b, c, n) for b, n in enumerate(counts) for c in range(n)]
         ws["split_map"] = torch.tensor(rows, dtype=torch.int32).reshape(-1).to(device)
         ws["split_counts"] = torch.tensor(counts, dtype=torch.int32).to(device)
         ws["split_map_key"] = key
-    return ws["split_map"], ws["split_counts"]
+    return ws["split_map"], ws["split_counts"], list(counts)
 
 
 def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Optional[torch.Tensor] = None,
@@ -280,7 +390,7 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         chunk = 0   # every split holds a partial
         if splits is None and S > 1:
             counts = _split_counts_mfma(cache.h_len[:S], H)
-            split_map, split_counts = _split_map(counts, ws, q.device)
+            split_map, split_counts, counts = _split_map(counts, ws, q.device)
             n_chunks, n_map = max(counts), sum(counts)
         else:
             n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)

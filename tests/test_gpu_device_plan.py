@@ -1,0 +1,158 @@
+"""Device-side append plans (kvt_append_plan through PosTieredCache.plan_device / launch_plan): the same cache state as
+the host planner (plan_append / commit) for the same inputs -- codes, scales, page tables and lengths bit for bit,
+pages in the seeded allocator's order (the oracle's PageAllocator) -- eagerly and replayed in a HIP graph together
+with the decode, and the refusal paths (pool exhausted)."""
+import pytest
+import torch
+
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+H, D, HQ = 2, 256, 16
+NAMES = ("k4", "v4", "ks4", "vs4", "rk", "rv", "rks", "rvs")
+
+
+def _pair(rings, n_pages, seed, shared=0):
+    """Two identical caches (one per planner); sequence 0 starts after a shared prefix of `shared` positions whose
+    pages both caches pop first (sequence 1 references them too when there are at least two sequences)."""
+    from kvtier.kvt import PosTieredCache
+    cs = []
+    for _ in range(2):
+        c = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=sum(rings), max_seqs=len(rings), max_pages=64,
+                           device=dev, page_seed=seed)
+        pages = [c.alloc.pop() for _ in range(shared // 64)]
+        for i, r in enumerate(rings):
+            if shared and i < 2:
+                c.add_seq(r, ring_start=shared, shared_pages=pages)
+            else:
+                c.add_seq(r)
+        cs.append(c)
+    return cs
+
+
+def _same(a, b):
+    for name in NAMES:
+        assert torch.equal(getattr(a, name)[0], getattr(b, name)[0]), name
+    assert torch.equal(a.page_table, b.page_table) and torch.equal(a.seq_lens, b.seq_lens)
+    assert a.h_len == b.h_len and a.h_pages == b.h_pages and a.alloc.next == b.alloc.next
+
+
+def test_device_plan_matches_host_plan(kvt_pkg):
+    """Three sequences (rings 256 / 128 / 512; the first two share a 128-position prefix): chunked appends of
+    several layouts, then 200 single-token steps; after each call both caches agree bit for bit, and the final
+    page lists are the allocator's pages in request order."""
+    host, devc = _pair([256, 128, 512], n_pages=64, seed=3, shared=128)
+    g = torch.Generator(device=dev).manual_seed(7)
+    layouts = [([0, 1, 2], [100, 50, 300]), ([2, 0], [200, 256]), ([1], [128]), ([0, 1, 2], [1, 1, 1])]
+    plans = {}
+    for step in range(203):
+        seqs, counts = layouts[min(step, 3)]
+        n = sum(counts)
+        k = torch.randn(n, H, D, device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, H, D, device=dev, generator=g).to(torch.bfloat16)
+        hp = host.plan_append(seqs, counts)
+        host.append(0, hp, k, v)
+        host.commit(hp)
+        key = (tuple(seqs), tuple(counts))
+        if key not in plans:
+            plans[key] = devc.plan_device(seqs, counts)
+        dp = plans[key]
+        devc.launch_plan(dp)
+        devc.append(0, dp, k, v)
+        devc.commit(dp)
+        if step < 4 or step % 50 == 0:
+            torch.cuda.synchronize()
+            _same(host, devc)
+    torch.cuda.synchronize()
+    _same(host, devc)
+    assert int(devc.plan_status.item()) == 0
+    assert devc.alloc.next == int(devc.free_head.item())
+    order = ref.PageAllocator(64, seed=3).free
+    used = sorted(p for s in range(3) for p in devc.h_pages[s][(2 if s < 2 else 0):]) + sorted(devc.h_pages[0][:2])
+    assert sorted(used) == sorted(order[:devc.alloc.next])
+
+
+def test_device_plan_graph_replay(kvt_pkg):
+    """One decode step -- device plan (one token per sequence), append, decode -- captured once and replayed 300
+    times with fresh inputs copied in between: the cache then equals the host planner's after the same 300 appends,
+    the last replay's output equals an eager decode of the final state bit for bit (fixed tile order), and
+    sync_host() restores the host mirror."""
+    from kvtier.kvt import kvt_decode_attn
+    host, devc = _pair([512, 256], n_pages=64, seed=4)
+    g = torch.Generator(device=dev).manual_seed(8)
+    pre = [700, 300]
+    k = torch.randn(sum(pre), H, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(sum(pre), H, D, device=dev, generator=g).to(torch.bfloat16)
+    for c in (host, devc):   # the same prefill through the host planner
+        for a in range(0, 700, 256):
+            n0 = min(256, 700 - a)
+            n1 = min(256, max(0, 300 - a))
+            seqs = [0] + ([1] if n1 else [])
+            cnts = [n0] + ([n1] if n1 else [])
+            p = c.plan_append(seqs, cnts)
+            kk = torch.cat([k[a:a + n0]] + ([k[700 + a:700 + a + n1]] if n1 else []))
+            vv = torch.cat([v[a:a + n0]] + ([v[700 + a:700 + a + n1]] if n1 else []))
+            c.append(0, p, kk, vv)
+            c.commit(p)
+    steps = 300
+    knew = torch.randn(steps, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    vnew = torch.randn(steps, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    q = (torch.randn(2, HQ, D, device=dev, generator=g) / 16).to(torch.bfloat16)
+    kin, vin = knew[0].clone(), vnew[0].clone()
+    dp = devc.plan_device([0, 1], [1, 1])
+    ws = {}
+    out = torch.empty(2, HQ, D, device=dev)
+    # warm-up: fill the workspace (decode of the current state), then capture one step
+    kvt_decode_attn(devc, 0, q, out=out, impl="mfma", workspace=ws, splits=8, deterministic=True)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        devc.launch_plan(dp)
+        devc.append(0, dp, kin, vin)
+        kvt_decode_attn(devc, 0, q, out=out, impl="mfma", workspace=ws, splits=8, deterministic=True)
+    for i in range(steps):
+        kin.copy_(knew[i])
+        vin.copy_(vnew[i])
+        graph.replay()
+        hp = host.plan_append([0, 1], [1, 1])
+        host.append(0, hp, knew[i], vnew[i])
+        host.commit(hp)
+    torch.cuda.synchronize()
+    devc.sync_host()
+    _same(host, devc)
+    want = kvt_decode_attn(host, 0, q, impl="mfma", splits=8, deterministic=True)
+    assert torch.equal(out, want)
+
+
+def test_device_plan_refusals(kvt_pkg):
+    """Eagerly, a plan needing more pages than the pool holds raises before any launch; a launch through the C ABI
+    with an empty free list raises the status flag, assigns no page, writes no page-table entry, and sync_host()
+    reports it; a plan listing a sequence twice is refused."""
+    from kvtier import _lib
+    from kvtier.kvt import PosTieredCache
+    c = PosTieredCache(1, H, D, n_pages=2, ring_total=64, max_seqs=1, max_pages=8, device=dev, page_seed=1)
+    c.add_seq(64)
+    with pytest.raises(ValueError):
+        c.plan_device([0, 0], [1, 1])
+    p = c.plan_device([0], [64])
+    g = torch.Generator(device=dev).manual_seed(9)
+    for _ in range(3):   # 192 positions: pages for positions 0 .. 127
+        c.launch_plan(p)
+        c.append(0, p, torch.randn(64, H, D, device=dev, generator=g).to(torch.bfloat16),
+                 torch.randn(64, H, D, device=dev, generator=g).to(torch.bfloat16))
+    with pytest.raises(RuntimeError):
+        c.launch_plan(p)                 # positions 128 .. 191 need a third page
+    torch.cuda.synchronize()
+    pt0 = c.page_table.clone()
+    empty = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("kvt_append_plan", 1, p.seqs_dev.data_ptr(), p.cu_dev.data_ptr(), c.seq_lens.data_ptr(),
+              c.ring_len.data_ptr(), c.ring_start.data_ptr(), c.page_table.data_ptr(), c.page_table.stride(0),
+              c.max_pages, empty.data_ptr(), 0, c.free_head.data_ptr(), p.seq_ids.data_ptr(), p.positions.data_ptr(),
+              c.plan_status.data_ptr(), _lib.stream())
+    torch.cuda.synchronize()
+    assert int(c.plan_status.item()) == 1 and torch.equal(c.page_table, pt0) and int(c.seq_lens[0]) == 256
+    with pytest.raises(RuntimeError):
+        c.sync_host()

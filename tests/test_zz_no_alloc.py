@@ -53,7 +53,7 @@ def test_noalloc_ragged_split_map(kvt_pkg):
     ws = {}
     want = kvt_decode_attn(cache, 0, q, impl="mfma", deterministic=True, workspace=ws)
     counts = _split_counts_mfma(cache.h_len, H)
-    smap, scounts = _split_map(counts, {}, q.device)
+    smap, scounts, _ = _split_map(counts, {}, q.device)
     got = torch.empty_like(want)
     kvt_decode_attn_noalloc(cache, 0, q, got, splits=max(counts), split_map=smap, split_counts=scounts,
                             deterministic=True)
