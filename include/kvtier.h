@@ -236,7 +236,8 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
                             void* stream);
 
 /* Causal prefill attention of a chunk of queries over the position-indexed tiered cache on the matrix cores
- * (v_mfma_f32_16x16x32_f16, K/V tiles dequantized once per 16 queries into LDS).  Sequence b's queries are rows
+ * (v_mfma_f32_16x16x32_bf16, K/V tiles dequantized once per 16 queries into LDS as the exact bf16 rows
+ * bf16(code * scale); P as two bf16 parts; fp32 softmax and accumulation).  Sequence b's queries are rows
  * cu_q[b] .. cu_q[b+1] of q (bf16 [total_q, Hq, D], strides sq_n / sq_h) at positions kv_lens[b] - q_len .. ;
  * each attends to every position <= its own (patches/kv_paged_prefix.py:200), read from the cache tiers of
  * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16

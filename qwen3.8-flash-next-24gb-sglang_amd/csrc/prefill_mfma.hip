@@ -6,18 +6,21 @@
 // from the chunk's own bf16 K/V (the reference attends to fresh bf16 K/V there).
 //
 // Work item = (sequence, KV head, tile of 16 queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
-// first.  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as fp16
+// first.  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as bf16
 // (threads 0-255 the K tile row-major, threads 256-511 the V tile transposed), with the next tile's codes already
 // loaded into registers during the matrix work on the current one; the eight wavefronts then reuse it for their
 // 2 queries x 8 heads = 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
 // docs/KV_PAGED_PREFIX_PLAN.md:188-191).
-//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 K rows x 32 channels from LDS, B = Q (rows = 2 queries x 8
-//   heads) held in registers, pre-multiplied by scale * log2(e).  The D
+//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 channels from LDS, B = Q (rows = 2 queries x 8
+//   heads) held in registers as the input bf16 values; the fp32 scores are scaled by scale * log2(e).  The D
 //   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
 //   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
-//   O += P V on the same instruction: B = V^T rows from LDS (one 16-byte read per 16-dim column block).
-// Numerics: fp16 K/V = code * scale (finer than the oracle's bf16 rows), fp16 Q * scale * log2(e) and P, fp32
-// accumulation and softmax; bf16 (as the reference) or fp32 output.
+//   O += P V on the same instruction: B = V^T rows from LDS (one 16-byte read per 16-dim column block); P enters
+//   as a bf16 high part and a bf16 remainder (two products), ~16 significant bits.
+// Numerics: the K/V operands are exactly the oracle's rows, bf16(code * scale) rounded to nearest even from the
+// exact fp32 product (or the chunk's own bf16 K/V); Q exact; fp32 accumulation and softmax; bf16 (as the reference)
+// or fp32 output.  Every value of the clamp regime (scale 65504, |code * scale| up to 127 * 65504) is finite in
+// bf16.
 
 #include "kvt_common.h"
 
@@ -25,8 +28,7 @@ using namespace kvt;
 
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
@@ -34,17 +36,17 @@ constexpr int kD = 256;
 constexpr int kQT = 16;                 // queries per block
 constexpr int kT = 32;                  // key positions per tile
 // LDS tiles, XOR-swizzled so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
-//   K: fp16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
+//   K: bf16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
 //      4 st + kb of 16 consecutive keys: 16 distinct chunks mod 16, i.e. all 64 banks.
-//   V^T: fp16 row per dim (64 B = 32 keys) in four 16-byte chunks; chunk q holds the keys of matrix k-group q
+//   V^T: bf16 row per dim (64 B = 32 keys) in four 16-byte chunks; chunk q holds the keys of matrix k-group q
 //      (keys 4 q .. 4 q + 3, then 16 + 4 q .. 16 + 4 q + 3: the k order of the P operand).  Dim d is stored in row
 //      r = d ^ ((d >> 4) & 3), its chunk q at chunk q ^ ((r >> 1) & 3).  A B-operand read is one 16-byte read of
 //      chunk kb for 16 consecutive dims: each 8-lane phase covers 8 distinct 16-byte bank groups whether the LDS
 //      is served as 32 or 64 banks; the transposed dword stores of the dequantizing threads (16 key pairs x 4 dim
 //      blocks per wavefront) hit distinct banks per 32 lanes.  Measured: 18.1 M bank-conflict cycles per 10k-token
 //      chunk dispatch, against 60.2 M with 8-byte chunks.
-constexpr int kKPitch = kD * 2;         // bytes per fp16 K row
-constexpr int kVPitch = kT * 2;         // bytes per fp16 V^T row
+constexpr int kKPitch = kD * 2;         // bytes per bf16 K row
+constexpr int kVPitch = kT * 2;         // bytes per bf16 V^T row
 KVT_DEV uint32_t k_chunk(int key, int c) { return 16u * (uint32_t)(c ^ (key & 15)); }
 KVT_DEV uint32_t vt_row_chunk(int dim, int q) {
   const int row = dim ^ ((dim >> 4) & 3);
@@ -84,9 +86,12 @@ struct __align__(16) Lds {
   int32_t pages[kMaxLdsPages];
 };
 
-KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-KVT_DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
-KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
+KVT_DEV f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+
+// bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
+KVT_DEV uint32_t bf2(float lo, float hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
 
 KVT_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -180,52 +185,44 @@ KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   return x;
 }
 
-// 8 INT4 codes (one dword, natural channel order c0..c7) -> 4 fp16 pairs (c0,c1) .. (c6,c7) = (code - 8) * s.
-KVT_DEV void int4_pairs(uint32_t w, h2 s2, uint32_t out[4]) {
-  const h2 mul = {(_Float16)1.0f, (_Float16)0.0625f};
-  const h2 add = {(_Float16)-1032.0f, (_Float16)-72.0f};
+// 8 INT4 codes (one dword, natural channel order c0..c7; byte j = channels 2 j (low nibble), 2 j + 1) -> 4 bf16
+// pairs bf16((code - 8) * s): (n - 8) s = fma(n, s, -8 s) is exact in fp32 (15 significant bits), then RNE.
+KVT_DEV void int4_pairs(uint32_t w, float s, uint32_t out[4]) {
+  const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+  const float m8 = -8.0f * s;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // byte i into bytes 0 and 2, then low nibble -> half 0, high nibble (<< 4) -> half 1
-    const uint32_t x = __builtin_amdgcn_perm(w, w, 0x0C000C00u | ((uint32_t)i << 16) | (uint32_t)i);
-    const uint32_t m = (x & 0x00F0000Fu) | 0x64006400u;
-    out[i] = as_u32((as_h2(m) * mul + add) * s2);
-  }
+  for (int i = 0; i < 4; ++i)
+    out[i] = bf2(fmaf((float)((ev >> (8 * i)) & 0xffu), s, m8), fmaf((float)((od >> (8 * i)) & 0xffu), s, m8));
 }
 
-// 4 INT8 codes (one dword) -> 2 fp16 pairs = code * s.
-KVT_DEV void int8_pairs(uint32_t w, h2 s2, uint32_t out[2]) {
+// 4 INT8 codes (one dword) -> 2 bf16 pairs bf16(code * s): (b + 128) s - 128 s, exact in fp32, then RNE.
+KVT_DEV void int8_pairs(uint32_t w, float s, uint32_t out[2]) {
   const uint32_t u = w ^ 0x80808080u;
-  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  out[0] = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + off) * s2);
-  out[1] = as_u32((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + off) * s2);
+  const float m = -128.0f * s;
+  out[0] = bf2(fmaf((float)(u & 0xffu), s, m), fmaf((float)((u >> 8) & 0xffu), s, m));
+  out[1] = bf2(fmaf((float)((u >> 16) & 0xffu), s, m), fmaf((float)(u >> 24), s, m));
 }
 
-// 2 bf16 (one dword) -> 2 fp16.
-KVT_DEV uint32_t bf16x2_to_f16x2(uint32_t w) {
-  const float lo = __uint_as_float(w << 16), hi = __uint_as_float(w & 0xffff0000u);
-  const h2 r = {(_Float16)lo, (_Float16)hi};
-  return as_u32(r);
-}
+KVT_DEV float scale_of(uint32_t s) { return f16_bits_to_f32((uint16_t)(s & 0xffffu)); }
 
-KVT_DEV h2 splat(uint32_t s) { return as_h2((s & 0xffffu) | ((s & 0xffffu) << 16)); }
-
-// K row fragment -> LDS (fp16, natural order): channels 32 dc .. 32 dc + 31 of key row `key` (4 chunks).
+// K row fragment -> LDS (bf16, natural order): channels 32 dc .. 32 dc + 31 of key row `key` (4 chunks).
 KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
   uint32_t o[16];
   if (x.hot == 2) {
     const uint32_t w[16] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w,
                             x.c.x, x.c.y, x.c.z, x.c.w, x.d.x, x.d.y, x.d.z, x.d.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = bf16x2_to_f16x2(w[i]);
+    for (int i = 0; i < 16; ++i) o[i] = w[i];
   } else if (x.hot == 1) {
     const uint32_t w[8] = {x.b.x, x.b.y, x.b.z, x.b.w, x.c.x, x.c.y, x.c.z, x.c.w};
+    const float sc = scale_of(x.s8);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) int8_pairs(w[i], splat(x.s8), o + 2 * i);
+    for (int i = 0; i < 8; ++i) int8_pairs(w[i], sc, o + 2 * i);
   } else {
     const uint32_t w[4] = {x.a.x, x.a.y, x.a.z, x.a.w};
+    const float sc = scale_of(x.s4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) int4_pairs(w[i], splat(x.s4), o + 4 * i);
+    for (int i = 0; i < 4; ++i) int4_pairs(w[i], sc, o + 4 * i);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -233,19 +230,21 @@ KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
                                                                           o[4 * i + 3]);
 }
 
-// 16 channels of one V row -> 8 fp16 pairs (natural order).
+// 16 channels of one V row -> 8 bf16 pairs (natural order).
 KVT_DEV void v_row16(const RawV& x, int t, uint32_t o[8]) {
   if (x.hot[t] == 2) {
     const uint32_t c[8] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w, x.bb[t].x, x.bb[t].y, x.bb[t].z, x.bb[t].w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = bf16x2_to_f16x2(c[i]);
+    for (int i = 0; i < 8; ++i) o[i] = c[i];
   } else if (x.hot[t] == 1) {
     const uint32_t c[4] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w};
+    const float sc = scale_of(x.s8[t]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) int8_pairs(c[i], splat(x.s8[t]), o + 2 * i);
+    for (int i = 0; i < 4; ++i) int8_pairs(c[i], sc, o + 2 * i);
   } else {
-    int4_pairs(x.c4[t].x, splat(x.s4[t]), o);
-    int4_pairs(x.c4[t].y, splat(x.s4[t]), o + 4);
+    const float sc = scale_of(x.s4[t]);
+    int4_pairs(x.c4[t].x, sc, o);
+    int4_pairs(x.c4[t].y, sc, o + 4);
   }
 }
 
@@ -329,10 +328,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   __syncthreads();
 
   // ---- Q operands: row j of the wavefront's 16 = query qt0 + 2 wave + (j >> 3), head j & 7
-  h8 qop[8];
+  bf8 qop[8];
   int64_t qpos;   // position of this lane's query row (as the S^T column)
+  const float qmul = scale * kLog2e;
   {
-    const float qmul = scale * kLog2e;
     const int64_t qi = qt0 + 2 * wave + (n16 >> 3);
     const int hq = n16 & 7;
     const bool ok = qi < q_len && hq < gs;
@@ -341,10 +340,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = bf16_to_f32(qr[32 * st + 8 * kb + e]) * qmul;
-        qop[st][e] = (_Float16)(ok ? x : 0.0f);
-      }
+      for (int e = 0; e < 8; ++e)
+        qop[st][e] = __builtin_bit_cast(__bf16, (uint16_t)(ok ? qr[32 * st + 8 * kb + e] : 0));
     }
   }
 
@@ -388,11 +385,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       const uint8_t* krow = lds.k[cb] + (16 * nt + n16) * kKPitch;
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const h8 a = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(krow + k_chunk(n16, 4 * st + kb)));
+        const bf8 a = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(krow + k_chunk(n16, 4 * st + kb)));
         d0 = mfma(a, qop[st], d0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r];
+      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r] * qmul;
     }
     __builtin_amdgcn_s_setprio(1);
     // ---- tile it + 1 into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go
@@ -417,8 +414,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
           s[nt][r] = (kp <= qp && kp < kend) ? s[nt][r] : -INFINITY;
         }
     }
-    // ---- online softmax; P as the A operand of P.V
-    h8 pa;
+    // ---- online softmax; P as the A operand of P.V (bf16 high part pa, remainder pb)
+    bf8 pa, pb;
     {
       float mloc = -INFINITY;
 #pragma unroll
@@ -427,7 +424,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[nt][r]);
       mloc = max_xor16_32(mloc);
       // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
-      // by more than 8 (log2 units), so P = 2^(s - m) <= 256 stays well inside fp16
+      // by more than 8 (log2 units), so P = 2^(s - m) <= 256
       const float m_new = fmaxf(m_run, mloc);
       if (__any(m_new > m_run + 8.0f)) {
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -452,15 +449,22 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
           psum += s[nt][r];
         }
       l_run += psum;
-      pa = h8{(_Float16)s[0][0], (_Float16)s[0][1], (_Float16)s[0][2], (_Float16)s[0][3],
-              (_Float16)s[1][0], (_Float16)s[1][1], (_Float16)s[1][2], (_Float16)s[1][3]};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = s[i >> 1][2 * (i & 1)], x1 = s[i >> 1][2 * (i & 1) + 1];
+        hw[i] = bf2(x0, x1);
+        lw[i] = bf2(x0 - __uint_as_float(hw[i] << 16), x1 - __uint_as_float(hw[i] & 0xffff0000u));
+      }
+      pa = __builtin_bit_cast(bf8, u4v{hw[0], hw[1], hw[2], hw[3]});
+      pb = __builtin_bit_cast(bf8, u4v{lw[0], lw[1], lw[2], lw[3]});
     }
     // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read
     __builtin_amdgcn_s_setprio(0);
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      const h8 bv = __builtin_bit_cast(h8, *reinterpret_cast<const u4v*>(lds.vt[cb] + vt_row_chunk(16 * c + n16, kb)));
-      acc[c] = mfma(pa, bv, acc[c]);
+      const bf8 bv = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(lds.vt[cb] + vt_row_chunk(16 * c + n16, kb)));
+      acc[c] = mfma(pb, bv, mfma(pa, bv, acc[c]));
     }
     __builtin_amdgcn_s_setprio(1);
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more

@@ -4,8 +4,10 @@ Chunked prefill as the reference serves it (patches/kv_paged_prefix.py:200, docs
 first chunk attends to its own fresh bf16 K/V; every later chunk is first appended to the cache (the ring's oldest
 rows requantized into INT4 pages) and then attends to all positions up to its own, read back from the tiers.  The
 oracle is fp32 softmax attention over the oracle cache's bf16-dequantized rows (gemv/test_kv_paged_prefix.py:506-531).
-Tolerance: 2e-3 max-abs / 1e-3 mean-abs on fp32 outputs (fp16 K/V/Q/P on the matrix cores, fp32 accumulation); the
-bf16 output is the fp32 output rounded to nearest even, bit for bit.
+Tolerance: 2e-3 max-abs / 1e-3 mean-abs on fp32 outputs (bf16 K/V/Q equal to the oracle's, P as two bf16 parts on the
+matrix cores, fp32 accumulation); the bf16 output is the fp32 output rounded to nearest even, bit for bit.  The
+clamp regime (groups saturating the fp16 scale at 65504, gemv/test_kv_tiers.py:412-456) adds 2^-14 * sum_i p_i |v_i|:
+P's 16 significant bits against V rows of up to 127 * 65504.
 """
 import pytest
 import torch
@@ -18,9 +20,9 @@ H, D, HQ = 2, 256, 16
 SCALE = D ** -0.5
 
 
-def _chunked(lens_chunks, ring, seed, group8=64, n_pages=64):
+def _chunked(lens_chunks, ring, seed, group8=64, n_pages=64, edit=None):
     """Append chunks to a device and an oracle cache (one sequence); yield (start, n, xk, xv, dc, oc) after each
-    chunk's append."""
+    chunk's append.  `edit(start, xk, xv)` may change a chunk's rows before they are appended."""
     from kvtier.kvt import PosTieredCache
     gen = torch.Generator().manual_seed(seed)
     och = ref.outlier_channels(H, D, 8, gen)
@@ -33,6 +35,8 @@ def _chunked(lens_chunks, ring, seed, group8=64, n_pages=64):
     a = 0
     for n in lens_chunks:
         xk, xv = ref.make_kv(n, H, D, gen, och)
+        if edit is not None:
+            edit(a, xk, xv)
         done = 0
         while done < n:   # one append never exceeds the ring
             m = min(ring, n - done)
@@ -127,3 +131,76 @@ def test_prefill_two_sequences_cache(kvt_pkg):
         exp = _oracle_chunk(q[q0:q1], L - (q1 - q0), kk, vv)
         err = (out[q0:q1] - exp).abs()
         assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (s, float(err.max()), float(err.mean()))
+
+
+BIG_POS = (5, 40, 150, 250, 300)
+
+
+def _big_row(bf16_max):
+    """The reference's clamp-regime row (gemv/test_kv_tiers.py:412-415): KV head 0 channels 0-31 = +-1e6 / 5e5 / 4.6e5
+    / 1e5, KV head 1 channels 64-95 = bf16 max (1e6 where the row is attended from the bf16 source chunk: there the
+    V rows are the raw bf16 values, not dequantized ones bounded by 127 * 65504)."""
+    big = torch.zeros(H, D)
+    big[0, :32] = torch.tensor([1e6, -1e6, 5e5, -5e5, 4.6e5, -4.6e5, 1e5, -1e5] * 4)
+    big[1, 64:96] = torch.finfo(torch.bfloat16).max if bf16_max else 1e6
+    return big.to(torch.bfloat16)
+
+
+def _place_big(a, xk, xv):
+    for p in BIG_POS:
+        if a <= p < a + xk.shape[0]:
+            big = _big_row(bf16_max=a > 0)
+            xk[p - a] = big
+            xv[p - a] = -big
+
+
+def _clamp_case(zero_big_channels):
+    """Chunks 96 / 96 / 96 / 80 over ring 128 with the clamp rows at BIG_POS: positions 5 / 40 / 150 end in INT4 pages
+    (INT8 scale 65504, requantized to INT4 scale 65504), 250 / 300 stay INT8 ring rows; chunk 0 attends them from
+    the bf16 source.  Yields (out fp32, expected, bound) per chunk, bound = 2^-14 sum_i p_i |v_i| per output."""
+    from kvtier.kvt import kvt_prefill_attn
+    for a, n, xk, xv, dc, oc, gen in _chunked([96, 96, 96, 80], 128, seed=21, edit=_place_big):
+        q = ref.make_q(HQ, D, gen, n=n)
+        if zero_big_channels:
+            q[:, :8, :32] = 0
+            q[:, 8:, 64:96] = 0
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        if a == 0:
+            out = kvt_prefill_attn(dc, 0, q.to(dev), cu, k_src=xk.to(dev), v_src=xv.to(dev), out_dtype=torch.float32)
+            kk, vv = xk, xv
+        else:
+            out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32)
+            kk, vv = oc.rows(0)
+        yield a, q, out.cpu(), _oracle_chunk(q, a, kk, vv), 2.0 ** -14 * _oracle_chunk(q, a, kk, vv.abs()), kk
+
+
+def test_prefill_clamp_regime_tiers(kvt_pkg):
+    """Clamp rows in every tier, queries zero on the saturated channels: the scores stay ordinary while K rows reach
+    127 * 65504 (beyond fp16) and V rows carry the saturated values into every output; all outputs finite and within
+    2e-3 + 2^-14 sum p|v| of the oracle."""
+    for a, q, out, exp, bound, kk in _clamp_case(zero_big_channels=True):
+        assert torch.isfinite(out).all(), a
+        assert float(exp.abs().max()) > 1e4, a                   # the saturated V rows reach the outputs
+        assert bool(((out - exp).abs() <= 2e-3 + bound).all()), (a, float(((out - exp).abs() - bound).max()))
+
+
+def test_prefill_clamp_regime_scores(kvt_pkg):
+    """Clamp rows with random queries: scores of order 1e4 on the saturated keys.  Every output is finite; rows whose
+    softmax is one-hot (max weight > 1 - 1e-6) or ignores the clamp keys (their weight < 1e-12) match the oracle to
+    2e-3 + 2^-14 sum p|v| (elsewhere the outputs are ill-conditioned: fp32 rounding of 1e4-sized scores moves the
+    weights)."""
+    checked = 0
+    for a, q, out, exp, bound, kk in _clamp_case(zero_big_channels=False):
+        assert torch.isfinite(out).all(), a
+        n = q.shape[0]
+        for h in range(H):
+            s = torch.einsum("jgd,kd->jgk", q[:, 8 * h:8 * h + 8].float(), kk[:, h].float()) * SCALE
+            keys = torch.arange(kk.shape[0])
+            s = s.masked_fill(keys[None, None, :] > (a + torch.arange(n))[:, None, None], float("-inf"))
+            w = torch.softmax(s, dim=-1)
+            big = torch.tensor([p for p in BIG_POS if p < kk.shape[0]])
+            ok = (w.max(-1).values > 1 - 1e-6) | (w[..., big].sum(-1) < 1e-12)
+            err = (out[:, 8 * h:8 * h + 8] - exp[:, 8 * h:8 * h + 8]).abs() - bound[:, 8 * h:8 * h + 8]
+            assert bool((err[ok] <= 2e-3).all()), (a, h, float(err[ok].max()))
+            checked += int(ok.sum())
+    assert checked > 2000
