@@ -29,6 +29,9 @@ using namespace kvt;
 namespace {
 
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
@@ -88,9 +91,9 @@ struct __align__(16) Lds {
 
 KVT_DEV f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 
-// bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
+// bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32): lo in bits 0-15.
 KVT_DEV uint32_t bf2(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){lo, hi}, bf2v));
 }
 
 KVT_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
@@ -185,44 +188,63 @@ KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   return x;
 }
 
-// 8 INT4 codes (one dword, natural channel order c0..c7; byte j = channels 2 j (low nibble), 2 j + 1) -> 4 bf16
-// pairs bf16((code - 8) * s): (n - 8) s = fma(n, s, -8 s) is exact in fp32 (15 significant bits), then RNE.
-KVT_DEV void int4_pairs(uint32_t w, float s, uint32_t out[4]) {
-  const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
-  const float m8 = -8.0f * s;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    out[i] = bf2(fmaf((float)((ev >> (8 * i)) & 0xffu), s, m8), fmaf((float)((od >> (8 * i)) & 0xffu), s, m8));
+// Codes -> exact bf16 rows.  A code c with offset o (c + o >= 0) is placed in the mantissa of an fp16 "magic" value
+// h = 1024 + (c + o) (bits 0x6400 | (c + o)); v_fma_mix_f32 converts h and the fp16 scale s to fp32 and computes
+// h * s - (1024 + o) * s in one rounding, whose exact value c * s is representable (4 or 8 bits times the scale's
+// 11), so the result is the oracle's fp32 product; v_cvt_pk_bf16_f32 then rounds it to nearest even.
+KVT_DEV float mix(uint32_t w, int half, _Float16 s, float c) {
+  return fmaf((float)__builtin_bit_cast(h2v, w)[half], (float)s, c);
+}
+// (x & m) | o in one VALU instruction (VOP3 takes no literal and at most one scalar operand: m from a scalar
+// register, o from a vector register)
+KVT_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
+  return r;
+}
+KVT_DEV _Float16 half_of(uint32_t bits) { return __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu)); }
+
+// 8 INT4 codes (one dword; byte j = channel 2 j in the low nibble, 2 j + 1 in the high one, stored as code + 8) ->
+// 4 bf16 pairs in channel order; c = -1032 s.  Word A holds channels 0 / 4, B 1 / 5, C 2 / 6, D 3 / 7.
+KVT_DEV void int4_pairs(uint32_t w, _Float16 s, float c, uint32_t out[4]) {
+  const uint32_t A = and_or(w, 0x000F000Fu, 0x64006400u), B = and_or(w >> 4, 0x000F000Fu, 0x64006400u);
+  const uint32_t C = and_or(w >> 8, 0x000F000Fu, 0x64006400u), D = and_or(w >> 12, 0x000F000Fu, 0x64006400u);
+  out[0] = bf2(mix(A, 0, s, c), mix(B, 0, s, c));
+  out[1] = bf2(mix(C, 0, s, c), mix(D, 0, s, c));
+  out[2] = bf2(mix(A, 1, s, c), mix(B, 1, s, c));
+  out[3] = bf2(mix(C, 1, s, c), mix(D, 1, s, c));
 }
 
-// 4 INT8 codes (one dword) -> 2 bf16 pairs bf16(code * s): (b + 128) s - 128 s, exact in fp32, then RNE.
-KVT_DEV void int8_pairs(uint32_t w, float s, uint32_t out[2]) {
+// 4 INT8 codes (one dword) -> 2 bf16 pairs; c = -1152 s.  u = code + 128 per byte; e holds channels 0 / 2, o 1 / 3.
+KVT_DEV void int8_pairs(uint32_t w, _Float16 s, float c, uint32_t out[2]) {
   const uint32_t u = w ^ 0x80808080u;
-  const float m = -128.0f * s;
-  out[0] = bf2(fmaf((float)(u & 0xffu), s, m), fmaf((float)((u >> 8) & 0xffu), s, m));
-  out[1] = bf2(fmaf((float)((u >> 16) & 0xffu), s, m), fmaf((float)(u >> 24), s, m));
+  const uint32_t e = __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u);
+  const uint32_t o = __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u);
+  out[0] = bf2(mix(e, 0, s, c), mix(o, 0, s, c));
+  out[1] = bf2(mix(e, 1, s, c), mix(o, 1, s, c));
 }
-
-KVT_DEV float scale_of(uint32_t s) { return f16_bits_to_f32((uint16_t)(s & 0xffffu)); }
 
 // K row fragment -> LDS (bf16, natural order): channels 32 dc .. 32 dc + 31 of key row `key` (4 chunks).
+template <bool BF16>
 KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
   uint32_t o[16];
-  if (x.hot == 2) {
+  if constexpr (BF16) {
     const uint32_t w[16] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w,
                             x.c.x, x.c.y, x.c.z, x.c.w, x.d.x, x.d.y, x.d.z, x.d.w};
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[i] = w[i];
-  } else if (x.hot == 1) {
+  } else if (x.hot) {
     const uint32_t w[8] = {x.b.x, x.b.y, x.b.z, x.b.w, x.c.x, x.c.y, x.c.z, x.c.w};
-    const float sc = scale_of(x.s8);
+    const _Float16 s = half_of(x.s8);
+    const float c = -1152.0f * (float)s;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) int8_pairs(w[i], sc, o + 2 * i);
+    for (int i = 0; i < 8; ++i) int8_pairs(w[i], s, c, o + 2 * i);
   } else {
     const uint32_t w[4] = {x.a.x, x.a.y, x.a.z, x.a.w};
-    const float sc = scale_of(x.s4);
+    const _Float16 s = half_of(x.s4);
+    const float c = -1032.0f * (float)s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) int4_pairs(w[i], sc, o + 4 * i);
+    for (int i = 0; i < 4; ++i) int4_pairs(w[i], s, c, o + 4 * i);
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -231,28 +253,32 @@ KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
 }
 
 // 16 channels of one V row -> 8 bf16 pairs (natural order).
+template <bool BF16>
 KVT_DEV void v_row16(const RawV& x, int t, uint32_t o[8]) {
-  if (x.hot[t] == 2) {
+  if constexpr (BF16) {
     const uint32_t c[8] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w, x.bb[t].x, x.bb[t].y, x.bb[t].z, x.bb[t].w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = c[i];
-  } else if (x.hot[t] == 1) {
+  } else if (x.hot[t]) {
     const uint32_t c[4] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w};
-    const float sc = scale_of(x.s8[t]);
+    const _Float16 s = half_of(x.s8[t]);
+    const float cc = -1152.0f * (float)s;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) int8_pairs(c[i], sc, o + 2 * i);
+    for (int i = 0; i < 4; ++i) int8_pairs(c[i], s, cc, o + 2 * i);
   } else {
-    const float sc = scale_of(x.s4[t]);
-    int4_pairs(x.c4[t].x, sc, o);
-    int4_pairs(x.c4[t].y, sc, o + 4);
+    const _Float16 s = half_of(x.s4[t]);
+    const float cc = -1032.0f * (float)s;
+    int4_pairs(x.c4[t].x, s, cc, o);
+    int4_pairs(x.c4[t].y, s, cc, o + 4);
   }
 }
 
 // Two keys x 16 channels -> V^T rows (dim 16 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
+template <bool BF16>
 KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   uint32_t a[8], b[8];
-  v_row16(x, 0, a);
-  v_row16(x, 1, b);
+  v_row16<BF16>(x, 0, a);
+  v_row16<BF16>(x, 1, b);
   // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
   const int q = (tp >> 1) & 3;
   const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
@@ -361,11 +387,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   RawV rv_next;
   if (krole) {
     rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-    store_k(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
+    store_k<BF16>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
     if (ntiles > 1) rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
   } else {
     rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
-    store_v(rv_next, lds.vt[0], db, tp);
+    store_v<BF16>(rv_next, lds.vt[0], db, tp);
     if (ntiles > 1) rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
   }
   __syncthreads();
@@ -374,9 +400,18 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   for (int it = 0; it < ntiles; ++it) {
     const int t0 = it * kT;
     const int cb = it & 1;
-    // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16
-    // Issue priority: the matrix phases run at 0 and the VALU phases (dequantization, softmax) at 1, so the SIMD's
-    // two wavefronts overlap one's VALU work with the other's products (kernel 19.6 against 20.2 ms per 10k prompt).
+    const bool more = it + 1 < ntiles;
+    const int t2 = t0 + 2 * kT;
+    // Tile it + 1 goes into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go out.
+    // The V-role wavefronts do this before their score products and the K-role ones after: each SIMD runs one
+    // wavefront of each role, so one's dequantization (VALU) meets the other's products (matrix cores).  Issue
+    // priority: matrix phases at 0, VALU phases at 1.
+    __builtin_amdgcn_s_setprio(1);
+    if (!krole && more) {
+      store_v<BF16>(rv_next, lds.vt[cb ^ 1], db, tp);
+      if (it + 2 < ntiles) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+    }
+    // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16 (unscaled)
     __builtin_amdgcn_s_setprio(0);
     float s[2][4];
 #pragma unroll
@@ -389,20 +424,12 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         d0 = mfma(a, qop[st], d0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r] * qmul;
+      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r];
     }
     __builtin_amdgcn_s_setprio(1);
-    // ---- tile it + 1 into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go
-    // out: the dequantization's VALU work overlaps this tile's matrix work
-    if (it + 1 < ntiles) {
-      const int t2 = t0 + 2 * kT;
-      if (krole) {
-        store_k(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
-        if (it + 2 < ntiles) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
-      } else {
-        store_v(rv_next, lds.vt[cb ^ 1], db, tp);
-        if (it + 2 < ntiles) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
-      }
+    if (krole && more) {
+      store_k<BF16>(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
+      if (it + 2 < ntiles) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
     }
     // causal / end mask, only on the tiles that reach the block's first query or the key end
     if (t0 + kT > qmin || t0 + kT > kend) {
@@ -422,9 +449,9 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[nt][r]);
-      mloc = max_xor16_32(mloc);
+      mloc = max_xor16_32(mloc) * qmul;   // log2 units
       // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
-      // by more than 8 (log2 units), so P = 2^(s - m) <= 256
+      // by more than 8 (log2 units), so P = 2^(s qmul - m) <= 256
       const float m_new = fmaxf(m_run, mloc);
       if (__any(m_new > m_run + 8.0f)) {
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -445,7 +472,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          s[nt][r] = __builtin_amdgcn_exp2f(s[nt][r] - m_use);
+          s[nt][r] = __builtin_amdgcn_exp2f(fmaf(s[nt][r], qmul, -m_use));
           psum += s[nt][r];
         }
       l_run += psum;
