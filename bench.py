@@ -8,7 +8,10 @@ head x8 (seeded per layer), V ~ N(0,1), Q ~ N(0,1)/16, bf16.
 
 Prints ONE JSON line: value = KV GB/s (algorithmic KV payload + scale bytes read per step / step time), with
 us/token over all layers, the roofline of the decode kernel (live HIP-event timing of its launches) and the CPU
-oracle timed on a bounded sample (one layer at the full context) as the baseline.
+oracle timed on a bounded sample (one layer at the full context) as the baseline; its output also checks layer 0
+of the timed path against the oracle ("parity").  The same line carries "configs": compact figures of the other
+configurations (chunked prefill, quantize-append, decode with append, ragged decode, top-k sparse decode at 16 / 2
+and 24 / 2 heads), measured after the headline; --no-sub-configs leaves them out.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl mfma|ref]
 """
@@ -304,12 +307,16 @@ def prefill_workload(args) -> dict:
 
     for _ in range(args.warmup):
         run()
-    times, ev = [], []
+    times, evs = [], []
     for _ in range(args.steps):
+        ev = []
         times.append(run(ev))
+        evs.append(ev)
     torch.cuda.synchronize()
     t_prompt = min(times)
-    t_prefill = sum(a.elapsed_time(b) for a, b in ev) / 1e3 / args.steps
+    # per prompt, the sum of its prefill launches' event intervals; the least over the timed prompts (as t_prompt),
+    # since an interval also holds any wait for the host to issue the launch
+    t_prefill = min(sum(a.elapsed_time(b) for a, b in ev) for ev in evs) / 1e3
     flops = 4.0 * HQ * D * (N * (N + 1) // 2) * LAYERS
     cpu = None
     if not args.no_cpu_baseline:   # the last 64 queries of layer 0 over its dequantized cache (oracle rows)
@@ -433,9 +440,13 @@ def _graph_time(fn, warmup: int, reps: int) -> float:
 def sparse_workload(args) -> dict:
     """Top-k sparse decode over the tiered (slot-indexed) pool: 8 requests of 65,536 tokens on randomly allocated
     slots, 12 layers, 2,051 selected positions per request (distinct, random), INT8-G64 ring of 8,192 rows whose
-    owner table names one slot per row.  Times one HIP graph of the 12 layers' fused top-k decode (split-K +
-    combine) and, for scale, one of the 12 layers' gathers into the bf16 scratch alone (the reference's unfused
-    path runs an attention over that scratch on top).  Synthetic random codes and scales."""
+    owner table names one slot per row; args.hq query heads over 2 KV heads (16, or 24 as the served model).
+    Times one HIP graph of the 12 layers' fused top-k decode (split-K + combine) and, for scale, one of the 12
+    layers' gathers into the bf16 scratch alone (the reference's unfused path runs an attention over that scratch on
+    top).  Byte model per layer: each selected position's K and V rows of both KV heads from the tier that serves
+    it (codes + fp16 scales), plus the index entry, its req_to_token slot and the ring owner probe (4 B each).
+    Synthetic random codes and scales."""
+    hq = getattr(args, "hq", HQ)
     import kvtier  # noqa: F401
     from kvtier import sparse_attn as sa
     B, CTX, TOPK, R = 8, 65_536, 2051, 8192
@@ -465,8 +476,8 @@ def sparse_workload(args) -> dict:
     cu_k = torch.empty(B + 1, dtype=torch.int32, device="cuda")
     sa.qwen_sparse_fa2_cu_seqlens_triton(seq_lens, idx, counts, cu_k, B, TOPK)
     sm = (0.5 + torch.rand(H, D, device="cuda", generator=g)).half()
-    q = [(torch.randn(B, HQ, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
-    outs = [torch.empty(B, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
+    q = [(torch.randn(B, hq, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty(B, hq, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
     ws = [{} for _ in range(LAYERS)]
     scr_k = torch.empty(B * TOPK, H, D, dtype=torch.bfloat16, device="cuda")
     scr_v = torch.empty_like(scr_k)
@@ -475,7 +486,7 @@ def sparse_workload(args) -> dict:
     hot = (owner.long()[sel & (R - 1)] == sel)
     n_hot = int(hot.sum())
     n_cold = hot.numel() - n_hot
-    bytes_layer = H * 2 * (n_hot * (D + 2 * (D // 64)) + n_cold * (D // 2 + 2 * (D // 32)))
+    bytes_layer = H * 2 * (n_hot * (D + 2 * (D // 64)) + n_cold * (D // 2 + 2 * (D // 32))) + 3 * 4 * hot.numel()
 
     def fused():
         for layer in range(LAYERS):
@@ -499,10 +510,10 @@ def sparse_workload(args) -> dict:
     gbps = bytes_layer * LAYERS / t_fused / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_sparse(pools[0], owner, r2t, idx, q[0], R, sm)
     return {
-        "metric": "top-k sparse decode, fused (12 layers, batch 8, topk 2051): us per step", "value":
-            round(t_fused * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
+        "metric": f"top-k sparse decode, fused (12 layers, batch 8, topk 2051, {hq} Q / 2 KV heads): us per step",
+        "value": round(t_fused * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
         "warmup": args.warmup, "dtype": "bf16-mfma/f32", "data": "synthetic",
-        "config": {"workload": "8 requests x 65,536 tokens on random slots, 12 layers, 16 Q / 2 KV heads, D 256, "
+        "config": {"workload": f"8 requests x 65,536 tokens on random slots, 12 layers, {hq} Q / 2 KV heads, D 256, "
                                "2,051 selected positions each, tiered pool (INT8-G64 ring of 8,192 rows + INT4-G32)",
                    "hot_fraction": round(n_hot / hot.numel(), 4)},
         "gather_only_us_per_step": round(t_gather * 1e6, 1),
@@ -558,8 +569,8 @@ def lazy_workload(args) -> dict:
     seq_lens = torch.full((B,), CTXB, dtype=torch.int32, device="cuda")
     cu_k = torch.tensor([i * TOPK for i in range(B + 1)], dtype=torch.int32, device="cuda")
     cu_p = torch.tensor([i * CTXB for i in range(B + 1)], dtype=torch.int32, device="cuda")
-    q = [(torch.randn(B, HQ, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
-    outs = [torch.empty(B, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
+    q = [(torch.randn(B, hq, D, device="cuda", generator=g) / 4).to(torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty(B, hq, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
     scr_k = torch.empty(SIZE, H, D, dtype=torch.bfloat16, device="cuda")
     scr_v = torch.empty_like(scr_k)
 
@@ -776,6 +787,45 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     }
 
 
+def sub_configs(args) -> dict:
+    """Compact figures of the other configurations, measured in the same process after the headline (whose cache
+    is freed first): chunked prefill of a 10,001-token prompt, the 8,192-token quantize-append with eviction, decode
+    with append at a 10,001-token context, ragged 8-sequence decode, and the top-k sparse decode at 16 / 2 and
+    24 / 2 heads.  Each runs without its CPU baseline; a failure is reported in place of its figures."""
+    sub = argparse.Namespace(**vars(args))
+    sub.no_cpu_baseline, sub.steps, sub.warmup = True, 5, 1
+    res = {}
+
+    def run(name, fn, pick):
+        try:
+            res[name] = pick(fn(sub))
+        except Exception as e:  # noqa: BLE001 -- reported in the line, never hidden
+            res[name] = {"error": f"{type(e).__name__}: {e}"}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+
+    def pick_steps(r):
+        return {"us_per_step": r["value"], "device_us_per_step": r["device_us_per_step"],
+                "kv_GBps": r["kv_GBps_per_step"], "decode_graph_us_per_step": r["decode_graph_us_per_step"],
+                "decode_graph_kv_GBps": r["decode_graph_kv_GBps"]}
+
+    def pick_sparse(r):
+        return {"us_per_step": r["value"], "GBps": r["roofline"]["achieved"], "hbm_frac": r["roofline"]["frac"],
+                "kv_bytes_per_layer": r["kv_bytes_per_layer"], "gather_only_us_per_step": r["gather_only_us_per_step"]}
+
+    run("prefill10k", prefill_workload,
+        lambda r: {"ms_per_prompt": r["value"], "kernel_ms": r["roofline"]["kernel_ms"],
+                   "TFLOPs": r["roofline"]["achieved"], "mfma_frac": r["roofline"]["frac"]})
+    run("append8192", append_workload,
+        lambda r: {"GBps": r["value"], "hbm_frac": r["roofline"]["frac"], "us_per_launch": r["us_per_launch"]})
+    run("decode10k_append", lambda a: decode_steps_workload(a, False), pick_steps)
+    run("ragged8", lambda a: decode_steps_workload(a, True), pick_steps)
+    for hq in (16, 24):
+        run(f"sparse_topk2051_{hq}q", lambda a, hq=hq: sparse_workload(argparse.Namespace(**dict(vars(a), hq=hq))),
+            pick_sparse)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -787,6 +837,9 @@ def main():
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
     ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "lazy"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
+    ap.add_argument("--hq", type=int, default=HQ, help="query heads of the sparse workload (2 KV heads)")
+    ap.add_argument("--no-sub-configs", action="store_true",
+                    help="headline only: skip the compact figures of the other configurations")
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
                     help="summarize two rocprofv3 --pmc counter CSVs into the traffic file and exit")
@@ -909,6 +962,11 @@ def main():
     }
     if parity is not None and not parity["ok"]:
         line["invalid"] = "decode output outside the oracle tolerance"
+    if not args.no_sub_configs:
+        del cache, q, outs, ws, graph
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        line["configs"] = sub_configs(args)
     print(json.dumps(line))
     if parity is not None and not parity["ok"]:
         sys.exit(1)
