@@ -188,7 +188,7 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
  * (bit-reproducible).  split_map NULL: every (sequence, KV head) gets n_splits splits; otherwise split_map (int32
  * [n_map][3] = {sequence, split index, splits of that sequence}) lists the splits (per-sequence counts for ragged
  * batches) and n_splits is the partial slot stride per (sequence, head).  Partials in the layout of kvt_decode_ref;
- * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 8, D = 256, q and q_stride_b 16-byte
+ * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 16, D = 256, q and q_stride_b 16-byte
  * aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 <
  * 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the compact gather + FA2 pair (flat patch
  * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode.

@@ -5,7 +5,9 @@
 // kHotCost4 / 4 of a paged one; boundaries in the paged part are multiples of 32).  Inside a block, 32-position paged
 // tiles and 16-position ring tiles go to the wavefronts one at a time, from a counter in LDS (first come: the
 // wavefronts finish together although the oldest get more issue slots) or in a fixed order (bit-reproducible).
-// GQA groups of up to 8 q heads per KV head; the block copies the group's Q rows to LDS once.
+// GQA groups of up to 16 q heads per KV head, one per column of the MFMA B operand: groups of up to 8 fill columns
+// 0-7 and repeat them in 8-15, and the block copies the group's Q rows to LDS once; wider groups (up to 16) take a
+// column each and every wavefront reads its Q rows from memory (the LDS holds no 16 rows beside the tile stages).
 //   Paged positions (< hot_start, INT4-G32 pages through the page table): a 32-aligned tile lies in one 64-position
 //   page, i.e. 32 consecutive pool rows.  Each wavefront double-buffers its tiles in LDS with direct-to-LDS copies
 //   (buffer_load_dwordx4 ... lds, 16 B per lane): the next-but-one tile's K codes and scale rows are issued before a
@@ -18,7 +20,7 @@
 // QK^T (paged) on v_mfma_f32_16x16x32_f16, one instruction per 16 tokens x 32 channels (= one INT4 scale group):
 //   A = raw magic-number values of the codes (0x6400 | nibble = 1024 + n for even channels, 0x6400 | nibble << 4 =
 //   1024 + 16 n for odd channels: one v_and_or_b32 per two values), channel order [0,4,1,5,2,6,3,7] of each 8; B = Q
-//   in the same order with odd channels divided by 16, the group's q heads in columns 0-7 and again in 8-15.  Each
+//   in the same order with odd channels divided by 16, one q head per column (narrow groups: 0-7, again in 8-15).  Each
 //   product carries a constant excess: (1024 + n) q = (n - 8) q + 1032 q and (1024 + 16 n) q / 16 = (n - 8) q +
 //   1152 (q / 16); the per-(group, head) excess bias_g is token independent, so the score of token t is
 //   sum_g s_g(t) D_g(t) - sum_g s_g(t) bias_g.  The first sum folds the fp32 group results with the fp16 scales
@@ -31,7 +33,7 @@
 //   from ds_read_b64_tr_b4, a 16 x 16 nibble transpose per 16 lanes, which turns token-major code rows into the
 //   channel-major operand layout in one LDS instruction.
 // Ring P.V: v_mfma_f32_16x16x16_f16 with B from ds_read_b64_tr_b8 (exact fp16 codes) and the ring scale folded
-//   into P the same way.  Accumulators: acc[a] = 16 channels x 8 heads (rows 8-15 repeat 0-7).
+//   into P the same way.  Accumulators: acc[a] = 16 channels x 16 head rows (narrow groups: rows 8-15 repeat 0-7).
 // The block's wavefronts merge (max, sum, o) in LDS; one fp32 partial per (split, q head) goes to kvt_decode_combine.
 //
 // Numerics versus the oracle (bf16(code * scale) rows, fp32 softmax): codes enter exactly, K scales in fp32, V scales
@@ -150,12 +152,14 @@ union WaveArea {
   HotStage hot[2];
 };
 
-constexpr int kMergePitch = kD * 8 + (kD / 8) * 4;   // floats per wavefront: [dim][8 heads], 4 floats pad per 8 dims
+// floats per wavefront of the merge: [dim][8 or 16 heads], 4 floats of padding per 8 dims
+template <bool WIDE>
+constexpr int merge_pitch() { return kD * (WIDE ? 16 : 8) + (kD / 8) * 4; }
 
 struct MergeArea {
-  float m[kWaves][8];
-  float l[kWaves][8];
-  float o[kWaves][kMergePitch];
+  float m[kWaves][16];
+  float l[kWaves][16];
+  float o[kWaves * merge_pitch<true>()];
 };
 
 // A fixup block's per-wavefront merge of 64 output float4s (in-kernel merge of the splits).
@@ -436,7 +440,7 @@ KVT_DEV u4v cold_softmax(const float s[8], f4 acc[16], float& m_run, float& l_ru
     l_run *= alpha;
     float arow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, (4 * kb + i) & 7, 64);
+    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);   // lane 4 kb + i: the head of row 4 kb + i
 #pragma unroll
     for (int a = 0; a < 16; ++a)
 #pragma unroll
@@ -457,7 +461,7 @@ KVT_DEV u4v cold_softmax(const float s[8], f4 acc[16], float& m_run, float& l_ru
 }
 
 // P.V of one staged tile.  Per scale group g (32 channels) and half hf (16 channels 32 g + 16 hf + j):
-//   acc[2 g + hf] += A_g * B_{g,hf} + A_g * C,  A_g = P16 * s_v(t, g)  (8 heads in rows 0-7, again in 8-15),
+//   acc[2 g + hf] += A_g * B_{g,hf} + A_g * C,  A_g = P16 * s_v(t, g)  (one head per row),
 // where B_{g,hf} holds the raw magic values of the codes (1024 + n for tokens 0, 1, 4, 5 of the k block, 1024 + 16 n
 // for tokens 2, 3, 6, 7, whose P16 entries carry the 1/16) and C = -(1032 | 1152) removes the constant excess: the
 // products are exact in fp32 and the V scale never multiplies a code.  B comes from ds_read_b64_tr_b4, a 16 x 16
@@ -784,7 +788,7 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
     l_run *= alpha;
     float arow[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, (4 * kb + i) & 7, 64);
+    for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * kb + i, 64);   // lane 4 kb + i: the head of row 4 kb + i
 #pragma unroll
     for (int a = 0; a < 16; ++a)
 #pragma unroll
@@ -991,7 +995,7 @@ KVT_DEV void fixup_block(FixArea& F, const float* part_o, const float* part_ml, 
   }
 }
 
-template <int G8>
+template <int G8, bool WIDE>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64_t* ring_start,
                    const int32_t* page_table, int64_t pt_stride, const int32_t* split_map, int H, int n_splits,
@@ -1058,19 +1062,26 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
   const int64_t w0 = bound(c);
   const int64_t w1 = bound(c + 1);
   const float cscale = scale * kLog2e;
-  const int hq = n16 & 7;
+  const int hq = WIDE ? n16 : n16 & 7;   // the lane's q head (column n16 of the B operand)
   const bool qvalid = hq < gs;
-  // the group's q heads into LDS (waves 0-3, 1 KB each; heads beyond the group read as zero)
-  if (wave < 4) {
-    const i32x4 rq = buffer_rsrc(q + b * q_stride_b + (int64_t)h * gs * kD, (uint32_t)gs * kD * 2u);
-    copy16_to_lds(rq, &lds.q.q[2 * wave][0], (uint32_t)(1024 * wave + 16 * lane));
+  const uint16_t* qrow;                   // its Q row (a valid row of the group when the head is beyond it)
+  if constexpr (WIDE) {
+    qrow = q + b * q_stride_b + (int64_t)(h * gs + (qvalid ? hq : 0)) * kD;
+  } else {
+    // the group's q heads into LDS (waves 0-3, 1 KB each; heads beyond the group read as zero)
+    if (wave < 4) {
+      const i32x4 rq = buffer_rsrc(q + b * q_stride_b + (int64_t)h * gs * kD, (uint32_t)gs * kD * 2u);
+      copy16_to_lds(rq, &lds.q.q[2 * wave][0], (uint32_t)(1024 * wave + 16 * lane));
+    }
+    qrow = &lds.q.q[hq][0];
   }
   if (threadIdx.x == 0) {
     lds.q.cold_next = 2 * kWaves;   // the first round starts with tiles w and w + kWaves of each wavefront
     lds.q.hot_next = 0;
   }
 
-  f4 acc[16];   // acc[a]: channels 16 a + j (lane j + 16 kb), q heads 4 kb + i in rows (kb 2, 3 repeat kb 0, 1)
+  f4 acc[16];   // acc[a]: channels 16 a + j (lane j + 16 kb), q head 4 kb + i in row 4 kb + i (narrow groups:
+                // head (4 kb + i) % 8, rows of kb 2, 3 repeat kb 0, 1)
 #pragma unroll
   for (int a = 0; a < 16; ++a) acc[a] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
@@ -1086,7 +1097,7 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
     ColdMath M;
     M.cscale = cscale;
     M.nm = nibble_masks();
-    M.qrow = &lds.q.q[hq][0];
+    M.qrow = qrow;
     M.qvalid = qvalid;
     M.ready = false;
     cold_block(A, C, lds, wave, b, w0, ce, dyn, M, acc, m_run, l_run);
@@ -1105,47 +1116,55 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
              buffer_rsrc(A.rks + rbase * H * NG8, ring_rows * (uint32_t)H * NG8 * 2u),
              buffer_rsrc(A.rvs + rbase * H * NG8, ring_rows * (uint32_t)H * NG8 * 2u),
              (uint32_t)H * kD, (uint32_t)h * kD, (uint32_t)H * NG8 * 2u, (uint32_t)h * NG8 * 2u, R - 1};
-    hot_block<G8>(C, lds.w[wave], &lds.q.hot_next, dyn, hp, w1, &lds.q.q[hq][0], qvalid, cscale, acc, m_run, l_run);
+    hot_block<G8>(C, lds.w[wave], &lds.q.hot_next, dyn, hp, w1, qrow, qvalid, cscale, acc, m_run, l_run);
   }
 
-  // ---- merge the wavefronts (heads 0-7 of the group; lanes n16 >= 8 duplicate n16 - 8)
+  // ---- merge the wavefronts (narrow groups: heads 0-7, lanes n16 >= 8 duplicate n16 - 8)
+  constexpr int kPitch = merge_pitch<WIDE>();
+  constexpr int kRows = WIDE ? 16 : 8;    // distinct accumulator rows
   l_run = sum_xor16_32(l_run);
   wait_vmcnt<0>();                        // (a block without positions still has its Q copy in flight)
   __syncthreads();                        // every wavefront is done with its staging area
   const int tid = threadIdx.x;
   const bool fused = counters != nullptr;
-  if (kb == 0 && n16 < 8) {
+  if (kb == 0 && n16 < kRows) {
     lds.merge.m[wave][n16] = m_run;
     lds.merge.l[wave][n16] = l_run;
   }
   __syncthreads();
-  // accumulator row 4 kb + i is q head (4 kb + i) % 8 = 4 (kb & 1) + i; lanes kb < 2 write heads 0-7
+  // accumulator row 4 kb + i holds q head 4 kb + i (narrow: (4 kb + i) % 8, lanes kb < 2 write heads 0-7)
+  const bool writer = WIDE || kb < 2;
+  const int hrow = WIDE ? 4 * kb : 4 * (kb & 1);
   f4 wrow;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int hr = 4 * (kb & 1) + i;
+    const int hr = hrow + i;
     float M = lds.merge.m[0][hr];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) M = fmaxf(M, lds.merge.m[w][hr]);
     const float mw = lds.merge.m[wave][hr];
     wrow[i] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
   }
-  float* ow = lds.merge.o[wave];
-  if (kb < 2) {
+  float* ow = lds.merge.o + wave * kPitch;
+  if (writer) {
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       const int dim = 16 * a + n16;
-      *reinterpret_cast<f4*>(&ow[dim * 8 + (dim >> 3) * 4 + 4 * kb]) = acc[a] * wrow;
+      *reinterpret_cast<f4*>(&ow[dim * kRows + (dim >> 3) * 4 + hrow]) = acc[a] * wrow;
     }
   }
   __syncthreads();
-  // the block's partial: thread (d, half) holds o of dim d for q heads 4 half .. + 3; threads < gs (m, l) of a head
+  // the block's partial: thread (d, half) holds o of dim d for q heads kRows / 2 * half + 4 j + i; threads < gs
+  // (m, l) of a head
+  constexpr int kF4 = kRows / 8;          // float4s per thread
   const int d = tid & (kD - 1), half = tid / kD;
-  f4 ob = {0.f, 0.f, 0.f, 0.f};
-  {
-    const int base = d * 8 + (d >> 3) * 4 + 4 * half;
+  f4 ob[kF4];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) ob += *reinterpret_cast<const f4*>(&lds.merge.o[w][base]);
+  for (int j = 0; j < kF4; ++j) {
+    ob[j] = f4{0.f, 0.f, 0.f, 0.f};
+    const int base = d * kRows + (d >> 3) * 4 + (kRows / 2) * half + 4 * j;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) ob[j] += *reinterpret_cast<const f4*>(&lds.merge.o[w * kPitch + base]);
   }
   float mb = -INFINITY, lb = 0.f;   // natural-log units
   if (tid < gs) {
@@ -1159,8 +1178,12 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
   }
   // the partial, in the slot of this split (read by the combine kernel or by the mergers below)
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (4 * half + i < gs) st_dev(&part_o[(item * gs + 4 * half + i) * kD + d], ob[i]);
+  for (int j = 0; j < kF4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int hd = (kRows / 2) * half + 4 * j + i;
+      if (hd < gs) st_dev(&part_o[(item * gs + hd) * kD + d], ob[j][i]);
+    }
   if (tid < gs) {
     st_dev(&part_ml[(item * gs + tid) * 2 + 0], mb);
     st_dev(&part_ml[(item * gs + tid) * 2 + 1], lb);
@@ -1186,7 +1209,7 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
   if ((((uintptr_t)q) | (uintptr_t)(q_stride_b * 2)) & 15) return KVT_EINVAL;   // Q rows are copied in 16-byte pieces
   if (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL) return KVT_ERANGE;   // 32-bit byte offsets
   const int gs = Hq / H;
-  if (gs > 8 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
+  if (gs > 16 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
   if (counters != nullptr && out_f32 == nullptr && out_bf16 == nullptr) return KVT_EINVAL;
   // grid: the work blocks (rows 0 .. work_rows - 1), then, with counters, rows of fixup blocks
   const unsigned gx = split_map != nullptr ? (unsigned)n_map : (unsigned)n_splits;
@@ -1202,10 +1225,15 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
       out_stride_b, work_rows, batch, n_map
   const dim3 grid((unsigned)n_blocks);
   hipStream_t st = (hipStream_t)stream;
-  if (group8 == 64) {
-    hipLaunchKernelGGL(decode_mfma_kernel<64>, grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
+  const bool wide = gs > 8;
+  if (group8 == 64 && !wide) {
+    hipLaunchKernelGGL((decode_mfma_kernel<64, false>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
+  } else if (group8 == 64) {
+    hipLaunchKernelGGL((decode_mfma_kernel<64, true>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
+  } else if (group8 == 256 && !wide) {
+    hipLaunchKernelGGL((decode_mfma_kernel<256, false>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else if (group8 == 256) {
-    hipLaunchKernelGGL(decode_mfma_kernel<256>, grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
+    hipLaunchKernelGGL((decode_mfma_kernel<256, true>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else {
     return KVT_EINVAL;
   }

@@ -18,8 +18,9 @@ H, D, HQ = 2, 256, 16
 SCALE = D ** -0.5
 
 
-def _build(lens, rings, seed=0, n_pages=None, chunk=512, starts=None):
-    """Device and oracle caches with the same appended tokens (configuration-style K with outlier channels)."""
+def _build(lens, rings, seed=0, n_pages=None, chunk=512, starts=None, hq=HQ):
+    """Device and oracle caches with the same appended tokens (configuration-style K with outlier channels) and one
+    query of hq heads per sequence."""
     from kvtier.kvt import PosTieredCache
     gen = torch.Generator().manual_seed(seed)
     n_pages = n_pages or sum(max(0, l - r) // 64 + 2 for l, r in zip(lens, rings))
@@ -49,7 +50,7 @@ def _build(lens, rings, seed=0, n_pages=None, chunk=512, starts=None):
         dc.commit(plan)
         for s, n in zip(seqs, cnt):
             done[s] += n
-    q = ref.make_q(HQ, D, gen, n=len(lens))
+    q = ref.make_q(hq, D, gen, n=len(lens))
     oc.alloc = alloc   # the oracle's page allocator, for callers that keep appending
     return dc, oc, q
 
@@ -73,6 +74,26 @@ def test_decode_pos_rings(kvt_pkg, impl, tol, mtol):
     exp = _oracle_out(oc, q)
     err = (out - exp).abs()
     assert float(err.max()) < tol and float(err.mean()) < mtol, (float(err.max()), float(err.mean()))
+
+
+@pytest.mark.parametrize("hq", [20, 24, 32])
+def test_decode_mfma_wide_groups(kvt_pkg, hq):
+    """Groups of more than 8 q heads per KV head (10, 12 -- the served model's 24 / 2 -- and 16): one head per MFMA
+    column, Q rows read by every wavefront.  Three sequences through the split map and at fixed split counts, the
+    combine kernel and the in-kernel merge, against the oracle; the scalar reference kernel too."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([5000, 2100, 700], [2048, 1024, 256], seed=51, hq=hq)
+    qd = q.to(dev)
+    exp = _oracle_out(oc, q)
+    outs = {"map": kvt_decode_attn(dc, 0, qd, impl="mfma"),
+            "splits17": kvt_decode_attn(dc, 0, qd, impl="mfma", splits=17, deterministic=True),
+            "fused17": kvt_decode_attn(dc, 0, qd, impl="mfma", splits=17, tile_order="fixed", fused_combine=True),
+            "ref": kvt_decode_attn(dc, 0, qd, impl="ref")}
+    for name, out in outs.items():
+        assert out.shape == (3, hq, D), name
+        err = (out.cpu() - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (hq, name, float(err.max()), float(err.mean()))
+    assert float((outs["fused17"] - outs["splits17"]).abs().max()) < 1e-5
 
 
 @pytest.mark.parametrize("splits", [1, 3, 17, 64])
@@ -163,17 +184,19 @@ def test_decode_mfma_page_windows(kvt_pkg):
     assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (float(err.max()), float(err.mean()))
 
 
-def test_decode_mfma_closed_forms(kvt_pkg):
+@pytest.mark.parametrize("hq", [16, 24])
+def test_decode_mfma_closed_forms(kvt_pkg, hq):
     """Hot: a single ring position gives out == code * scale of its V row in fp32 (P = 1; the scale enters the matrix
     product through P and the fp16 x fp16 products are exact).  Cold: 64 identical rows in a shared INT4 page
     (positions below ring_start) give uniform attention, out == code * scale of that row; the V row is k / 8 with
     integers k in -7..7 and +-7 in every group of 32 channels, so every scale is exactly 1/8 and every partial sum of
     the kernel (raw 1024 + n / 1024 + 16 n values times 1/8 or 1/128, the constant excess removed per tile) is a
-    small multiple of 1/8: exact in fp32."""
+    small multiple of 1/8: exact in fp32.  16 q heads (groups of 8) and 24 (groups of 12, one head per column)."""
     from kvtier import sparse_attn as sa
     from kvtier.kvt import PosTieredCache, kvt_decode_attn
     gen = torch.Generator().manual_seed(4)
-    q = ref.make_q(HQ, D, gen)
+    q = ref.make_q(hq, D, gen)
+    gs = hq // H
     xk = (torch.randn(1, H, D, generator=gen) * 2).to(torch.bfloat16)
     xv = (torch.randn(1, H, D, generator=gen) * 2).to(torch.bfloat16)
     # hot
@@ -184,8 +207,8 @@ def test_decode_mfma_closed_forms(kvt_pkg):
     dc.commit(plan)
     out = kvt_decode_attn(dc, 0, q.to(dev), impl="mfma").cpu()
     vrow = dc.rv[0][0].cpu().float() * dc.rvs[0][0].cpu().float().repeat_interleave(64, -1)
-    for hq in range(HQ):
-        assert torch.equal(out[0, hq], vrow[hq // 8]), ("hot", hq)
+    for i in range(hq):
+        assert torch.equal(out[0, i], vrow[i // gs]), ("hot", i)
     # cold: page 1 holds 64 copies of the row, written by the INT4 writer; the sequence starts at position 64
     dc = PosTieredCache(1, H, D, n_pages=2, ring_total=64, max_seqs=1, max_pages=2, device=dev)
     ones = torch.ones(H, D, dtype=torch.float16, device=dev)
@@ -199,8 +222,8 @@ def test_decode_mfma_closed_forms(kvt_pkg):
     codes = ref.unpack4(dc.v4[0][64].cpu()).float()
     vrow = codes * dc.vs4[0][64].cpu().float().repeat_interleave(32, -1)
     assert torch.equal(dc.vs4[0][64].cpu().float(), torch.full((H, 8), 0.125)) and torch.equal(vrow, kv.float() / 8)
-    for hq in range(HQ):
-        assert torch.equal(out[0, hq], vrow[hq // 8]), ("cold", hq)
+    for i in range(hq):
+        assert torch.equal(out[0, i], vrow[i // gs]), ("cold", i)
 
 
 def test_decode_mfma_group256(kvt_pkg):
