@@ -243,7 +243,7 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
  * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16
  * [positions, H, D] rows (the reference attends to fresh bf16 K/V there).  out: bf16 or fp32 (out_f32) with the
  * layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
- * chunks.  Hq / H <= 8, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
+ * chunks.  Hq / H <= 16, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
  * offsets are 32-bit, else KVT_ERANGE). */
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,

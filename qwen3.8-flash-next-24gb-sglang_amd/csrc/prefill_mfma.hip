@@ -5,14 +5,15 @@
 // values come from the cache tiers (INT4 pages below hot_start, INT8 ring above) or, for a chunk without a prefix,
 // from the chunk's own bf16 K/V (the reference attends to fresh bf16 K/V there).
 //
-// Work item = (sequence, KV head, tile of 16 queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
-// first.  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as bf16
+// Work item = (sequence, KV head, tile of queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
+// first.  A wavefront owns 16 query rows = 16 / gs queries x the gs q heads of the KV head (gs <= 16; rows beyond
+// 16 / gs * gs idle).  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as bf16
 // (threads 0-255 the K tile row-major, threads 256-511 the V tile transposed), with the next tile's codes already
 // loaded into registers during the matrix work on the current one; the eight wavefronts then reuse it for their
-// 2 queries x 8 heads = 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
+// 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
 // docs/KV_PAGED_PREFIX_PLAN.md:188-191).
-//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 channels from LDS, B = Q (rows = 2 queries x 8
-//   heads) held in registers as the input bf16 values; the fp32 scores are scaled by scale * log2(e).  The D
+//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 channels from LDS, B = Q (the wavefront's 16 rows)
+//   held in registers as the input bf16 values; the fp32 scores are scaled by scale * log2(e).  The D
 //   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
 //   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
 //   O += P V on the same instruction: B = V^T rows from LDS (one 16-byte read per 16-dim column block); P enters
@@ -36,7 +37,6 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 256;
-constexpr int kQT = 16;                 // queries per block
 constexpr int kT = 32;                  // key positions per tile
 // LDS tiles, XOR-swizzled so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
 //   K: bf16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
@@ -292,7 +292,7 @@ KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   }
 }
 
-constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 2 queries x 8 heads = 16 rows
+constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 16 rows (16 / gs queries x gs heads)
 
 template <int G8, bool BF16>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -305,6 +305,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, kb = lane >> 4;
   const int qt = n_qtiles - 1 - (int)blockIdx.x;   // latest (heaviest) query tiles first
+  const int qpw = 16 / gs;                         // queries per wavefront
+  const int qb = kWaves * qpw;                     // queries per block
   const int b = blockIdx.y / H;
   const int h = blockIdx.y - b * H;
   const int64_t qs = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b]
@@ -314,9 +316,9 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   const int64_t q_len = qe - qs;
   const int64_t L = kv_lens[b];
   const int64_t q_pos0 = L - q_len;   // position of the chunk's first query
-  const int64_t qt0 = (int64_t)qt * kQT;
+  const int64_t qt0 = (int64_t)qt * qb;
   if (qt0 >= q_len) return;
-  const int64_t key_end = min(L, q_pos0 + min(q_len, qt0 + kQT));   // keys visible to the tile's last query
+  const int64_t key_end = min(L, q_pos0 + min(q_len, qt0 + qb));   // keys visible to the tile's last query
   constexpr uint32_t NG8 = kD / G8;
   Tier T;
   T.H = H;
@@ -353,14 +355,14 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   }
   __syncthreads();
 
-  // ---- Q operands: row j of the wavefront's 16 = query qt0 + 2 wave + (j >> 3), head j & 7
+  // ---- Q operands: row j of the wavefront's 16 = query qt0 + qpw wave + j / gs, head j % gs
   bf8 qop[8];
   int64_t qpos;   // position of this lane's query row (as the S^T column)
   const float qmul = scale * kLog2e;
   {
-    const int64_t qi = qt0 + 2 * wave + (n16 >> 3);
-    const int hq = n16 & 7;
-    const bool ok = qi < q_len && hq < gs;
+    const int rq = n16 / gs, hq = n16 - rq * gs;
+    const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
+    const bool ok = rq < qpw && qi < q_len;
     qpos = q_pos0 + qi;
     const uint16_t* qr = q + (qs + (ok ? qi : 0)) * sq_n + (int64_t)(h * gs + (ok ? hq : 0)) * sq_h;
 #pragma unroll
@@ -497,16 +499,16 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
   }
 
-  // ---- normalize and store: accumulator row 4 kb + i = query qt0 + 2 wave + (kb >> 1), head 4 (kb & 1) + i;
+  // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
   // column n16 of block c = dim 16 c + n16
   {
     const float l = sum_xor16_32(l_run);
-    const int64_t qi = qt0 + 2 * wave + (kb >> 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float lr = __shfl(l, 4 * kb + i, 64);
-      const int hq = 4 * (kb & 1) + i;
-      if (qi < q_len && hq < gs) {
+      const int r = 4 * kb + i, rq = r / gs, hq = r - rq * gs;
+      const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
+      if (rq < qpw && qi < q_len) {
         const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
         if (out_f32) {
           float* orow = reinterpret_cast<float*>(out) + o0;
@@ -534,7 +536,7 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
                      const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
                      int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
                      void* stream) {
-  if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || Hq / H > 8 || max_q < 0) return KVT_EINVAL;
+  if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || Hq / H > 16 || max_q < 0) return KVT_EINVAL;
   if ((k_bf16 == nullptr) != (v_bf16 == nullptr)) return KVT_EINVAL;
   const bool bf16 = k_bf16 != nullptr;
   // 32-bit byte offsets inside each buffer
@@ -548,7 +550,8 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
           (const int64_t*)ring_base, (const int32_t*)ring_len, (const int64_t*)ring_start,
           (const int32_t*)page_table, pt_stride,               (uint32_t)pool_rows,      (const uint16_t*)k_bf16,
           (const uint16_t*)v_bf16,   kb_n, kb_h, vb_n, vb_h, kb_rows};
-  const int n_qtiles = (max_q + kQT - 1) / kQT;
+  const int qb = kWaves * (16 / (Hq / H));   // queries per block
+  const int n_qtiles = (max_q + qb - 1) / qb;
   const dim3 grid((unsigned)n_qtiles, (unsigned)(batch * H));
   hipStream_t st = (hipStream_t)stream;
 #define KVT_PF(G, B)                                                                                              \

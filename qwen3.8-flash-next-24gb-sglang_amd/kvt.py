@@ -552,7 +552,7 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
     batch = cu_q.shape[0] - 1
     H, D = cache.H, cache.D
     Hq = q.shape[1]
-    assert Hq % H == 0 and Hq // H <= 8
+    assert Hq % H == 0 and Hq // H <= 16
     if kv_lens is None:
         kv_lens = cache.seq_lens[:batch]
     assert kv_lens.dtype == torch.int32 and kv_lens.is_cuda and kv_lens.numel() >= batch

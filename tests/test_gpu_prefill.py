@@ -79,6 +79,25 @@ def test_prefill_chunks_vs_oracle(kvt_pkg, group8):
         assert torch.equal(outb.cpu(), out.to(torch.bfloat16)), ("bf16 output != rounded fp32 output", a)
 
 
+@pytest.mark.parametrize("hq", [20, 24, 32])
+def test_prefill_wide_groups(kvt_pkg, hq):
+    """Groups of more than 8 q heads per KV head (10, 12 -- the served model's 24 / 2 -- and 16): 16 / gs queries per
+    wavefront; chunk 0 from bf16, chunks 1-2 from the tiers (ragged last query tiles), fp32 and bf16 outputs."""
+    from kvtier.kvt import kvt_prefill_attn
+    for a, n, xk, xv, dc, oc, gen in _chunked([96, 90, 37], 128, seed=14):
+        q = ref.make_q(hq, D, gen, n=n)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        src = dict(k_src=xk.to(dev), v_src=xv.to(dev)) if a == 0 else {}
+        out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32, **src).cpu()
+        outb = kvt_prefill_attn(dc, 0, q.to(dev), cu, **src).cpu()
+        kk, vv = (xk, xv) if a == 0 else oc.rows(0)
+        exp = _oracle_chunk(q, a, kk, vv)
+        err = (out - exp).abs()
+        assert out.shape == (n, hq, D)
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (hq, a, float(err.max()), float(err.mean()))
+        assert torch.equal(outb, out.to(torch.bfloat16)), (hq, a)
+
+
 def test_prefill_first_query_closed_form(kvt_pkg):
     """Query 0 of a chunk without a prefix sees only key 0: the output is exactly that V row (P = 1), for every q
     head of each KV head."""
