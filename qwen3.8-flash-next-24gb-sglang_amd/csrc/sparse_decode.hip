@@ -154,17 +154,19 @@ KVT_DEV void issue_tile(const PoolRsrc& P, int flags, uint32_t coff, uint32_t so
   }
 }
 
-// One 16-column tile of a wavefront, folded into its running softmax state (m, l per q head n16 of this lane, o):
-// resolve the columns, load and dequantize K into the wavefront's LDS rows, S^T = K Q^T, dequantize V into the same
-// rows, online softmax, O += P V.
+// A tile's 16 columns resolved by lanes 0-15 (lane r: column c0 + r): attended or not, tier, and the row's byte
+// offsets in its tier (codes: INT8 rows D bytes, INT4 rows D / 2; scales).
+struct TileCols {
+  int flags;   // bit 0 attended, bit 1 ring (INT8) row
+  uint32_t coff, soff;
+};
+
+// Resolve a tile's columns: position from the index row, slot from req_to_token, tier from the owner table (three
+// dependent loads, independent of Q).
 template <int KIND, int G8>
-KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt, int64_t c0,
-                         int64_t c_end, const int32_t* idx_row, int64_t L, int64_t req, int h, int lane,
-                         const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16]) {
-  const int H = A.H;
-  const int n16 = lane & 15, kq = lane >> 4;
-  // lane r < 16 resolves column c0 + r to (valid, hot, row)
-  const int64_t col = c0 + n16;
+KVT_DEV TileCols resolve_tile(const SparseArgs& A, int64_t c0, int64_t c_end, const int32_t* idx_row, int64_t L,
+                              int64_t req, int h, int lane) {
+  const int64_t col = c0 + (lane & 15);
   bool valid = false, hot = KIND == 0;
   int64_t row = 0;
   if (lane < kRows && col < c_end) {
@@ -182,13 +184,24 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
       }
     }
   }
-  const int flags = (valid ? 1 : 0) | (hot ? 2 : 0);
-  // the row's byte offsets in its tier: codes (INT8 rows D bytes, INT4 rows D / 2) and scales
-  const int64_t rh = row * H + h;
-  const uint32_t coff = !valid ? kNoRow : (uint32_t)(hot ? rh * kD : rh * (kD / 2));
-  const uint32_t soff = !valid ? kNoRow : (uint32_t)(hot ? rh * (kD / G8) * 2 : rh * (kD / kG4) * 2);
+  const int64_t rh = row * A.H + h;
+  TileCols tc;
+  tc.flags = (valid ? 1 : 0) | (hot ? 2 : 0);
+  tc.coff = !valid ? kNoRow : (uint32_t)(hot ? rh * kD : rh * (kD / 2));
+  tc.soff = !valid ? kNoRow : (uint32_t)(hot ? rh * (kD / G8) * 2 : rh * (kD / kG4) * 2);
+  return tc;
+}
+
+// One resolved 16-column tile of a wavefront, folded into its running softmax state (m, l per q head n16 of this
+// lane, o): load and dequantize K into the wavefront's LDS rows, S^T = K Q^T, dequantize V into the same rows,
+// online softmax, O += P V.
+template <int KIND, int G8>
+KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt, const TileCols& tc,
+                         int lane, const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16]) {
+  const int n16 = lane & 15, kq = lane >> 4;
+  const int flags = tc.flags;
   TileLoads T;
-  issue_tile<G8>(P, flags, coff, soff, lane, T);
+  issue_tile<G8>(P, flags, tc.coff, tc.soff, lane, T);
 
   // K rows into this wavefront's LDS rows (row-major); a wavefront's LDS accesses complete in order, so these
   // stores land after the previous tile's V reads
@@ -303,6 +316,12 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
     c_end = c_begin + kCols < lim ? c_begin + kCols : lim;
   }
 
+  const int64_t req = load_idx(A.req_indices, A.req64, b);
+  const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
+  // decode: the wavefront's one tile is resolved first, so that its chain of dependent loads runs beside the Q copy
+  TileCols tc0{};
+  const bool has_tile = !ROWS && c_begin + kRows * wave < c_end;
+  if (has_tile) tc0 = resolve_tile<KIND, G8>(A, c_begin + kRows * wave, c_end, idx_row, L, req, h, lane);
   // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
 #pragma unroll
   for (int i = threadIdx.x; i < kHeads * kD / 8; i += 64 * kWaves) {
@@ -311,8 +330,6 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
     if (hq < gs) w = *reinterpret_cast<const uint4*>(A.q + qrow * A.sq_n + (int64_t)(h * gs + hq) * A.sq_h + 8 * ch);
     *reinterpret_cast<uint4*>(&qs[hq * kKPitch + 8 * ch]) = w;
   }
-  const int64_t req = load_idx(A.req_indices, A.req64, b);
-  const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
   PoolRsrc P;
   {
     const uint32_t n8 = A.rows8 * (uint32_t)H * kD, n4 = A.rows4 * (uint32_t)H * (kD / 2);
@@ -349,12 +366,12 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
 #pragma unroll
   for (int n = 0; n < 16; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
   if constexpr (ROWS) {
-    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols)
-      attend_tile<KIND, G8>(A, P, qs, kv[wave], c0, c_end, idx_row, L, req, h, lane, smk, smv, m_run, l_run, o);
+    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
+      const TileCols tc = resolve_tile<KIND, G8>(A, c0, c_end, idx_row, L, req, h, lane);
+      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o);
+    }
   } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads
-    if (c_begin + kRows * wave < c_end)
-      attend_tile<KIND, G8>(A, P, qs, kv[wave], c_begin + kRows * wave, c_end, idx_row, L, req, h, lane, smk, smv,
-                            m_run, l_run, o);
+    if (has_tile) attend_tile<KIND, G8>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o);
   }
 
   // merge the 4 wavefronts through LDS, 8 q heads per pass: wavefront w stores the O rows of the pass's heads and
