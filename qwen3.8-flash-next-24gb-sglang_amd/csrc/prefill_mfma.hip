@@ -8,7 +8,7 @@
 // Work item = (sequence, KV head, tile of queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
 // first.  A wavefront owns 16 query rows = 16 / gs queries x the gs q heads of the KV head (gs <= 16; rows beyond
 // 16 / gs * gs idle).  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as bf16
-// (threads 0-255 the K tile row-major, threads 256-511 the V tile transposed), with the next tile's codes already
+// (each thread 16 channels of a K row and 8 channels of two V rows, the V rows transposed), with the next tile's codes already
 // loaded into registers during the matrix work on the current one; the eight wavefronts then reuse it for their
 // 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
 // docs/KV_PAGED_PREFIX_PLAN.md:188-191).
@@ -120,30 +120,32 @@ struct Tier {
   int H, h;
 };
 
-// Raw K of one key row, channels 32 dc .. 32 dc + 31: INT4 (a, s4) or INT8 (b, c, s8); bf16 source: a, b, c, d.
+// Raw K of one key row, channels 16 dc .. 16 dc + 15: INT4 (a4, s4) or INT8 (b, s8); bf16 source: a, b.
 struct RawK {
-  uint4 a, b, c, d;
+  uint4 a, b;
+  uint2 a4;
   uint32_t s4, s8;
   int hot;
 };
-// Raw V of two key rows, channels 16 db .. 16 db + 15 each: INT4 (c4, s4) or INT8 (a, s8); bf16 source: a, bb.
+// Raw V of two key rows, channels 8 db .. 8 db + 7 each: INT4 (c4, s4) or INT8 (a8, s8); bf16 source: a.
 struct RawV {
-  uint4 a[2], bb[2];
-  uint2 c4[2];
+  uint4 a[2];
+  uint2 a8[2];
+  uint32_t c4[2];
   uint32_t s4[2], s8[2];
   int hot[2];
 };
+
+KVT_DEV uint32_t ld32(Rsrc r, uint32_t off) { return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0); }
 
 template <int G8, bool BF16>
 KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int p, int dc) {
   RawK x;
   p = min(p, T.key_end - 1);   // keys past the end: valid rows, masked in the scores
   if constexpr (BF16) {
-    const uint32_t off = (uint32_t)(p * T.kb_n + T.h * T.kb_h + 32 * dc) * 2u;
+    const uint32_t off = (uint32_t)(p * T.kb_n + T.h * T.kb_h + 16 * dc) * 2u;
     x.a = ld128(T.kb, off);
     x.b = ld128(T.kb, off + 16);
-    x.c = ld128(T.kb, off + 32);
-    x.d = ld128(T.kb, off + 48);
     x.hot = 2;
   } else {
     constexpr int NG8 = kD / G8;
@@ -151,11 +153,10 @@ KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int p, int dc) {
     const int pg = hot ? 0 : min(p >> 6, kMaxLdsPages - 1);
     const uint32_t rh4 = ((uint32_t)lpages[pg] * kPage + (uint32_t)(p & (kPage - 1))) * T.H + T.h;
     const uint32_t rh8 = (uint32_t)(p & T.rmask) * T.H + T.h;
-    x.a = ld128(T.k4, hot ? kOOB : rh4 * 128u + 16u * dc);
-    x.s4 = ld16(T.ks4, hot ? kOOB : (rh4 * 8u + dc) * 2u);
-    x.b = ld128(T.rk, hot ? rh8 * 256u + 32u * dc : kOOB);
-    x.c = ld128(T.rk, hot ? rh8 * 256u + 32u * dc + 16u : kOOB);
-    x.s8 = ld16(T.rks, hot ? (rh8 * NG8 + (32u * dc) / G8) * 2u : kOOB);
+    x.a4 = ld64(T.k4, hot ? kOOB : rh4 * 128u + 8u * dc);
+    x.s4 = ld16(T.ks4, hot ? kOOB : (rh4 * 8u + dc / 2) * 2u);
+    x.b = ld128(T.rk, hot ? rh8 * 256u + 16u * dc : kOOB);
+    x.s8 = ld16(T.rks, hot ? (rh8 * NG8 + (16u * dc) / G8) * 2u : kOOB);
     x.hot = hot ? 1 : 0;
   }
   return x;
@@ -168,9 +169,8 @@ KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   for (int t = 0; t < 2; ++t) {
     const int p = min(p0 + t, T.key_end - 1);
     if constexpr (BF16) {
-      const uint32_t off = (uint32_t)(p * T.vb_n + T.h * T.vb_h + 16 * db) * 2u;
+      const uint32_t off = (uint32_t)(p * T.vb_n + T.h * T.vb_h + 8 * db) * 2u;
       x.a[t] = ld128(T.vb, off);
-      x.bb[t] = ld128(T.vb, off + 16);
       x.hot[t] = 2;
     } else {
       constexpr int NG8 = kD / G8;
@@ -178,10 +178,10 @@ KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
       const int pg = hot ? 0 : min(p >> 6, kMaxLdsPages - 1);
       const uint32_t rh4 = ((uint32_t)lpages[pg] * kPage + (uint32_t)(p & (kPage - 1))) * T.H + T.h;
       const uint32_t rh8 = (uint32_t)(p & T.rmask) * T.H + T.h;
-      x.c4[t] = ld64(T.v4, hot ? kOOB : rh4 * 128u + 8u * db);
-      x.s4[t] = ld16(T.vs4, hot ? kOOB : (rh4 * 8u + db / 2) * 2u);
-      x.a[t] = ld128(T.rv, hot ? rh8 * 256u + 16u * db : kOOB);
-      x.s8[t] = ld16(T.rvs, hot ? (rh8 * NG8 + (16u * db) / G8) * 2u : kOOB);
+      x.c4[t] = ld32(T.v4, hot ? kOOB : rh4 * 128u + 4u * db);
+      x.s4[t] = ld16(T.vs4, hot ? kOOB : (rh4 * 8u + db / 4) * 2u);
+      x.a8[t] = ld64(T.rv, hot ? rh8 * 256u + 8u * db : kOOB);
+      x.s8[t] = ld16(T.rvs, hot ? (rh8 * NG8 + (8u * db) / G8) * 2u : kOOB);
       x.hot[t] = hot ? 1 : 0;
     }
   }
@@ -224,69 +224,63 @@ KVT_DEV void int8_pairs(uint32_t w, _Float16 s, float c, uint32_t out[2]) {
   out[1] = bf2(mix(e, 1, s, c), mix(o, 1, s, c));
 }
 
-// K row fragment -> LDS (bf16, natural order): channels 32 dc .. 32 dc + 31 of key row `key` (4 chunks).
+// K row fragment -> LDS (bf16, natural order): channels 16 dc .. 16 dc + 15 of key row `key` (2 chunks).
 template <bool BF16>
 KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
-  uint32_t o[16];
+  uint32_t o[8];
   if constexpr (BF16) {
-    const uint32_t w[16] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w,
-                            x.c.x, x.c.y, x.c.z, x.c.w, x.d.x, x.d.y, x.d.z, x.d.w};
+    const uint32_t w[8] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[i] = w[i];
+    for (int i = 0; i < 8; ++i) o[i] = w[i];
   } else if (x.hot) {
-    const uint32_t w[8] = {x.b.x, x.b.y, x.b.z, x.b.w, x.c.x, x.c.y, x.c.z, x.c.w};
+    const uint32_t w[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
     const _Float16 s = half_of(x.s8);
     const float c = -1152.0f * (float)s;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) int8_pairs(w[i], s, c, o + 2 * i);
+    for (int i = 0; i < 4; ++i) int8_pairs(w[i], s, c, o + 2 * i);
   } else {
-    const uint32_t w[4] = {x.a.x, x.a.y, x.a.z, x.a.w};
     const _Float16 s = half_of(x.s4);
     const float c = -1032.0f * (float)s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) int4_pairs(w[i], s, c, o + 4 * i);
+    int4_pairs(x.a4.x, s, c, o);
+    int4_pairs(x.a4.y, s, c, o + 4);
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    *reinterpret_cast<uint4*>(row + k_chunk(key, 4 * dc + i)) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2],
+  for (int i = 0; i < 2; ++i)
+    *reinterpret_cast<uint4*>(row + k_chunk(key, 2 * dc + i)) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2],
                                                                           o[4 * i + 3]);
 }
 
-// 16 channels of one V row -> 8 bf16 pairs (natural order).
+// 8 channels of one V row -> 4 bf16 pairs (natural order).
 template <bool BF16>
-KVT_DEV void v_row16(const RawV& x, int t, uint32_t o[8]) {
+KVT_DEV void v_row8(const RawV& x, int t, uint32_t o[4]) {
   if constexpr (BF16) {
-    const uint32_t c[8] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w, x.bb[t].x, x.bb[t].y, x.bb[t].z, x.bb[t].w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = c[i];
+    o[0] = x.a[t].x, o[1] = x.a[t].y, o[2] = x.a[t].z, o[3] = x.a[t].w;
   } else if (x.hot[t]) {
-    const uint32_t c[4] = {x.a[t].x, x.a[t].y, x.a[t].z, x.a[t].w};
     const _Float16 s = half_of(x.s8[t]);
     const float cc = -1152.0f * (float)s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) int8_pairs(c[i], s, cc, o + 2 * i);
+    int8_pairs(x.a8[t].x, s, cc, o);
+    int8_pairs(x.a8[t].y, s, cc, o + 2);
   } else {
     const _Float16 s = half_of(x.s4[t]);
     const float cc = -1032.0f * (float)s;
-    int4_pairs(x.c4[t].x, s, cc, o);
-    int4_pairs(x.c4[t].y, s, cc, o + 4);
+    int4_pairs(x.c4[t], s, cc, o);
   }
 }
 
-// Two keys x 16 channels -> V^T rows (dim 16 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
+// Two keys x 8 channels -> V^T rows (dim 8 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
 template <bool BF16>
 KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
-  uint32_t a[8], b[8];
-  v_row16<BF16>(x, 0, a);
-  v_row16<BF16>(x, 1, b);
+  uint32_t a[4], b[4];
+  v_row8<BF16>(x, 0, a);
+  v_row8<BF16>(x, 1, b);
   // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
   const int q = (tp >> 1) & 3;
   const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < 4; ++i) {
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
     const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
-    const int d0 = 16 * db + 2 * i, d1 = d0 + 1;
+    const int d0 = 8 * db + 2 * i, d1 = d0 + 1;
     *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d0, q) + inner) = lo;
     *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d1, q) + inner) = hi;
   }
@@ -378,23 +372,19 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   for (int c = 0; c < 16; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // dequant roles: threads 0-255 the K tile (row tk = t >> 3, channels 32 (t & 7) ..), threads 256-511 the V tile
-  // (keys 2 tp, 2 tp + 1 with tp = t & 15, channels 16 db .. with db = t >> 4), t = tid mod 256
-  const bool krole = tid < 256;
-  const int t8 = tid & 255;
-  const int tk = t8 >> 3, dc = t8 & 7;
-  const int tp = t8 & 15, db = t8 >> 4;
+  // dequantization, the same for every thread t: 16 channels (16 (t & 15) ..) of K row t >> 4, and 8 channels
+  // (8 (t >> 4) ..) of V rows 2 (t & 15), 2 (t & 15) + 1
+  const int tk = tid >> 4, dc = tid & 15;
+  const int tp = tid & 15, db = tid >> 4;
+  const bool early = wave >= 4;   // the second wavefront of each SIMD dequantizes before its score products
   const int ntiles = (int)((key_end + kT - 1) / kT);
-  RawK rk_next;
-  RawV rv_next;
-  if (krole) {
-    rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-    store_k<BF16>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
-    if (ntiles > 1) rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
-  } else {
-    rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
-    store_v<BF16>(rv_next, lds.vt[0], db, tp);
-    if (ntiles > 1) rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
+  RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
+  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
+  store_k<BF16>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
+  store_v<BF16>(rv_next, lds.vt[0], db, tp);
+  if (ntiles > 1) {
+    rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
+    rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
   }
   __syncthreads();
   const int qmin = (int)(q_pos0 + qt0);   // the block's first query position: tiles below it need no causal mask
@@ -405,13 +395,17 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     const bool more = it + 1 < ntiles;
     const int t2 = t0 + 2 * kT;
     // Tile it + 1 goes into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go out.
-    // The V-role wavefronts do this before their score products and the K-role ones after: each SIMD runs one
-    // wavefront of each role, so one's dequantization (VALU) meets the other's products (matrix cores).  Issue
-    // priority: matrix phases at 0, VALU phases at 1.
+    // Wavefronts 4-7 do this before their score products and 0-3 after: each SIMD runs one of each, so one's
+    // dequantization (VALU) meets the other's products (matrix cores).  Issue priority: matrix phases at 0, VALU
+    // phases at 1.
     __builtin_amdgcn_s_setprio(1);
-    if (!krole && more) {
+    if (early && more) {
+      store_k<BF16>(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
       store_v<BF16>(rv_next, lds.vt[cb ^ 1], db, tp);
-      if (it + 2 < ntiles) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+      if (it + 2 < ntiles) {
+        rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
+        rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+      }
     }
     // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16 (unscaled)
     __builtin_amdgcn_s_setprio(0);
@@ -429,9 +423,13 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       for (int r = 0; r < 4; ++r) s[nt][r] = d0[r];
     }
     __builtin_amdgcn_s_setprio(1);
-    if (krole && more) {
+    if (!early && more) {
       store_k<BF16>(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
-      if (it + 2 < ntiles) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
+      store_v<BF16>(rv_next, lds.vt[cb ^ 1], db, tp);
+      if (it + 2 < ntiles) {
+        rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
+        rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+      }
     }
     // causal / end mask, only on the tiles that reach the block's first query or the key end
     if (t0 + kT > qmin || t0 + kT > kend) {
