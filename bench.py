@@ -11,7 +11,8 @@ us/token over all layers, the roofline of the decode kernel (live HIP-event timi
 oracle timed on a bounded sample (one layer at the full context) as the baseline; its output also checks layer 0
 of the timed path against the oracle ("parity").  The same line carries "configs": compact figures of the other
 configurations (chunked prefill, quantize-append, decode with append, ragged decode, top-k sparse decode at 16 / 2
-and 24 / 2 heads), measured after the headline; --no-sub-configs leaves them out.
+and 24 / 2 heads, dense decode over the slot-indexed pool), measured after the headline; --no-sub-configs leaves them
+out.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl mfma|ref]
 """
@@ -525,6 +526,68 @@ def sparse_workload(args) -> dict:
     }
 
 
+def slots_workload(args) -> dict:
+    """Dense decode over the slot-indexed tiered pool (the layout the reference's backend reads): 4 requests of
+    65,536 positions on randomly permuted slots, 1 layer, INT8-G64 ring of 8,192 rows whose owner table names one slot
+    per row (3 % of the positions hot), every position attended.  Times one HIP graph of decode_attn_slots through the
+    matrix cores (the fused sparse decode with every position selected, + the combine) and, for scale, the scalar
+    reference-precision kernel.  Byte model per position and KV head: the K and V rows of its tier (INT8 256 B + 8 B
+    of scales, or INT4 128 B + 16 B, per tensor) plus its req_to_token slot and owner probe.  Synthetic random codes
+    and scales."""
+    import kvtier  # noqa: F401
+    from kvtier.kvt import decode_attn_slots
+    B, CTX, R = 4, 65_536, 8192
+    slots = B * CTX
+    g = torch.Generator(device="cuda").manual_seed(51)
+    gc = torch.Generator().manual_seed(51)
+    k4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, device="cuda", generator=g)
+    v4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, device="cuda", generator=g)
+    ks4 = (0.05 + 0.3 * torch.rand(slots, H, D // 32, device="cuda", generator=g)).half()
+    vs4 = (0.05 + 0.3 * torch.rand(slots, H, D // 32, device="cuda", generator=g)).half()
+    rk = torch.randint(-127, 128, (R, H, D), dtype=torch.int8, device="cuda", generator=g)
+    rv = torch.randint(-127, 128, (R, H, D), dtype=torch.int8, device="cuda", generator=g)
+    rks = (0.002 + 0.02 * torch.rand(R, H, D // 64, device="cuda", generator=g)).half()
+    rvs = (0.002 + 0.02 * torch.rand(R, H, D // 64, device="cuda", generator=g)).half()
+    owner = (torch.arange(R, dtype=torch.int64) + R * torch.randint(0, slots // R, (R,), generator=gc)).to(torch.int32)
+    r2t = torch.randperm(slots, generator=gc).to(torch.int32).reshape(B, CTX)
+    hot = (owner.long()[r2t.long() & (R - 1)] == r2t.long())
+    n_hot = int(hot.sum())
+    n_cold = hot.numel() - n_hot
+    owner, r2t = owner.to("cuda"), r2t.to("cuda")
+    req_idx = torch.arange(B, dtype=torch.int64, device="cuda")
+    seq = torch.full((B,), CTX, dtype=torch.int32, device="cuda")
+    q = (torch.randn(B, HQ, D, device="cuda", generator=g) / 16).to(torch.bfloat16)
+    bytes_step = H * (n_hot * 2 * (D + 2 * (D // 64)) + n_cold * 2 * (D // 2 + 2 * (D // 32))) + 8 * hot.numel()
+    ws = {}
+    outs = {}
+
+    def run(impl):
+        def fn():
+            outs[impl] = decode_attn_slots(q, seq, r2t, req_idx, k4, v4, ks4, vs4, rk, rv, rks, rvs, owner, R - 1,
+                                           impl=impl, max_len=CTX, workspace=ws if impl == "mfma" else None)
+        return fn
+
+    t_mfma = _graph_time(run("mfma"), args.warmup, args.steps)
+    t_ref = _graph_time(run("ref"), 1, max(1, args.steps // 4))
+    err = float((outs["mfma"] - outs["ref"]).abs().max())
+    gbps = bytes_step / t_mfma / 1e9
+    return {
+        "metric": "dense decode over the slot-indexed tiered pool (4 x 65,536 positions, 1 layer): us per step",
+        "value": round(t_mfma * 1e6, 1), "unit": "us", "higher_is_better": False, "steps": max(1, args.steps),
+        "warmup": args.warmup, "dtype": "bf16-mfma/f32", "data": "synthetic",
+        "config": {"workload": "4 requests x 65,536 positions on random slots, 1 layer, 16 Q / 2 KV heads, D 256, "
+                               "tiered pool (INT8-G64 ring of 8,192 rows + INT4-G32)",
+                   "hot_fraction": round(n_hot / hot.numel(), 4)},
+        "scalar_kernel_us_per_step": round(t_ref * 1e6, 1),
+        "max_abs_vs_scalar_kernel": err,
+        "kv_bytes_per_step": bytes_step,
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
+                     "kernel": "sparse_decode over every position + combine"},
+        "cpu_baseline": None,
+    }
+
+
 def lazy_workload(args) -> dict:
     """Lazy backing of the tiered slot pool on HIP virtual memory at the full context: 262,144 slots x 12 layers
     (2 KV heads, D 256; INT8 ring of 8,192 rows eagerly allocated).  Times, host wall with the device synchronized:
@@ -790,8 +853,8 @@ def decode_steps_workload(args, ragged: bool) -> dict:
 def sub_configs(args) -> dict:
     """Compact figures of the other configurations, measured in the same process after the headline (whose cache
     is freed first): chunked prefill of a 10,001-token prompt, the 8,192-token quantize-append with eviction, decode
-    with append at a 10,001-token context, ragged 8-sequence decode, and the top-k sparse decode at 16 / 2 and
-    24 / 2 heads.  Each runs without its CPU baseline; a failure is reported in place of its figures."""
+    with append at a 10,001-token context, ragged 8-sequence decode, the top-k sparse decode at 16 / 2 and 24 / 2
+    heads, and the dense decode over the slot-indexed pool.  Each runs without its CPU baseline; a failure is reported in place of its figures."""
     sub = argparse.Namespace(**vars(args))
     sub.no_cpu_baseline, sub.steps, sub.warmup = True, 5, 1
     res = {}
@@ -823,6 +886,9 @@ def sub_configs(args) -> dict:
     for hq in (16, 24):
         run(f"sparse_topk2051_{hq}q", lambda a, hq=hq: sparse_workload(argparse.Namespace(**dict(vars(a), hq=hq))),
             pick_sparse)
+    run("slots_dense_4x65k", slots_workload,
+        lambda r: {"us_per_step": r["value"], "GBps": r["roofline"]["achieved"], "hbm_frac": r["roofline"]["frac"],
+                   "scalar_kernel_us_per_step": r["scalar_kernel_us_per_step"]})
     return res
 
 
@@ -835,7 +901,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fused-combine", action="store_true",
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
-    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "lazy"],
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "slots", "lazy"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--hq", type=int, default=HQ, help="query heads of the sparse workload (2 KV heads)")
     ap.add_argument("--no-sub-configs", action="store_true",
@@ -857,7 +923,7 @@ def main():
     if args.workload != "decode262k":
         fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
               "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload,
-              "sparse": sparse_workload, "lazy": lazy_workload}[args.workload]
+              "sparse": sparse_workload, "slots": slots_workload, "lazy": lazy_workload}[args.workload]
         line = fn(args)
         line["n_gpus"] = 1
         print(json.dumps(line))

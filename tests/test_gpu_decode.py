@@ -298,12 +298,61 @@ def test_decode_slot_rings_config0(kvt_pkg):
     for i in range(9):
         assert torch.equal(got[i], e[i]), i
     rtt = torch.arange(N, dtype=torch.int32, device=dev)[None]
-    out = decode_attn_slots(q.to(dev), torch.tensor([N], dtype=torch.int32, device=dev), rtt,
-                            torch.zeros(1, dtype=torch.int64, device=dev), k4, v4, ks4, vs4, rk, rv, rks, rvs, owner,
-                            R - 1).cpu()
     kk, vv = ref.dequant_slots_tiered(torch.arange(N), *e, R - 1, group8=256)
     exp = ref.attention_rows(q[0], kk, vv, SCALE)
-    assert float((out[0] - exp).abs().max()) < 2e-5
+    for impl, tol, mtol in (("ref", 2e-5, 2e-5), ("mfma", 2e-3, 1e-3)):
+        out = decode_attn_slots(q.to(dev), torch.tensor([N], dtype=torch.int32, device=dev), rtt,
+                                torch.zeros(1, dtype=torch.int64, device=dev), k4, v4, ks4, vs4, rk, rv, rks, rvs,
+                                owner, R - 1, impl=impl).cpu()
+        err = (out[0] - exp).abs()
+        assert float(err.max()) < tol and float(err.mean()) < mtol, (impl, float(err.max()))
+
+
+@pytest.mark.parametrize("hq", [16, 24])
+def test_decode_slots_mfma_ragged(kvt_pkg, hq):
+    """Dense decode over the slot-indexed tiered pool through the matrix cores: 3 requests (5,000 / 1,300 / 64
+    positions) on randomly permuted slots of one pool, ring of 1,024 rows with owners from the dual write (the ring
+    has wrapped: most positions are INT4 rows, the newest are ring rows), G64 ring scales, smoothing factors,
+    against the oracle's gathered rows and fp32 attention."""
+    from kvtier import sparse_attn as sa
+    from kvtier.kvt import decode_attn_slots
+    gen = torch.Generator().manual_seed(61)
+    lens, R, slots = [5000, 1300, 64], 1024, 8192
+    och = ref.outlier_channels(H, D, 8, gen)
+    perm = torch.randperm(slots, generator=gen).to(torch.int32)
+    r2t = torch.full((4, 5100), -7, dtype=torch.int32)
+    req_idx = torch.tensor([2, 0, 3], dtype=torch.int64)
+    a = 0
+    for b, L in enumerate(lens):
+        r2t[int(req_idx[b]), :L] = perm[a:a + L]
+        a += L
+    k4 = torch.zeros(slots, H, D // 2, dtype=torch.uint8, device=dev); v4 = torch.zeros_like(k4)
+    ks4 = torch.zeros(slots, H, 8, dtype=torch.float16, device=dev); vs4 = torch.zeros_like(ks4)
+    rk = torch.zeros(R, H, D, dtype=torch.int8, device=dev); rv = torch.zeros_like(rk)
+    rks = torch.zeros(R, H, 4, dtype=torch.float16, device=dev); rvs = torch.zeros_like(rks)
+    owner = torch.full((R,), -1, dtype=torch.int32, device=dev)
+    sm = (0.5 + torch.rand(H, D, generator=gen)).half()
+    smi = (1.0 / sm.float()).half()
+    xs = []
+    for b, L in enumerate(lens):   # the dual write in position order, request by request
+        xk, xv = ref.make_kv(L, H, D, gen, och)
+        locs = r2t[int(req_idx[b]), :L].long()
+        for c0 in range(0, L, 512):
+            c1 = min(L, c0 + 512)
+            sa.quant_store_kv_tiered(xk[c0:c1].to(dev), xv[c0:c1].to(dev), locs[c0:c1].to(dev), k4, v4, ks4, vs4, rk,
+                                     rv, rks, rvs, owner, smi.to(dev), smi.to(dev), R - 1)
+    torch.cuda.synchronize()
+    q = ref.make_q(hq, D, gen, n=3)
+    seq = torch.tensor(lens, dtype=torch.int32)
+    out = decode_attn_slots(q.to(dev), seq.to(dev), r2t.to(dev), req_idx.to(dev), k4, v4, ks4, vs4, rk, rv, rks, rvs,
+                            owner, R - 1, sm_k=sm.to(dev), sm_v=sm.to(dev)).cpu()
+    pools = [t.cpu() for t in (k4, v4, ks4, vs4, rk, rv, rks, rvs, owner)]
+    for b, L in enumerate(lens):
+        kk, vv = ref.dequant_slots_tiered(r2t[int(req_idx[b]), :L].long(), *pools, R - 1, group8=64, sm_k=sm,
+                                          sm_v=sm)
+        exp = ref.attention_rows(q[b], kk, vv, SCALE)
+        err = (out[b] - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (hq, b, float(err.max()), float(err.mean()))
 
 
 @pytest.mark.parametrize("deterministic", [True, False])
