@@ -224,25 +224,45 @@ KVT_DEV void int8_pairs(uint32_t w, _Float16 s, float c, uint32_t out[2]) {
   out[1] = bf2(mix(e, 1, s, c), mix(o, 1, s, c));
 }
 
+// Tier of a tile's dequantization: every key INT4, every key INT8, per key (the tile straddles hot_start), the bf16
+// source, or no tile (kTierNone).
+enum { kTierInt4 = 0, kTierInt8 = 1, kTierMixed = 2, kTierBf16 = 3, kTierNone = 4 };
+template <int N>
+struct TierTag {
+  static constexpr int value = N;
+};
+
+KVT_DEV void k_int8(const RawK& x, uint32_t o[8]) {
+  const uint32_t w[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
+  const _Float16 s = half_of(x.s8);
+  const float c = -1152.0f * (float)s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) int8_pairs(w[i], s, c, o + 2 * i);
+}
+KVT_DEV void k_int4(const RawK& x, uint32_t o[8]) {
+  const _Float16 s = half_of(x.s4);
+  const float c = -1032.0f * (float)s;
+  int4_pairs(x.a4.x, s, c, o);
+  int4_pairs(x.a4.y, s, c, o + 4);
+}
+
 // K row fragment -> LDS (bf16, natural order): channels 16 dc .. 16 dc + 15 of key row `key` (2 chunks).
-template <bool BF16>
+template <int TIER>
 KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
   uint32_t o[8];
-  if constexpr (BF16) {
+  if constexpr (TIER == kTierBf16) {
     const uint32_t w[8] = {x.a.x, x.a.y, x.a.z, x.a.w, x.b.x, x.b.y, x.b.z, x.b.w};
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = w[i];
-  } else if (x.hot) {
-    const uint32_t w[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
-    const _Float16 s = half_of(x.s8);
-    const float c = -1152.0f * (float)s;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) int8_pairs(w[i], s, c, o + 2 * i);
+  } else if constexpr (TIER == kTierInt8) {
+    k_int8(x, o);
+  } else if constexpr (TIER == kTierInt4) {
+    k_int4(x, o);
   } else {
-    const _Float16 s = half_of(x.s4);
-    const float c = -1032.0f * (float)s;
-    int4_pairs(x.a4.x, s, c, o);
-    int4_pairs(x.a4.y, s, c, o + 4);
+    if (x.hot)
+      k_int8(x, o);
+    else
+      k_int4(x, o);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -250,34 +270,124 @@ KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
                                                                           o[4 * i + 3]);
 }
 
+KVT_DEV void v_int8(const RawV& x, int t, uint32_t o[4]) {
+  const _Float16 s = half_of(x.s8[t]);
+  const float cc = -1152.0f * (float)s;
+  int8_pairs(x.a8[t].x, s, cc, o);
+  int8_pairs(x.a8[t].y, s, cc, o + 2);
+}
+KVT_DEV void v_int4(const RawV& x, int t, uint32_t o[4]) {
+  const _Float16 s = half_of(x.s4[t]);
+  const float cc = -1032.0f * (float)s;
+  int4_pairs(x.c4[t], s, cc, o);
+}
+
 // 8 channels of one V row -> 4 bf16 pairs (natural order).
-template <bool BF16>
+template <int TIER>
 KVT_DEV void v_row8(const RawV& x, int t, uint32_t o[4]) {
-  if constexpr (BF16) {
+  if constexpr (TIER == kTierBf16) {
     o[0] = x.a[t].x, o[1] = x.a[t].y, o[2] = x.a[t].z, o[3] = x.a[t].w;
-  } else if (x.hot[t]) {
-    const _Float16 s = half_of(x.s8[t]);
-    const float cc = -1152.0f * (float)s;
-    int8_pairs(x.a8[t].x, s, cc, o);
-    int8_pairs(x.a8[t].y, s, cc, o + 2);
+  } else if constexpr (TIER == kTierInt8) {
+    v_int8(x, t, o);
+  } else if constexpr (TIER == kTierInt4) {
+    v_int4(x, t, o);
   } else {
-    const _Float16 s = half_of(x.s4[t]);
-    const float cc = -1032.0f * (float)s;
-    int4_pairs(x.c4[t], s, cc, o);
+    if (x.hot[t])
+      v_int8(x, t, o);
+    else
+      v_int4(x, t, o);
   }
 }
 
 // Two keys x 8 channels -> V^T rows (dim 8 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
-template <bool BF16>
+template <int TIER>
 KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
   uint32_t a[4], b[4];
-  v_row8<BF16>(x, 0, a);
-  v_row8<BF16>(x, 1, b);
+  v_row8<TIER>(x, 0, a);
+  v_row8<TIER>(x, 1, b);
   // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
   const int q = (tp >> 1) & 3;
   const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
+    const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
+    const int d0 = 8 * db + 2 * i, d1 = d0 + 1;
+    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d0, q) + inner) = lo;
+    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d1, q) + inner) = hi;
+  }
+}
+
+// Tile it + 1's rows are converted in pieces, one per matrix step of tile it (the loops below fence every step with
+// sched_barrier, so each piece issues between two groups of products instead of in one run of vector instructions).
+// K: 8 steps beside the score products; the rows go to LDS in the two steps after the conversion, and the codes of
+// tile it + 2 are fetched at step kFetchK.  V: 16 steps beside P.V, likewise with kFetchV.
+template <int TIER>
+constexpr int kConvK = TIER == kTierInt8 ? 4 : TIER == kTierInt4 ? 2 : 1;   // conversion steps of a K fragment
+template <int TIER>
+constexpr int kFetchK = kConvK<TIER> + 2;
+template <int TIER>
+constexpr int kConvV = TIER == kTierInt8 ? 4 : TIER == kTierInt4 ? 2 : 1;
+template <int TIER>
+constexpr int kFetchV = kConvV<TIER> + 5;
+
+KVT_DEV uint32_t word_of(const uint4& w, int j) { return j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w; }
+
+template <int TIER>
+KVT_DEV void k_step(int j, const RawK& x, uint32_t o[8], uint8_t* row, int key, int dc) {
+  if constexpr (TIER == kTierInt8) {
+    if (j < 4) {
+      const _Float16 s = half_of(x.s8);
+      int8_pairs(word_of(x.b, j), s, -1152.0f * (float)s, o + 2 * j);
+    }
+  } else if constexpr (TIER == kTierInt4) {
+    if (j < 2) {
+      const _Float16 s = half_of(x.s4);
+      int4_pairs(j == 0 ? x.a4.x : x.a4.y, s, -1032.0f * (float)s, o + 4 * j);
+    }
+  } else if constexpr (TIER == kTierBf16) {
+    if (j == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = word_of(x.a, i), o[4 + i] = word_of(x.b, i);
+    }
+  } else {
+    if (j == 0) {
+      if (x.hot)
+        k_int8(x, o);
+      else
+        k_int4(x, o);
+    }
+  }
+  constexpr int w0 = kConvK<TIER>;
+  if (j == w0 || j == w0 + 1) {
+    const int i = j - w0;
+    *reinterpret_cast<uint4*>(row + k_chunk(key, 2 * dc + i)) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2],
+                                                                          o[4 * i + 3]);
+  }
+}
+
+template <int TIER>
+KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t* vt, int db, int tp) {
+  if constexpr (TIER == kTierInt8) {
+    if (j < 4) {
+      const int t = j >> 1, hw = j & 1;
+      const _Float16 s = half_of(x.s8[t]);
+      int8_pairs(hw ? x.a8[t].y : x.a8[t].x, s, -1152.0f * (float)s, (t ? b : a) + 2 * hw);
+    }
+  } else if constexpr (TIER == kTierInt4) {
+    if (j < 2) v_int4(x, j, j ? b : a);
+  } else {
+    if (j == 0) {
+      v_row8<TIER>(x, 0, a);
+      v_row8<TIER>(x, 1, b);
+    }
+  }
+  constexpr int w0 = kConvV<TIER>;
+  if (j >= w0 && j < w0 + 4) {
+    // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
+    const int i = j - w0;
+    const int q = (tp >> 1) & 3;
+    const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
     const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
     const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
     const int d0 = 8 * db + 2 * i, d1 = d0 + 1;
@@ -376,60 +486,70 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   // (8 (t >> 4) ..) of V rows 2 (t & 15), 2 (t & 15) + 1
   const int tk = tid >> 4, dc = tid & 15;
   const int tp = tid & 15, db = tid >> 4;
-  const bool early = wave >= 4;   // the second wavefront of each SIMD dequantizes before its score products
   const int ntiles = (int)((key_end + kT - 1) / kT);
+  constexpr int kFirst = BF16 ? kTierBf16 : kTierMixed;
   RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
   RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
-  store_k<BF16>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
-  store_v<BF16>(rv_next, lds.vt[0], db, tp);
-  if (ntiles > 1) {
-    rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);
-    rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
-  }
+  store_k<kFirst>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
+  store_v<kFirst>(rv_next, lds.vt[0], db, tp);
+  rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);   // (past the end it rereads the last key)
+  rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
   __syncthreads();
   const int qmin = (int)(q_pos0 + qt0);   // the block's first query position: tiles below it need no causal mask
   const int qp = (int)qpos, kend = (int)key_end;
-  for (int it = 0; it < ntiles; ++it) {
+  // One iteration per key tile it.  Tile it + 1's rows (codes loaded during tile it - 1) go into the other buffer
+  // beside this tile's products, a piece per matrix step: its K rows beside the score products, its V rows beside
+  // P.V; tile it + 2's codes go out during the same steps.  The body is specialized on the tier of tile it + 1;
+  // tiers change monotonically along the keys (INT4 tiles, at most one tile that straddles hot_start, INT8 tiles),
+  // so the iterations run as consecutive loops with one code path each.
+  // LDS read offsets of this lane's MFMA operands, split into a per-lane part (computed once) and a constant:
+  // K chunk 4 st + kb of key row n16 sits at 256 (st >> 2) + koff[st & 3] (the swizzle n16 only touches the low
+  // four chunk bits), V^T row 16 c + n16, k-group kb at 1024 c + voff[c & 3] (row and chunk swizzles see only c & 3)
+  uint32_t koff[4], voff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    koff[j] = k_chunk(n16, 4 * j + kb);
+    voff[j] = vt_row_chunk(16 * j + n16, kb) - 1024u * (uint32_t)j;
+  }
+  int it = 0;
+  auto body = [&](auto tag) {
+    constexpr int TIER = decltype(tag)::value;
     const int t0 = it * kT;
     const int cb = it & 1;
-    const bool more = it + 1 < ntiles;
     const int t2 = t0 + 2 * kT;
-    // Tile it + 1 goes into the other buffer (its codes arrived during tile it - 1), then tile it + 2's codes go out.
-    // Wavefronts 4-7 do this before their score products and 0-3 after: each SIMD runs one of each, so one's
-    // dequantization (VALU) meets the other's products (matrix cores).  Issue priority: matrix phases at 0, VALU
-    // phases at 1.
-    __builtin_amdgcn_s_setprio(1);
-    if (early && more) {
-      store_k<BF16>(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
-      store_v<BF16>(rv_next, lds.vt[cb ^ 1], db, tp);
-      if (it + 2 < ntiles) {
-        rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
-        rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
-      }
-    }
-    // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16 (unscaled)
-    __builtin_amdgcn_s_setprio(0);
+    // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16 (unscaled).  Step st: the two
+    // products of k-slice st, the K operands of step st + 2 read from LDS, one piece of tile it + 1's K rows.
     float s[2][4];
+    {
+      constexpr bool kDq = TIER != kTierNone;
+      const uint8_t* kbuf = lds.k[cb];
+      uint8_t* krow_next = lds.k[cb ^ 1] + tk * kKPitch;
+      uint32_t ko[8];
+      bf8 kf[8][2];
+      f4 d[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      auto kread = [&](int st) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f4 d0 = {0.f, 0.f, 0.f, 0.f};
-      const uint8_t* krow = lds.k[cb] + (16 * nt + n16) * kKPitch;
+        for (int nt = 0; nt < 2; ++nt)
+          kf[st][nt] = __builtin_bit_cast(
+              bf8, *reinterpret_cast<const u4v*>(kbuf + (16 * nt + n16) * kKPitch + koff[st & 3] + 256 * (st >> 2)));
+      };
+      kread(0);
+      kread(1);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const bf8 a = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(krow + k_chunk(n16, 4 * st + kb)));
-        d0 = mfma(a, qop[st], d0);
+        if (st + 2 < 8) kread(st + 2);
+        d[0] = mfma(kf[st][0], qop[st], d[0]);
+        d[1] = mfma(kf[st][1], qop[st], d[1]);
+        if constexpr (kDq) {
+          k_step<TIER>(st, rk_next, ko, krow_next, tk, dc);
+          if (st == kFetchK<TIER>) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);   // (clamped at the end)
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[nt][r] = d0[r];
-    }
-    __builtin_amdgcn_s_setprio(1);
-    if (!early && more) {
-      store_k<BF16>(rk_next, lds.k[cb ^ 1] + tk * kKPitch, tk, dc);
-      store_v<BF16>(rv_next, lds.vt[cb ^ 1], db, tp);
-      if (it + 2 < ntiles) {
-        rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);
-        rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
-      }
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[nt][r] = d[nt][r];
     }
     // causal / end mask, only on the tiles that reach the block's first query or the key end
     if (t0 + kT > qmin || t0 + kT > kend) {
@@ -486,16 +606,46 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       pa = __builtin_bit_cast(bf8, u4v{hw[0], hw[1], hw[2], hw[3]});
       pb = __builtin_bit_cast(bf8, u4v{lw[0], lw[1], lw[2], lw[3]});
     }
-    // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read
-    __builtin_amdgcn_s_setprio(0);
+    // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read.
+    // Step c: the high-part product of dims 16 c .., the remainder product of dims 16 (c - 1) .., the V operand of
+    // step c + 2 read from LDS, one piece of tile it + 1's V rows.
+    {
+      constexpr bool kDq = TIER != kTierNone;
+      const uint8_t* vbuf = lds.vt[cb];
+      uint8_t* vt_next = lds.vt[cb ^ 1];
+      uint32_t va[4], vb[4];
+      bf8 vf[16];
+      auto vread = [&](int c) {
+        vf[c] = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(vbuf + voff[c & 3] + 1024 * c));
+      };
+      vread(0);
+      vread(1);
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const bf8 bv = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(lds.vt[cb] + vt_row_chunk(16 * c + n16, kb)));
-      acc[c] = mfma(pb, bv, mfma(pa, bv, acc[c]));
+      for (int c = 0; c < 16; ++c) {
+        if (c + 2 < 16) vread(c + 2);
+        acc[c] = mfma(pa, vf[c], acc[c]);
+        if (c > 0) acc[c - 1] = mfma(pb, vf[c - 1], acc[c - 1]);
+        if constexpr (kDq) {
+          v_step<TIER>(c, rv_next, va, vb, vt_next, db, tp);
+          if (c == kFetchV<TIER>) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      acc[15] = mfma(pb, vf[15], acc[15]);
     }
-    __builtin_amdgcn_s_setprio(1);
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
+    ++it;
+  };
+  const int nd = ntiles - 1;   // iterations that dequantize a tile (tile it + 1)
+  if constexpr (BF16) {
+    while (it < nd) body(TierTag<kTierBf16>{});
+  } else {
+    const int n4 = T.hs / kT;  // tiles entirely below hot_start
+    while (it < min(n4 - 1, nd)) body(TierTag<kTierInt4>{});
+    if ((T.hs & (kT - 1)) != 0 && it == n4 - 1 && it < nd) body(TierTag<kTierMixed>{});
+    while (it < nd) body(TierTag<kTierInt8>{});
   }
+  while (it < ntiles) body(TierTag<kTierNone>{});
 
   // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
   // column n16 of block c = dim 16 c + n16
