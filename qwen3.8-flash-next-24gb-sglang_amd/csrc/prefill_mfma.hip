@@ -188,6 +188,109 @@ KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   return x;
 }
 
+// Fetches of a whole tile t2 .. t2 + 31 whose keys all sit in one tier and before the key end: the row base of the
+// tile is uniform (a scalar offset of the buffer load) and the rest a per-lane constant (FetchLane), so the fetch
+// costs no vector address arithmetic.  Ring rows: R is a power of two >= 32, so (t2 + k) & (R - 1) =
+// (t2 & (R - 1)) + k; pages: the 32 keys of a tile lie on one 64-position page.  A whole-tile fetch fills only its
+// tier's fields (the tile is converted by that tier's loop body); other tiles take the per-key fetch above.  The
+// kind of fetch is a template parameter of the loop body, never a branch inside it: loads issued on different
+// paths that join inside the loop would leave the wait counters unknown, and the body would wait for every load.
+KVT_DEV uint4 ld128s(Rsrc r, uint32_t v, uint32_t s) {
+  const v4i x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)v, (int)s, 0);
+  return make_uint4((uint32_t)x.x, (uint32_t)x.y, (uint32_t)x.z, (uint32_t)x.w);
+}
+KVT_DEV uint2 ld64s(Rsrc r, uint32_t v, uint32_t s) {
+  const v2i x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)v, (int)s, 0);
+  return make_uint2((uint32_t)x.x, (uint32_t)x.y);
+}
+KVT_DEV uint32_t ld32s(Rsrc r, uint32_t v, uint32_t s) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)v, (int)s, 0);
+}
+KVT_DEV uint32_t ld16s(Rsrc r, uint32_t v, uint32_t s) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)v, (int)s, 0);
+}
+
+// Per-lane byte offsets within a tile: K row tk, channels 16 dc; V rows 2 tp (the second row adds one row's stride
+// to the scalar part), channels 8 db.  INT8 codes / scales, INT4 codes / scales; the bf16 source uses k8 and v8.
+struct FetchLane {
+  uint32_t k8, k8s, k4, k4s, v8, v8s, v4, v4s;
+};
+
+template <int G8, bool BF16>
+KVT_DEV FetchLane fetch_lane(const Tier& T, int tk, int dc, int tp, int db) {
+  constexpr uint32_t NG8 = kD / G8;
+  FetchLane F;
+  const uint32_t H = (uint32_t)T.H;
+  if constexpr (BF16) {
+    F.k8 = (uint32_t)(tk * T.kb_n + 16 * dc) * 2u;
+    F.v8 = (uint32_t)(2 * tp * T.vb_n + 8 * db) * 2u;
+    F.k8s = F.k4 = F.k4s = F.v8s = F.v4 = F.v4s = 0;
+  } else {
+    F.k8 = (uint32_t)tk * H * 256u + 16u * dc;
+    F.k8s = ((uint32_t)tk * H * NG8 + (16u * dc) / G8) * 2u;
+    F.k4 = (uint32_t)tk * H * 128u + 8u * dc;
+    F.k4s = ((uint32_t)tk * H * 8u + dc / 2) * 2u;
+    F.v8 = 2u * tp * H * 256u + 8u * db;
+    F.v8s = (2u * tp * H * NG8 + (8u * db) / G8) * 2u;
+    F.v4 = 2u * tp * H * 128u + 4u * db;
+    F.v4s = (2u * tp * H * 8u + db / 4) * 2u;
+  }
+  return F;
+}
+
+// How tile it + 2 is fetched: per key (kFetchKeys: a tile that straddles hot_start or the key end, or a ring
+// shorter than a tile), as a whole INT4 / INT8 / bf16 tile, or not at all (past the last tile).
+enum { kFetchKeys = 0, kFetchInt4 = 1, kFetchInt8 = 2, kFetchBf16 = 3, kFetchNone = 4 };
+
+template <int FETCH, int G8, bool BF16>
+KVT_DEV void fetch_k_tile(const Tier& T, const int32_t* lpages, int t2, const FetchLane& F, int tk, int dc, RawK& x) {
+  constexpr uint32_t NG8 = kD / G8;
+  if constexpr (FETCH == kFetchKeys) {
+    x = fetch_k<G8, BF16>(T, lpages, t2 + tk, dc);
+  } else if constexpr (FETCH == kFetchBf16) {
+    const uint32_t so = (uint32_t)(t2 * T.kb_n + T.h * T.kb_h) * 2u;
+    x.a = ld128s(T.kb, F.k8, so);
+    x.b = ld128s(T.kb, F.k8 + 16u, so);
+  } else if constexpr (FETCH == kFetchInt8) {
+    const uint32_t r8 = (uint32_t)((t2 & T.rmask) * T.H + T.h);
+    x.b = ld128s(T.rk, F.k8, r8 * 256u);
+    x.s8 = ld16s(T.rks, F.k8s, r8 * NG8 * 2u);
+  } else if constexpr (FETCH == kFetchInt4) {
+    const uint32_t pg = (uint32_t)__builtin_amdgcn_readfirstlane(lpages[min(t2 >> 6, kMaxLdsPages - 1)]);
+    const uint32_t r4 = (pg * kPage + (uint32_t)(t2 & (kPage - 1))) * (uint32_t)T.H + (uint32_t)T.h;
+    x.a4 = ld64s(T.k4, F.k4, r4 * 128u);
+    x.s4 = ld16s(T.ks4, F.k4s, r4 * 16u);
+  }
+}
+
+template <int FETCH, int G8, bool BF16>
+KVT_DEV void fetch_v_tile(const Tier& T, const int32_t* lpages, int t2, const FetchLane& F, int tp, int db, RawV& x) {
+  constexpr uint32_t NG8 = kD / G8;
+  const uint32_t H = (uint32_t)T.H;
+  if constexpr (FETCH == kFetchKeys) {
+    x = fetch_v<G8, BF16>(T, lpages, t2 + 2 * tp, db);
+  } else if constexpr (FETCH == kFetchBf16) {
+    const uint32_t so = (uint32_t)(t2 * T.vb_n + T.h * T.vb_h) * 2u;
+    x.a[0] = ld128s(T.vb, F.v8, so);
+    x.a[1] = ld128s(T.vb, F.v8, so + (uint32_t)T.vb_n * 2u);
+  } else if constexpr (FETCH == kFetchInt8) {
+    const uint32_t r8 = (uint32_t)((t2 & T.rmask) * T.H + T.h);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      x.a8[t] = ld64s(T.rv, F.v8, (r8 + t * H) * 256u);
+      x.s8[t] = ld16s(T.rvs, F.v8s, (r8 + t * H) * NG8 * 2u);
+    }
+  } else if constexpr (FETCH == kFetchInt4) {
+    const uint32_t pg = (uint32_t)__builtin_amdgcn_readfirstlane(lpages[min(t2 >> 6, kMaxLdsPages - 1)]);
+    const uint32_t r4 = (pg * kPage + (uint32_t)(t2 & (kPage - 1))) * H + (uint32_t)T.h;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      x.c4[t] = ld32s(T.v4, F.v4, (r4 + t * H) * 128u);
+      x.s4[t] = ld16s(T.vs4, F.v4s, (r4 + t * H) * 16u);
+    }
+  }
+}
+
 // Codes -> exact bf16 rows.  A code c with offset o (c + o >= 0) is placed in the mantissa of an fp16 "magic" value
 // h = 1024 + (c + o) (bits 0x6400 | (c + o)); v_fma_mix_f32 converts h and the fp16 scale s to fp32 and computes
 // h * s - (1024 + o) * s in one rounding, whose exact value c * s is representable (4 or 8 bits times the scale's
@@ -511,9 +614,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     koff[j] = k_chunk(n16, 4 * j + kb);
     voff[j] = vt_row_chunk(16 * j + n16, kb) - 1024u * (uint32_t)j;
   }
+  const FetchLane FL = fetch_lane<G8, BF16>(T, tk, dc, tp, db);
   int it = 0;
-  auto body = [&](auto tag) {
+  auto body = [&](auto tag, auto ftag) {
     constexpr int TIER = decltype(tag)::value;
+    constexpr int FETCH = decltype(ftag)::value;
     const int t0 = it * kT;
     const int cb = it & 1;
     const int t2 = t0 + 2 * kT;
@@ -542,7 +647,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         d[1] = mfma(kf[st][1], qop[st], d[1]);
         if constexpr (kDq) {
           k_step<TIER>(st, rk_next, ko, krow_next, tk, dc);
-          if (st == kFetchK<TIER>) rk_next = fetch_k<G8, BF16>(T, lds.pages, t2 + tk, dc);   // (clamped at the end)
+          if (st == kFetchK<TIER>) fetch_k_tile<FETCH, G8, BF16>(T, lds.pages, t2, FL, tk, dc, rk_next);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -627,7 +732,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         if (c > 0) acc[c - 1] = mfma(pb, vf[c - 1], acc[c - 1]);
         if constexpr (kDq) {
           v_step<TIER>(c, rv_next, va, vb, vt_next, db, tp);
-          if (c == kFetchV<TIER>) rv_next = fetch_v<G8, BF16>(T, lds.pages, t2 + 2 * tp, db);
+          if (c == kFetchV<TIER>) fetch_v_tile<FETCH, G8, BF16>(T, lds.pages, t2, FL, tp, db, rv_next);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -636,16 +741,32 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
     ++it;
   };
-  const int nd = ntiles - 1;   // iterations that dequantize a tile (tile it + 1)
+  // Iteration it converts tile it + 1 and fetches tile it + 2; a whole-tile fetch needs tile it + 2 to end at or
+  // before the key end (it + 3 <= kend / kT) and, for INT4, at or before hot_start.
+  const int nd = ntiles - 1;           // iterations that convert a tile (tile it + 1)
+  const int me = kend / kT - 2;        // iterations whose tile it + 2 ends at or before the key end
+  using KeysF = TierTag<kFetchKeys>;
+  // s_waitcnt vmcnt(0) before a loop: loads of an earlier loop still in flight into registers this loop reuses would
+  // otherwise make the loop header's wait state force vmcnt(0) inside the body, on every iteration
+  auto drain = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
   if constexpr (BF16) {
-    while (it < nd) body(TierTag<kTierBf16>{});
+    while (it < min(nd, me)) body(TierTag<kTierBf16>{}, TierTag<kFetchBf16>{});
+    drain();
+    while (it < nd) body(TierTag<kTierBf16>{}, KeysF{});
   } else {
-    const int n4 = T.hs / kT;  // tiles entirely below hot_start
-    while (it < min(n4 - 1, nd)) body(TierTag<kTierInt4>{});
-    if ((T.hs & (kT - 1)) != 0 && it == n4 - 1 && it < nd) body(TierTag<kTierMixed>{});
-    while (it < nd) body(TierTag<kTierInt8>{});
+    const int n4 = T.hs / kT;          // tiles entirely below hot_start
+    while (it < min(min(n4 - 1, nd), min(me, n4 - 2))) body(TierTag<kTierInt4>{}, TierTag<kFetchInt4>{});
+    drain();
+    while (it < min(n4 - 1, nd)) body(TierTag<kTierInt4>{}, KeysF{});
+    if ((T.hs & (kT - 1)) != 0 && it == n4 - 1 && it < nd) body(TierTag<kTierMixed>{}, KeysF{});
+    drain();
+    if (T.rmask >= kT - 1)
+      while (it < min(nd, me)) body(TierTag<kTierInt8>{}, TierTag<kFetchInt8>{});
+    drain();
+    while (it < nd) body(TierTag<kTierInt8>{}, KeysF{});
   }
-  while (it < ntiles) body(TierTag<kTierNone>{});
+  drain();
+  while (it < ntiles) body(TierTag<kTierNone>{}, TierTag<kFetchNone>{});
 
   // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
   // column n16 of block c = dim 16 c + n16
