@@ -499,6 +499,7 @@ KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t*
   }
 }
 
+constexpr int kAheadK = 3, kAheadV = 4;   // LDS operand reads issued this many matrix steps ahead
 constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 16 rows (16 / gs queries x gs heads)
 
 template <int G8, bool BF16>
@@ -623,7 +624,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     const int cb = it & 1;
     const int t2 = t0 + 2 * kT;
     // ---- S^T = K Q^T: lane holds keys t0 + 16 nt + 4 kb + r of query row n16 (unscaled).  Step st: the two
-    // products of k-slice st, the K operands of step st + 2 read from LDS, one piece of tile it + 1's K rows.
+    // products of k-slice st, the K operands of step st + kAheadK read from LDS, one piece of tile it + 1's K rows.
     float s[2][4];
     {
       constexpr bool kDq = TIER != kTierNone;
@@ -638,11 +639,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
           kf[st][nt] = __builtin_bit_cast(
               bf8, *reinterpret_cast<const u4v*>(kbuf + (16 * nt + n16) * kKPitch + koff[st & 3] + 256 * (st >> 2)));
       };
-      kread(0);
-      kread(1);
+#pragma unroll
+      for (int st = 0; st < kAheadK; ++st) kread(st);
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        if (st + 2 < 8) kread(st + 2);
+        if (st + kAheadK < 8) kread(st + kAheadK);
         d[0] = mfma(kf[st][0], qop[st], d[0]);
         d[1] = mfma(kf[st][1], qop[st], d[1]);
         if constexpr (kDq) {
@@ -713,7 +714,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     }
     // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read.
     // Step c: the high-part product of dims 16 c .., the remainder product of dims 16 (c - 1) .., the V operand of
-    // step c + 2 read from LDS, one piece of tile it + 1's V rows.
+    // step c + kAheadV read from LDS, one piece of tile it + 1's V rows.
     {
       constexpr bool kDq = TIER != kTierNone;
       const uint8_t* vbuf = lds.vt[cb];
@@ -723,11 +724,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       auto vread = [&](int c) {
         vf[c] = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(vbuf + voff[c & 3] + 1024 * c));
       };
-      vread(0);
-      vread(1);
+#pragma unroll
+      for (int c = 0; c < kAheadV; ++c) vread(c);
 #pragma unroll
       for (int c = 0; c < 16; ++c) {
-        if (c + 2 < 16) vread(c + 2);
+        if (c + kAheadV < 16) vread(c + kAheadV);
         acc[c] = mfma(pa, vf[c], acc[c]);
         if (c > 0) acc[c - 1] = mfma(pb, vf[c - 1], acc[c - 1]);
         if constexpr (kDq) {
