@@ -79,6 +79,22 @@ def test_prefill_chunks_vs_oracle(kvt_pkg, group8):
         assert torch.equal(outb.cpu(), out.to(torch.bfloat16)), ("bf16 output != rounded fp32 output", a)
 
 
+@pytest.mark.parametrize("ring", [16, 32])
+def test_prefill_short_ring(kvt_pkg, ring):
+    """Rings of 16 and 32 rows: a 32-key tile can hold more keys than the ring (every tile fetched per key) or exactly
+    the ring; chunks of 70 / 45 / 61 queries, so most positions sit in INT4 pages and hot_start falls inside a tile."""
+    from kvtier.kvt import kvt_prefill_attn
+    for a, n, xk, xv, dc, oc, gen in _chunked([70, 45, 61], ring, seed=17):
+        q = ref.make_q(HQ, D, gen, n=n)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        src = dict(k_src=xk.to(dev), v_src=xv.to(dev)) if a == 0 else {}
+        out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32, **src).cpu()
+        kk, vv = (xk, xv) if a == 0 else oc.rows(0)
+        exp = _oracle_chunk(q, a, kk, vv)
+        err = (out - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (ring, a, float(err.max()), float(err.mean()))
+
+
 @pytest.mark.parametrize("hq", [20, 24, 32])
 def test_prefill_wide_groups(kvt_pkg, hq):
     """Groups of more than 8 q heads per KV head (10, 12 -- the served model's 24 / 2 -- and 16): 16 / gs queries per
