@@ -117,10 +117,11 @@ int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_sca
  * q_stride_b elements, 16-byte aligned), the selected columns c < cu_k[b+1] - cu_k[b] (and < topk) whose position
  * indices[b * idx_stride + c] lies in [0, seq_lens[b]) are resolved through req_to_token[req_indices[b]] and, for
  * kind 2, the owner table, dequantized as kvt_compact_gather writes them (bf16(q * s * sm)) and attended with scale;
- * bf16 matrix-core products, fp32 accumulation.  Writes one unnormalized partial per 64 columns to part_o (fp32
- * [batch * H * n_splits, Hq / H, D]) and part_ml ([..., 2]): merge with kvt_decode_combine(n_chunks = n_splits,
- * chunk = 0, split_counts = NULL); a request with no attended column comes out NaN (0/0).  n_splits >= ceil(topk /
- * 64); Hq / H <= 16, D = 256.  Kinds and buffers as kvt_compact_gather; pool_rows = rows of k / v (byte offsets
+ * bf16 matrix-core products, fp32 accumulation.  Split s of a (request, KV head) covers columns [64 T s, 64 T (s + 1))
+ * with T = ceil(ceil(topk / 64) / n_splits) (T > 1: each wavefront loops over T 16-column tiles) and writes one
+ * unnormalized partial to part_o (fp32 [batch * H * n_splits, Hq / H, D]) and part_ml ([..., 2]): merge with
+ * kvt_decode_combine(n_chunks = n_splits, chunk = 0, split_counts = NULL); a request with no attended column comes
+ * out NaN (0/0).  n_splits >= 1; Hq / H <= 16, D = 256.  Kinds and buffers as kvt_compact_gather; pool_rows = rows of k / v (byte offsets
  * are 32-bit: pool_rows * H * D (INT8) or * D / 2 (INT4) < 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the
  * compact gather + FlashAttention-2 pair of the reference's decode (flat patch
  * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for top-k selections. */

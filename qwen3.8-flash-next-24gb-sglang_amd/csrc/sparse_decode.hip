@@ -69,6 +69,7 @@ struct SparseArgs {
   int H;
   int gs;
   int n_splits;
+  int tiles;             // decode: 16-column tiles per wavefront (a block takes kCols x tiles columns)
   uint32_t rows8;        // rows of the INT8 tensors (ring R when tiered, the pool otherwise)
   uint32_t rows4;        // rows of the INT4 pool
   float scale;
@@ -192,15 +193,56 @@ KVT_DEV TileCols resolve_tile(const SparseArgs& A, int64_t c0, int64_t c_end, co
   return tc;
 }
 
+// The same resolve in three stages, so that its chain of loads can run beside the previous tile's loads and math:
+// stage 0 loads the position, stage 1 the slot, stage 2 the owner; finish() computes the tile's columns.
+template <int KIND, int G8>
+struct Resolver {
+  int64_t col, pos, slot;
+  int own;
+  bool live;
+  KVT_DEV void stage0(const SparseArgs& A, int64_t c0, int64_t c_end, const int32_t* idx_row, int lane) {
+    col = c0 + (lane & 15);
+    live = lane < kRows && col < c_end;
+    pos = live ? (int64_t)idx_row[col * A.si_n] : -1;
+  }
+  KVT_DEV void stage1(const SparseArgs& A, int64_t L, int64_t req) {
+    live = live && pos >= 0 && pos < L;
+    slot = live ? (int64_t)A.req_to_token[req * A.req_stride + pos] : 0;
+  }
+  KVT_DEV void stage2(const SparseArgs& A) {
+    if constexpr (KIND == 2) own = live ? A.owner[slot & A.ring_mask] : -1;
+  }
+  KVT_DEV TileCols finish(const SparseArgs& A, int h) const {
+    bool hot = KIND == 0;
+    int64_t row = slot;
+    if constexpr (KIND == 2) {
+      if (live && (int64_t)own == slot) {
+        hot = true;
+        row = slot & A.ring_mask;
+      }
+    }
+    const int64_t rh = row * A.H + h;
+    TileCols tc;
+    tc.flags = (live ? 1 : 0) | (hot ? 2 : 0);
+    tc.coff = !live ? kNoRow : (uint32_t)(hot ? rh * kD : rh * (kD / 2));
+    tc.soff = !live ? kNoRow : (uint32_t)(hot ? rh * (kD / G8) * 2 : rh * (kD / kG4) * 2);
+    return tc;
+  }
+};
+
 // One resolved 16-column tile of a wavefront, folded into its running softmax state (m, l per q head n16 of this
 // lane, o): load and dequantize K into the wavefront's LDS rows, S^T = K Q^T, dequantize V into the same rows,
 // online softmax, O += P V.
-template <int KIND, int G8>
+// hook(k) runs other work at three points: k = 0 before the tile's loads, 1 after its K rows are in LDS, 2 after
+// S^T.
+template <int KIND, int G8, typename Hook>
 KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt, const TileCols& tc,
-                         int lane, const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16]) {
+                         int lane, const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16],
+                         Hook&& hook) {
   const int n16 = lane & 15, kq = lane >> 4;
   const int flags = tc.flags;
   TileLoads T;
+  hook(0);
   issue_tile<G8>(P, flags, tc.coff, tc.soff, lane, T);
 
   // K rows into this wavefront's LDS rows (row-major); a wavefront's LDS accesses complete in order, so these
@@ -215,6 +257,7 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
     for (int i = 0; i < 4; ++i) x[i] = c[i] * sk * smk[i];
     *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
   }
+  hook(1);
   // S^T = K Q^T: lane l holds rows 4 (l >> 4) + i of q head l & 15
   f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -223,6 +266,7 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
     const uint2 qb = *reinterpret_cast<const uint2*>(&qs[n16 * kKPitch + 16 * k + 4 * kq]);
     s = mfma_bf16(__builtin_bit_cast(bf4, ka), __builtin_bit_cast(bf4, qb), s);
   }
+  hook(2);
   // V rows into the same LDS rows (the stores stay behind the K reads above, which may alias them)
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
@@ -287,7 +331,7 @@ struct BlockLds {
   uint16_t qs[kHeads * kKPitch];
 };
 
-template <int KIND, int G8, bool ROWS>
+template <int KIND, int G8, bool ROWS, bool MULTI = false>
 KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
   auto& kv = S.kv;
   uint16_t* qs = S.qs;
@@ -311,9 +355,10 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
     qrow = b;
     L = A.seq_lens[b];
     const int64_t vcount = load_idx(A.cu_k, A.cu64, b + 1) - load_idx(A.cu_k, A.cu64, b);
-    c_begin = (int64_t)blockIdx.x * kCols;
+    const int64_t span = (int64_t)kCols * (MULTI ? A.tiles : 1);
+    c_begin = (int64_t)blockIdx.x * span;
     const int64_t lim = vcount < (int64_t)A.topk ? vcount : (int64_t)A.topk;
-    c_end = c_begin + kCols < lim ? c_begin + kCols : lim;
+    c_end = c_begin + span < lim ? c_begin + span : lim;
   }
 
   const int64_t req = load_idx(A.req_indices, A.req64, b);
@@ -368,10 +413,24 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
   if constexpr (ROWS) {
     for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
       const TileCols tc = resolve_tile<KIND, G8>(A, c0, c_end, idx_row, L, req, h, lane);
-      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o);
+      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
+    }
+  } else if constexpr (MULTI) {
+    // tiles c_begin + 16 wave + 64 k: the next tile's position, slot and owner loads go out beside this tile's
+    // loads and math (for the last tile they have no active lane)
+    TileCols tc = tc0;
+    Resolver<KIND, G8> rn;
+    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
+      const int64_t c1 = c0 + kCols;
+      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [&](int k) {
+        if (k == 0) rn.stage0(A, c1, c_end, idx_row, lane);
+        if (k == 1) rn.stage1(A, L, req);
+        if (k == 2) rn.stage2(A);
+      });
+      tc = rn.finish(A, h);
     }
   } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads
-    if (has_tile) attend_tile<KIND, G8>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o);
+    if (has_tile) attend_tile<KIND, G8>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o, [](int) {});
   }
 
   // merge the 4 wavefronts through LDS, 8 q heads per pass: wavefront w stores the O rows of the pass's heads and
@@ -454,6 +513,21 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
   sparse_attn_block<KIND, G8, false>(A, S);
 }
 
+// decode of long selections: a wavefront loops over A.tiles tiles with the accumulators live; 3 blocks per CU for
+// the tiered pool (168 VGPRs), 2 for the single-tier pools (about 200)
+template <int KIND, int G8>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
+sparse_decode_multi_kernel(SparseArgs A) {
+  __shared__ __align__(16) BlockLds S;
+  sparse_attn_block<KIND, G8, false, true>(A, S);
+}
+template <int G8>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3)))
+sparse_decode_multi_tiered_kernel(SparseArgs A) {
+  __shared__ __align__(16) BlockLds S;
+  sparse_attn_block<2, G8, false, true>(A, S);
+}
+
 // prefill rows: a wavefront loops over its row's tiles with the accumulators live, 2 blocks per CU
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) sparse_prefill_kernel(SparseArgs A) {
@@ -480,6 +554,10 @@ int launch(int kind, int group8, dim3 grid, hipStream_t st, const SparseArgs& A)
   do {                                                                                                     \
     if constexpr (ROWS)                                                                                    \
       hipLaunchKernelGGL((sparse_prefill_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);           \
+    else if (A.tiles > 1 && KIND_ == 2)                                                                    \
+      hipLaunchKernelGGL((sparse_decode_multi_tiered_kernel<G_>), grid, dim3(64 * kWaves), 0, st, A);      \
+    else if (A.tiles > 1)                                                                                  \
+      hipLaunchKernelGGL((sparse_decode_multi_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);      \
     else                                                                                                   \
       hipLaunchKernelGGL((sparse_decode_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);            \
   } while (0)
@@ -514,7 +592,10 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
                       const void* indices, int64_t idx_stride, const void* seq_lens, const void* cu_k,
                       int cu_is_int64, int batch, int topk, int H, int Hq, int D, int group8, float scale,
                       int n_splits, void* part_o, void* part_ml, void* stream) {
-  if (batch <= 0 || topk <= 0 || n_splits < (topk + kCols - 1) / kCols) return KVT_EINVAL;
+  if (batch <= 0 || topk <= 0 || n_splits <= 0) return KVT_EINVAL;
+  // n_splits blocks per (request, KV head) cover the topk columns with `tiles` 16-column tiles per wavefront
+  const int tiles64 = (topk + kCols - 1) / kCols;
+  const int tiles = (tiles64 + n_splits - 1) / n_splits;
   if ((q_stride_b & 7) != 0 || ((uintptr_t)q & 15) != 0) return KVT_EINVAL;
   int64_t rows8 = 0, rows4 = 0;
   const int st_ = pool_args(kind, pool_rows, ring_k, owner, ring_mask, H, Hq, D, group8, &rows8, &rows4);
@@ -527,8 +608,8 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
   A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
   A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.idx_stride = idx_stride;
   A.seq_lens = (const int32_t*)seq_lens, A.cu_k = cu_k, A.cu64 = cu_is_int64, A.topk = topk;
-  A.H = H, A.gs = Hq / H, A.n_splits = n_splits, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
-  A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = q_stride_b, A.sq_h = kD;
+  A.H = H, A.gs = Hq / H, A.n_splits = n_splits, A.tiles = tiles, A.rows8 = (uint32_t)rows8;
+  A.rows4 = (uint32_t)rows4, A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = q_stride_b, A.sq_h = kD;
   A.si_m = idx_stride, A.si_g = 0, A.si_n = 1, A.part_o = (float*)part_o, A.part_ml = (float*)part_ml;
   return launch<false>(kind, group8, dim3((unsigned)n_splits, (unsigned)(batch * H)), (hipStream_t)stream, A);
 }
@@ -556,7 +637,7 @@ int kvt_sparse_prefill(int kind, const void* q, int64_t sq_n, int64_t sq_h, cons
   A.sm_k = (const uint16_t*)sm_k, A.sm_v = (const uint16_t*)sm_v;
   A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
   A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.topk = topk;
-  A.H = H, A.gs = Hq / H, A.n_splits = 1, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
+  A.H = H, A.gs = Hq / H, A.n_splits = 1, A.tiles = 1, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
   A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = sq_n, A.sq_h = sq_h;
   A.si_m = si_m, A.si_g = si_g, A.si_n = si_n;
   A.cu_q = cu_q, A.cuq64 = cu_q_is_int64, A.kv_lens = (const int32_t*)kv_lens;

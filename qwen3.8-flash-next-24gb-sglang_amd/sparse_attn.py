@@ -216,7 +216,7 @@ def qwen_sparse_decode_attn(
     q, k, v, req_to_token, req_indices, indices, seq_lens, cu_k, batch, topk,
     k_scale=None, v_scale=None, sm_k=None, sm_v=None, kv_bits=None,
     ring_k=None, ring_v=None, ring_ks=None, ring_vs=None, owner=None, ring_mask=None,
-    scale=None, out=None, workspace=None,
+    scale=None, out=None, workspace=None, splits=None,
 ):
     """Top-k sparse decode attention fused over the quantized pool: what qwen_sparse_kv_extraction_compact_triton
     followed by FlashAttention-2 over its bf16 scratch computes for one query row per request (flat patch
@@ -225,7 +225,8 @@ def qwen_sparse_decode_attn(
     q: bf16 [batch, Hq, D]; the pool/ring/owner/scale arguments as the compact gather; cu_k: the valid counts'
     prefix sum (qwen_sparse_fa2_cu_seqlens_triton).  Column c of request b is attended when c < cu_k[b+1] - cu_k[b]
     and 0 <= indices[b, c] < seq_lens[b].  Returns out (fp32 [batch, Hq, D] unless a bf16/fp32 `out` is given);
-    a request with no attended column gives NaN.  `workspace` (a dict) keeps the partial buffers across calls."""
+    a request with no attended column gives NaN.  `workspace` (a dict) keeps the partial buffers across calls;
+    `splits` sets the number of column splits per (request, KV head) instead of the launch-size rule below."""
     _, heads, dim = k.shape
     if k.dtype == torch.uint8 and kv_bits == 4 and owner is not None:
         dim = 2 * dim
@@ -262,7 +263,15 @@ def qwen_sparse_decode_attn(
         return out
     _lib.require_device(q, k, v, req_to_token, indices, out)
     scale = float(dim ** -0.5) if scale is None else float(scale)
-    n_splits = (int(topk) + 63) // 64   # 64 selected columns per wavefront
+    # blocks of 64 selected columns (a 16-column tile per wavefront) while the launch holds at most 1,024 of them;
+    # longer selections take `tiles` tiles per wavefront in about one block per resident slot (3 per CU for the
+    # tiered pool, 2 for the others), each partial then covering 64 x tiles columns
+    tiles64 = (int(topk) + 63) // 64
+    blocks = batch * heads * tiles64
+    slots_ = 768 if kind == _KIND_TIERED else 512
+    tiles = 1 if blocks <= 1024 else -(-blocks // slots_)
+    n_splits = -(-tiles64 // tiles) if splits is None else int(splits)
+    assert n_splits >= 1
     ws = workspace if workspace is not None else {}
     need = batch * heads * n_splits * (Hq // heads)
     if ws.get("sparse_o") is None or ws["sparse_o"].numel() < need * dim:

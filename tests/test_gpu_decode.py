@@ -308,20 +308,22 @@ def test_decode_slot_rings_config0(kvt_pkg):
         assert float(err.max()) < tol and float(err.mean()) < mtol, (impl, float(err.max()))
 
 
-@pytest.mark.parametrize("hq", [16, 24])
-def test_decode_slots_mfma_ragged(kvt_pkg, hq):
-    """Dense decode over the slot-indexed tiered pool through the matrix cores: 3 requests (5,000 / 1,300 / 64
-    positions) on randomly permuted slots of one pool, ring of 1,024 rows with owners from the dual write (the ring
-    has wrapped: most positions are INT4 rows, the newest are ring rows), G64 ring scales, smoothing factors,
-    against the oracle's gathered rows and fp32 attention."""
+@pytest.mark.parametrize("hq,lens", [(16, [5000, 1300, 64]), (24, [5000, 1300, 64]), (16, [20000, 9000, 300, 17])])
+def test_decode_slots_mfma_ragged(kvt_pkg, hq, lens):
+    """Dense decode over the slot-indexed tiered pool through the matrix cores: requests of 5,000 / 1,300 / 64
+    positions (one 16-column tile per wavefront), and of 20,000 / 9,000 / 300 / 17 (past 1,024 blocks of 64 columns:
+    each wavefront loops over several tiles) on randomly permuted slots of one pool, ring of 1,024 rows with owners
+    from the dual write (the ring has wrapped: most positions are INT4 rows, the newest are ring rows), G64 ring
+    scales, smoothing factors, against the oracle's gathered rows and fp32 attention."""
     from kvtier import sparse_attn as sa
     from kvtier.kvt import decode_attn_slots
     gen = torch.Generator().manual_seed(61)
-    lens, R, slots = [5000, 1300, 64], 1024, 8192
+    R = 1024
+    slots = 8192 if sum(lens) <= 8192 else 32768
     och = ref.outlier_channels(H, D, 8, gen)
     perm = torch.randperm(slots, generator=gen).to(torch.int32)
-    r2t = torch.full((4, 5100), -7, dtype=torch.int32)
-    req_idx = torch.tensor([2, 0, 3], dtype=torch.int64)
+    r2t = torch.full((len(lens) + 1, max(lens) + 100), -7, dtype=torch.int32)
+    req_idx = torch.tensor([2, 0, 3, 1][:len(lens)], dtype=torch.int64)
     a = 0
     for b, L in enumerate(lens):
         r2t[int(req_idx[b]), :L] = perm[a:a + L]
@@ -342,7 +344,7 @@ def test_decode_slots_mfma_ragged(kvt_pkg, hq):
             sa.quant_store_kv_tiered(xk[c0:c1].to(dev), xv[c0:c1].to(dev), locs[c0:c1].to(dev), k4, v4, ks4, vs4, rk,
                                      rv, rks, rvs, owner, smi.to(dev), smi.to(dev), R - 1)
     torch.cuda.synchronize()
-    q = ref.make_q(hq, D, gen, n=3)
+    q = ref.make_q(hq, D, gen, n=len(lens))
     seq = torch.tensor(lens, dtype=torch.int32)
     out = decode_attn_slots(q.to(dev), seq.to(dev), r2t.to(dev), req_idx.to(dev), k4, v4, ks4, vs4, rk, rv, rks, rvs,
                             owner, R - 1, sm_k=sm.to(dev), sm_v=sm.to(dev)).cpu()

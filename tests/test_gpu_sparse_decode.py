@@ -53,10 +53,10 @@ def _rows(kind, p, slots, R, g8):
             ref.dequant8(p["v8"][sl], p["vs8"][sl], p["sm_v"], g8))
 
 
-def _call(kind, p, q, r2t, req_idx, idx, seq_lens, cu_k, batch, topk, R, out=None):
+def _call(kind, p, q, r2t, req_idx, idx, seq_lens, cu_k, batch, topk, R, out=None, splits=None):
     from kvtier import sparse_attn as sa
     d = {k: v.to(dev) for k, v in p.items()}
-    common = dict(scale=D ** -0.5, out=out)
+    common = dict(scale=D ** -0.5, out=out, splits=splits)
     if kind == "tiered":
         return sa.qwen_sparse_decode_attn(q.to(dev), d["k4"], d["v4"], r2t.to(dev), req_idx.to(dev), idx.to(dev),
                                           seq_lens.to(dev), cu_k.to(dev), batch, topk, d["ks4"], d["vs4"],
@@ -120,6 +120,21 @@ def test_sparse_decode_matches_oracle(kvt_pkg, kind, g8):
     r2t, req_idx, idx, sl, cu_k = _case(gen, [3000, 700, 9], 2051, slots)
     q = (torch.randn(3, HQ, D, generator=gen) / 4).to(torch.bfloat16)
     got = _call(kind, p, q, r2t, req_idx, idx, sl, cu_k, 3, 2051, R).cpu()
+    _close(got, _oracle(kind, p, q, r2t, req_idx, idx, sl, cu_k, 2051, R, g8))
+
+
+@pytest.mark.parametrize("kind,g8,splits", [("tiered", 64, 1), ("tiered", 256, 3), ("int4", 64, 11),
+                                            ("int8", 64, 3)])
+def test_sparse_decode_tiles_per_wavefront(kvt_pkg, kind, g8, splits):
+    """The 2,051 selected columns of the previous case in 1 / 3 / 11 splits: each wavefront loops over 33 / 11 / 3
+    tiles, resolving the next tile's positions, slots and owners beside the current one (the launch-size rule takes
+    this path for long selections)."""
+    gen = torch.Generator().manual_seed(31)
+    slots, R = 4096, 64
+    p = _pools(slots, R, g8, gen)
+    r2t, req_idx, idx, sl, cu_k = _case(gen, [3000, 700, 9], 2051, slots)
+    q = (torch.randn(3, HQ, D, generator=gen) / 4).to(torch.bfloat16)
+    got = _call(kind, p, q, r2t, req_idx, idx, sl, cu_k, 3, 2051, R, splits=splits).cpu()
     _close(got, _oracle(kind, p, q, r2t, req_idx, idx, sl, cu_k, 2051, R, g8))
 
 
