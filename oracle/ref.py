@@ -1,7 +1,7 @@
 """CPU oracle for the tiered quantized KV cache (``int8ring_int4``): TEST INFRASTRUCTURE ONLY.
 
 This module restates, on the CPU with torch tensors, the arithmetic of the reference's tiered KV path so that
-the HIP kernels can be checked against it.  It is the checker, never the product: only ``tests/``,
+the HIP kernels can be checked against it.  It is test infrastructure, never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may import it, and the package never
 falls back to it.
 

@@ -1,4 +1,4 @@
-"""Pinning the CPU oracle (oracle/ref.py) before it is trusted as the checker of the HIP kernels.
+"""Pinning the CPU oracle (oracle/ref.py) before the HIP kernels are compared with it.
 
 Each check is chosen so that a plausible mistake fails it: the reference tests' special cases and constants
 (gemv/test_kv_int4.py, gemv/test_kv_int8.py, gemv/test_kv_tiers.py), the golden vectors of the independent scalar
