@@ -91,6 +91,26 @@ struct __align__(16) Lds {
 
 KVT_DEV f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 
+// max of two scores in one v_max_f32: written as asm, the compiler adds no canonicalizing v_max_f32 x, x, x for
+// values out of a lane permute (the scores are finite or -inf, never NaN)
+KVT_DEV float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+KVT_DEV float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+// the max over the 4 lanes l, l ^ 16, l ^ 32, l ^ 48 (v_permlane16_swap / v_permlane32_swap; all lanes active)
+KVT_DEV float vmax_xor16_32(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32): lo in bits 0-15.
 KVT_DEV uint32_t bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){lo, hi}, bf2v));
@@ -670,15 +690,12 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     // ---- online softmax; P as the A operand of P.V (bf16 high part pa, remainder pb)
     bf8 pa, pb;
     {
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, s[nt][r]);
-      mloc = max_xor16_32(mloc) * qmul;   // log2 units
+      float mloc = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), s[0][3], s[1][0]);
+      mloc = vmax(vmax3(mloc, s[1][1], s[1][2]), s[1][3]);
+      mloc = vmax_xor16_32(mloc) * qmul;   // log2 units
       // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
       // by more than 8 (log2 units), so P = 2^(s qmul - m) <= 256
-      const float m_new = fmaxf(m_run, mloc);
+      const float m_new = vmax(m_run, mloc);
       if (__any(m_new > m_run + 8.0f)) {
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
