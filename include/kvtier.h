@@ -245,7 +245,8 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
  * [positions, H, D] rows (the reference attends to fresh bf16 K/V there).  out: bf16 or fp32 (out_f32) with the
  * layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
  * chunks.  Hq / H <= 16, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
- * offsets are 32-bit, else KVT_ERANGE). */
+ * offsets are 32-bit, else KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
+ * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device). */
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
                      const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
