@@ -35,26 +35,23 @@ typedef float f2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+typedef short s4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s4v lds_s4;
 
 constexpr int kD = 256;
 constexpr int kT = 32;                  // key positions per tile
-// LDS tiles, XOR-swizzled so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
+// LDS tiles, laid out so that the matrix operand reads are free of bank conflicts (64 banks of 4 bytes):
 //   K: bf16 row per key (512 B); its 16-byte chunk c lives at chunk c ^ (key & 15).  An A-operand read takes chunk
 //      4 st + kb of 16 consecutive keys: 16 distinct chunks mod 16, i.e. all 64 banks.
-//   V^T: bf16 row per dim (64 B = 32 keys) in four 16-byte chunks; chunk q holds the keys of matrix k-group q
-//      (keys 4 q .. 4 q + 3, then 16 + 4 q .. 16 + 4 q + 3: the k order of the P operand).  Dim d is stored in row
-//      r = d ^ ((d >> 4) & 3), its chunk q at chunk q ^ ((r >> 1) & 3).  A B-operand read is one 16-byte read of
-//      chunk kb for 16 consecutive dims: each 8-lane phase covers 8 distinct 16-byte bank groups whether the LDS
-//      is served as 32 or 64 banks; the transposed dword stores of the dequantizing threads (16 key pairs x 4 dim
-//      blocks per wavefront) hit distinct banks per 32 lanes.  Measured: 18.1 M bank-conflict cycles per 10k-token
-//      chunk dispatch, against 60.2 M with 8-byte chunks.
+//   V: bf16 row per key (256 dims) at a pitch of 544 B (136 dwords, 8 banks past a multiple of 64).  The P.V B
+//      operand (dims 16 c .. 16 c + 15 of keys 4 kb .. 4 kb + 3, then 16 + 4 kb .. 16 + 4 kb + 3: the k order of the
+//      P operand) is two ds_read_b64_tr_b16: in each 16-lane group lane m addresses 8 bytes of row 4 kb + (m >> 2)
+//      at dim 16 c + 4 (m & 3), and lane L receives element L & 3 of the 8 bytes of lanes 4 k + (L >> 2), i.e. the
+//      dim 16 c + L of keys 4 kb + k; the four rows of a group sit 8 banks apart.  A converting thread stores 8
+//      channels of keys tp and tp + 16 (16 bytes each) with no transposition.
 constexpr int kKPitch = kD * 2;         // bytes per bf16 K row
-constexpr int kVPitch = kT * 2;         // bytes per bf16 V^T row
+constexpr int kVRow = kD * 2 + 32;      // bytes per bf16 V row
 KVT_DEV uint32_t k_chunk(int key, int c) { return 16u * (uint32_t)(c ^ (key & 15)); }
-KVT_DEV uint32_t vt_row_chunk(int dim, int q) {
-  const int row = dim ^ ((dim >> 4) & 3);
-  return (uint32_t)row * kVPitch + 16u * (uint32_t)(q ^ ((row >> 1) & 3));
-}
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -85,7 +82,7 @@ struct KVSrc {
 
 struct __align__(16) Lds {
   uint8_t k[2][kT * kKPitch];    // double-buffered: tile i + 1 is dequantized while tile i is in use
-  uint8_t vt[2][kD * kVPitch];
+  uint8_t v[2][kT * kVRow];
   int32_t pages[kMaxLdsPages];
 };
 
@@ -147,7 +144,8 @@ struct RawK {
   uint32_t s4, s8;
   int hot;
 };
-// Raw V of two key rows, channels 8 db .. 8 db + 7 each: INT4 (c4, s4) or INT8 (a8, s8); bf16 source: a.
+// Raw V of two key rows (keys k and k + 16 of a tile), channels 8 db .. 8 db + 7 each: INT4 (c4, s4) or INT8 (a8,
+// s8); bf16 source: a.
 struct RawV {
   uint4 a[2];
   uint2 a8[2];
@@ -182,12 +180,13 @@ KVT_DEV RawK fetch_k(const Tier& T, const int32_t* lpages, int p, int dc) {
   return x;
 }
 
+// V of keys p0 and p0 + 16, channels 8 db .. 8 db + 7
 template <int G8, bool BF16>
 KVT_DEV RawV fetch_v(const Tier& T, const int32_t* lpages, int p0, int db) {
   RawV x;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int p = min(p0 + t, T.key_end - 1);
+    const int p = min(p0 + 16 * t, T.key_end - 1);
     if constexpr (BF16) {
       const uint32_t off = (uint32_t)(p * T.vb_n + T.h * T.vb_h + 8 * db) * 2u;
       x.a[t] = ld128(T.vb, off);
@@ -230,8 +229,8 @@ KVT_DEV uint32_t ld16s(Rsrc r, uint32_t v, uint32_t s) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)v, (int)s, 0);
 }
 
-// Per-lane byte offsets within a tile: K row tk, channels 16 dc; V rows 2 tp (the second row adds one row's stride
-// to the scalar part), channels 8 db.  INT8 codes / scales, INT4 codes / scales; the bf16 source uses k8 and v8.
+// Per-lane byte offsets within a tile: K row tk, channels 16 dc; V rows tp and tp + 16 (the second adds 16 rows'
+// stride to the scalar part), channels 8 db.  INT8 codes / scales, INT4 codes / scales; the bf16 source uses k8 and v8.
 struct FetchLane {
   uint32_t k8, k8s, k4, k4s, v8, v8s, v4, v4s;
 };
@@ -243,17 +242,17 @@ KVT_DEV FetchLane fetch_lane(const Tier& T, int tk, int dc, int tp, int db) {
   const uint32_t H = (uint32_t)T.H;
   if constexpr (BF16) {
     F.k8 = (uint32_t)(tk * T.kb_n + 16 * dc) * 2u;
-    F.v8 = (uint32_t)(2 * tp * T.vb_n + 8 * db) * 2u;
+    F.v8 = (uint32_t)(tp * T.vb_n + 8 * db) * 2u;
     F.k8s = F.k4 = F.k4s = F.v8s = F.v4 = F.v4s = 0;
   } else {
     F.k8 = (uint32_t)tk * H * 256u + 16u * dc;
     F.k8s = ((uint32_t)tk * H * NG8 + (16u * dc) / G8) * 2u;
     F.k4 = (uint32_t)tk * H * 128u + 8u * dc;
     F.k4s = ((uint32_t)tk * H * 8u + dc / 2) * 2u;
-    F.v8 = 2u * tp * H * 256u + 8u * db;
-    F.v8s = (2u * tp * H * NG8 + (8u * db) / G8) * 2u;
-    F.v4 = 2u * tp * H * 128u + 4u * db;
-    F.v4s = (2u * tp * H * 8u + db / 4) * 2u;
+    F.v8 = (uint32_t)tp * H * 256u + 8u * db;
+    F.v8s = ((uint32_t)tp * H * NG8 + (8u * db) / G8) * 2u;
+    F.v4 = (uint32_t)tp * H * 128u + 4u * db;
+    F.v4s = ((uint32_t)tp * H * 8u + db / 4) * 2u;
   }
   return F;
 }
@@ -288,25 +287,25 @@ KVT_DEV void fetch_v_tile(const Tier& T, const int32_t* lpages, int t2, const Fe
   constexpr uint32_t NG8 = kD / G8;
   const uint32_t H = (uint32_t)T.H;
   if constexpr (FETCH == kFetchKeys) {
-    x = fetch_v<G8, BF16>(T, lpages, t2 + 2 * tp, db);
+    x = fetch_v<G8, BF16>(T, lpages, t2 + tp, db);
   } else if constexpr (FETCH == kFetchBf16) {
     const uint32_t so = (uint32_t)(t2 * T.vb_n + T.h * T.vb_h) * 2u;
     x.a[0] = ld128s(T.vb, F.v8, so);
-    x.a[1] = ld128s(T.vb, F.v8, so + (uint32_t)T.vb_n * 2u);
+    x.a[1] = ld128s(T.vb, F.v8, so + 16u * (uint32_t)T.vb_n * 2u);
   } else if constexpr (FETCH == kFetchInt8) {
     const uint32_t r8 = (uint32_t)((t2 & T.rmask) * T.H + T.h);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      x.a8[t] = ld64s(T.rv, F.v8, (r8 + t * H) * 256u);
-      x.s8[t] = ld16s(T.rvs, F.v8s, (r8 + t * H) * NG8 * 2u);
+      x.a8[t] = ld64s(T.rv, F.v8, (r8 + 16u * t * H) * 256u);
+      x.s8[t] = ld16s(T.rvs, F.v8s, (r8 + 16u * t * H) * NG8 * 2u);
     }
   } else if constexpr (FETCH == kFetchInt4) {
     const uint32_t pg = (uint32_t)__builtin_amdgcn_readfirstlane(lpages[min(t2 >> 6, kMaxLdsPages - 1)]);
     const uint32_t r4 = (pg * kPage + (uint32_t)(t2 & (kPage - 1))) * H + (uint32_t)T.h;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      x.c4[t] = ld32s(T.v4, F.v4, (r4 + t * H) * 128u);
-      x.s4[t] = ld16s(T.vs4, F.v4s, (r4 + t * H) * 16u);
+      x.c4[t] = ld32s(T.v4, F.v4, (r4 + 16u * t * H) * 128u);
+      x.s4[t] = ld16s(T.vs4, F.v4s, (r4 + 16u * t * H) * 16u);
     }
   }
 }
@@ -422,29 +421,21 @@ KVT_DEV void v_row8(const RawV& x, int t, uint32_t o[4]) {
   }
 }
 
-// Two keys x 8 channels -> V^T rows (dim 8 db + c) at key pair tp: one dword [key 2 tp, key 2 tp + 1] per dim.
+// 8 channels of keys tp and tp + 16 -> their V rows (16 bytes each).
 template <int TIER>
-KVT_DEV void store_v(const RawV& x, uint8_t* vt, int db, int tp) {
+KVT_DEV void store_v(const RawV& x, uint8_t* vrows, int db, int tp) {
   uint32_t a[4], b[4];
   v_row8<TIER>(x, 0, a);
   v_row8<TIER>(x, 1, b);
-  // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
-  const int q = (tp >> 1) & 3;
-  const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
-    const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
-    const int d0 = 8 * db + 2 * i, d1 = d0 + 1;
-    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d0, q) + inner) = lo;
-    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d1, q) + inner) = hi;
-  }
+  *reinterpret_cast<uint4*>(vrows + tp * kVRow + 16 * db) = make_uint4(a[0], a[1], a[2], a[3]);
+  *reinterpret_cast<uint4*>(vrows + (tp + 16) * kVRow + 16 * db) = make_uint4(b[0], b[1], b[2], b[3]);
 }
 
 // Tile it + 1's rows are converted in pieces, one per matrix step of tile it (the loops below fence every step with
 // sched_barrier, so each piece issues between two groups of products instead of in one run of vector instructions).
 // K: 8 steps beside the score products; the rows go to LDS in the two steps after the conversion, and the codes of
-// tile it + 2 are fetched at step kFetchK.  V: 16 steps beside P.V, likewise with kFetchV.
+// tile it + 2 are fetched at step kFetchK.  V: 16 steps beside P.V, likewise with kFetchV; each thread converts
+// 8 channels of two keys and stores them as two 16-byte pieces of the row-major V tile.
 template <int TIER>
 constexpr int kConvK = TIER == kTierInt8 ? 4 : TIER == kTierInt4 ? 2 : 1;   // conversion steps of a K fragment
 template <int TIER>
@@ -452,7 +443,7 @@ constexpr int kFetchK = kConvK<TIER> + 2;
 template <int TIER>
 constexpr int kConvV = TIER == kTierInt8 ? 4 : TIER == kTierInt4 ? 2 : 1;
 template <int TIER>
-constexpr int kFetchV = kConvV<TIER> + 5;
+constexpr int kFetchV = kConvV<TIER> + 2;
 
 KVT_DEV uint32_t word_of(const uint4& w, int j) { return j == 0 ? w.x : j == 1 ? w.y : j == 2 ? w.z : w.w; }
 
@@ -490,7 +481,7 @@ KVT_DEV void k_step(int j, const RawK& x, uint32_t o[8], uint8_t* row, int key, 
 }
 
 template <int TIER>
-KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t* vt, int db, int tp) {
+KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t* vrows, int db, int tp) {
   if constexpr (TIER == kTierInt8) {
     if (j < 4) {
       const int t = j >> 1, hw = j & 1;
@@ -506,17 +497,8 @@ KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t*
     }
   }
   constexpr int w0 = kConvV<TIER>;
-  if (j >= w0 && j < w0 + 4) {
-    // keys 2 tp, 2 tp + 1: k-group q = (tp >> 1) & 3, second half of the chunk when tp >= 8, dword tp & 1
-    const int i = j - w0;
-    const int q = (tp >> 1) & 3;
-    const uint32_t inner = 8u * (uint32_t)(tp >> 3) + 4u * (uint32_t)(tp & 1);
-    const uint32_t lo = __builtin_amdgcn_perm(b[i], a[i], 0x05040100u);   // [a.lo, b.lo]: dim 2i
-    const uint32_t hi = __builtin_amdgcn_perm(b[i], a[i], 0x07060302u);   // [a.hi, b.hi]: dim 2i + 1
-    const int d0 = 8 * db + 2 * i, d1 = d0 + 1;
-    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d0, q) + inner) = lo;
-    *reinterpret_cast<uint32_t*>(vt + vt_row_chunk(d1, q) + inner) = hi;
-  }
+  if (j == w0) *reinterpret_cast<uint4*>(vrows + tp * kVRow + 16 * db) = make_uint4(a[0], a[1], a[2], a[3]);
+  if (j == w0 + 1) *reinterpret_cast<uint4*>(vrows + (tp + 16) * kVRow + 16 * db) = make_uint4(b[0], b[1], b[2], b[3]);
 }
 
 constexpr int kAheadK = 3, kAheadV = 4;   // LDS operand reads issued this many matrix steps ahead
@@ -613,11 +595,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   const int ntiles = (int)((key_end + kT - 1) / kT);
   constexpr int kFirst = BF16 ? kTierBf16 : kTierMixed;
   RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, 2 * tp, db);
+  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, tp, db);
   store_k<kFirst>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
-  store_v<kFirst>(rv_next, lds.vt[0], db, tp);
+  store_v<kFirst>(rv_next, lds.v[0], db, tp);
   rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);   // (past the end it rereads the last key)
-  rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + 2 * tp, db);
+  rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + tp, db);
   __syncthreads();
   const int qmin = (int)(q_pos0 + qt0);   // the block's first query position: tiles below it need no causal mask
   const int qp = (int)qpos, kend = (int)key_end;
@@ -628,13 +610,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   // so the iterations run as consecutive loops with one code path each.
   // LDS read offsets of this lane's MFMA operands, split into a per-lane part (computed once) and a constant:
   // K chunk 4 st + kb of key row n16 sits at 256 (st >> 2) + koff[st & 3] (the swizzle n16 only touches the low
-  // four chunk bits), V^T row 16 c + n16, k-group kb at 1024 c + voff[c & 3] (row and chunk swizzles see only c & 3)
-  uint32_t koff[4], voff[4];
+  // four chunk bits); the V reads of dims 16 c .. at vlane + 32 c (keys 4 kb + (n16 >> 2)) and + 16 rows
+  uint32_t koff[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    koff[j] = k_chunk(n16, 4 * j + kb);
-    voff[j] = vt_row_chunk(16 * j + n16, kb) - 1024u * (uint32_t)j;
-  }
+  for (int j = 0; j < 4; ++j) koff[j] = k_chunk(n16, 4 * j + kb);
+  const uint32_t vlane = (uint32_t)(4 * kb + (n16 >> 2)) * kVRow + 8u * (uint32_t)(n16 & 3);
   const FetchLane FL = fetch_lane<G8, BF16>(T, tk, dc, tp, db);
   int it = 0;
   auto body = [&](auto tag, auto ftag) {
@@ -729,17 +709,21 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       pa = __builtin_bit_cast(bf8, u4v{hw[0], hw[1], hw[2], hw[3]});
       pb = __builtin_bit_cast(bf8, u4v{lw[0], lw[1], lw[2], lw[3]});
     }
-    // ---- O += P V: B = V^T row (dim 16 c + n16), k-group kb = keys {4 kb .. +3, 16 + 4 kb .. +3}: one 16-byte read.
+    // ---- O += P V: B = dim 16 c + n16 of keys {4 kb .. +3, 16 + 4 kb .. +3}: two transposing 8-byte reads.
     // Step c: the high-part product of dims 16 c .., the remainder product of dims 16 (c - 1) .., the V operand of
     // step c + kAheadV read from LDS, one piece of tile it + 1's V rows.
     {
       constexpr bool kDq = TIER != kTierNone;
-      const uint8_t* vbuf = lds.vt[cb];
-      uint8_t* vt_next = lds.vt[cb ^ 1];
+      const uint8_t* vbuf = lds.v[cb];
+      uint8_t* v_next = lds.v[cb ^ 1];
       uint32_t va[4], vb[4];
       bf8 vf[16];
       auto vread = [&](int c) {
-        vf[c] = __builtin_bit_cast(bf8, *reinterpret_cast<const u4v*>(vbuf + voff[c & 3] + 1024 * c));
+        const uint32_t a0 = (uint32_t)(uintptr_t)(vbuf + vlane + 32 * c);
+        const auto lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(uintptr_t)a0);
+        const auto hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(uintptr_t)(a0 + 16u * kVRow));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        vf[c] = __builtin_bit_cast(bf8, u4v{l2.x, l2.y, h2.x, h2.y});
       };
 #pragma unroll
       for (int c = 0; c < kAheadV; ++c) vread(c);
@@ -749,7 +733,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         acc[c] = mfma(pa, vf[c], acc[c]);
         if (c > 0) acc[c - 1] = mfma(pb, vf[c - 1], acc[c - 1]);
         if constexpr (kDq) {
-          v_step<TIER>(c, rv_next, va, vb, vt_next, db, tp);
+          v_step<TIER>(c, rv_next, va, vb, v_next, db, tp);
           if (c == kFetchV<TIER>) fetch_v_tile<FETCH, G8, BF16>(T, lds.pages, t2, FL, tp, db, rv_next);
         }
         __builtin_amdgcn_sched_barrier(0);
