@@ -336,7 +336,7 @@ def prefill_workload(args) -> dict:
     return {
         "metric": "chunked prefill 10,001 tokens x 12 layers: ms per prompt (append + evict + causal prefill)",
         "value": round(t_prompt * 1e3, 3), "unit": "ms", "higher_is_better": False, "steps": args.steps,
-        "warmup": args.warmup, "dtype": "bf16-mfma/f32", "data": "synthetic",
+        "warmup": args.warmup, "dtype": "bf16 QK / f16 PV mfma, f32", "data": "synthetic",
         "config": {"workload": "10,001-token prompt, chunks of 2048, 12 layers, 16 Q / 2 KV heads, D 256, ring 8192 "
                                "(1,809 positions evicted to INT4 pages in the last chunk)"},
         "roofline": {"bound": "mfma", "achieved": round(flops / t_prefill / 1e12, 2), "peak": 2500.0,

@@ -237,13 +237,14 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
                             void* stream);
 
 /* Causal prefill attention of a chunk of queries over the position-indexed tiered cache on the matrix cores
- * (v_mfma_f32_16x16x32_bf16, K/V tiles dequantized once per 16 queries into LDS as the exact bf16 rows
- * bf16(code * scale); P as two bf16 parts; fp32 softmax and accumulation).  Sequence b's queries are rows
+ * (K/V tiles dequantized once per block into LDS as the exact bf16 rows bf16(code * scale); QK^T on
+ * v_mfma_f32_16x16x32_bf16; P.V on v_mfma_f32_16x16x32_f16 with P rounded to fp16 and V = the bf16 rows / 128 in
+ * fp16; fp32 softmax and accumulation).  Sequence b's queries are rows
  * cu_q[b] .. cu_q[b+1] of q (bf16 [total_q, Hq, D], strides sq_n / sq_h) at positions kv_lens[b] - q_len .. ;
  * each attends to every position <= its own (patches/kv_paged_prefix.py:200), read from the cache tiers of
  * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16
- * [positions, H, D] rows (the reference attends to fresh bf16 K/V there).  out: bf16 or fp32 (out_f32) with the
- * layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
+ * [positions, H, D] rows (the reference attends to fresh bf16 K/V there; |V| <= 128 * 65504).  out: bf16 or fp32
+ * (out_f32) with the layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
  * chunks.  Hq / H <= 16, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
  * offsets are 32-bit, else KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
  * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device). */

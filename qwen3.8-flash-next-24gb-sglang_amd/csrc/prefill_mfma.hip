@@ -7,21 +7,23 @@
 //
 // Work item = (sequence, KV head, tile of queries), 8 wavefronts (2 per SIMD), heaviest (latest) query tiles
 // first.  A wavefront owns 16 query rows = 16 / gs queries x the gs q heads of the KV head (gs <= 16; rows beyond
-// 16 / gs * gs idle).  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE into LDS as bf16
-// (each thread 16 channels of a K row and 8 channels of two V rows, the V rows transposed), with the next tile's codes already
+// 16 / gs * gs idle).  The block walks the keys in tiles of 32 positions.  All 512 threads dequantize a tile ONCE
+// into LDS (each thread 16 channels of a K row and 8 channels of two V rows), with the next tile's codes already
 // loaded into registers during the matrix work on the current one; the eight wavefronts then reuse it for their
 // 16 rows each (dequantizing per query row is what made the reference's fused kernel slow,
 // docs/KV_PAGED_PREFIX_PLAN.md:188-191).
-//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 channels from LDS, B = Q (the wavefront's 16 rows)
-//   held in registers as the input bf16 values; the fp32 scores are scaled by scale * log2(e).  The D
-//   layout puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values
-//   are directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
-//   O += P V on the same instruction: B = V^T rows from LDS (one 16-byte read per 16-dim column block); P enters
-//   as a bf16 high part and a bf16 remainder (two products), ~16 significant bits.
-// Numerics: the K/V operands are exactly the oracle's rows, bf16(code * scale) rounded to nearest even from the
-// exact fp32 product (or the chunk's own bf16 K/V); Q exact; fp32 accumulation and softmax; bf16 (as the reference)
-// or fp32 output.  Every value of the clamp regime (scale 65504, |code * scale| up to 127 * 65504) is finite in
-// bf16.
+//   S^T = K Q^T on v_mfma_f32_16x16x32_bf16: A = 16 K rows x 32 channels from LDS (bf16), B = Q (the wavefront's 16
+//   rows) held in registers as the input bf16 values; the fp32 scores are scaled by scale * log2(e).  The D layout
+//   puts 4 keys of one query row in each lane: row max / sum need two cross-lane steps, and the lane's P values are
+//   directly the A operand of P.V (k = keys {4 kb .. +3, 16 + 4 kb .. +3}).
+//   O += P V / 128 on v_mfma_f32_16x16x32_f16: A = P rounded to fp16, B = V rows from LDS in fp16, each value the
+//   bf16 row value / 128 (two transposing 8-byte reads per 16-dim column block).  The reference's kernel rounds P to
+//   bf16 for its P.V product (patches/kv_paged_prefix.py:251-252); fp16 keeps 11 significant bits, and the row sum
+//   adds the rounded P, so the output is a weighted mean with exactly the weights of the products.
+// Numerics: K operands are exactly the oracle's rows, bf16(code * scale) rounded to nearest even from the exact fp32
+// product (or the chunk's own bf16 K/V); V operands the same values / 128 in fp16, exact for |v| >= 2^-10 up to
+// 65504 * 128 (every clamp-regime value, |code * scale| <= 127 * 65504) and to 2^-18 below; Q exact; fp32
+// accumulation and softmax; bf16 (as the reference) or fp32 output.  The bf16 source must keep |V| <= 65504 * 128.
 
 #include "kvt_common.h"
 
@@ -33,6 +35,7 @@ typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
 typedef float f2v __attribute__((ext_vector_type(2)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef short s4v __attribute__((ext_vector_type(4)));
@@ -87,6 +90,7 @@ struct __align__(16) Lds {
 };
 
 KVT_DEV f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
 
 // max of two scores in one v_max_f32: written as asm, the compiler adds no canonicalizing v_max_f32 x, x, x for
 // values out of a lane permute (the scores are finite or -inf, never NaN)
@@ -314,6 +318,11 @@ KVT_DEV void fetch_v_tile(const Tier& T, const int32_t* lpages, int t2, const Fe
 // h = 1024 + (c + o) (bits 0x6400 | (c + o)); v_fma_mix_f32 converts h and the fp16 scale s to fp32 and computes
 // h * s - (1024 + o) * s in one rounding, whose exact value c * s is representable (4 or 8 bits times the scale's
 // 11), so the result is the oracle's fp32 product; v_cvt_pk_bf16_f32 then rounds it to nearest even.
+// V operands (VH) are fp16 for the P.V products: the magic value 0x4800 | (c + o) = 8 + (c + o) / 128 gives the
+// exact product c * s / 128, v_cvt_pk_bf16_f32 rounds it (rounding commutes with the power-of-two scale) and
+// v_cvt_pk_f16_f32 carries the 8-bit significand over unchanged: fp16 holds bf16(c * s) / 128 exactly for
+// |bf16(c * s)| in [2^-10, 65504 * 128] (every clamp-regime value, up to bf16(127 * 65504) / 128 = 65024, included;
+// below 2^-7 as subnormals of spacing 2^-24), and to within 2^-18 (in units of the row) below 2^-10.
 KVT_DEV float mix(uint32_t w, int half, _Float16 s, float c) {
   return fmaf((float)__builtin_bit_cast(h2v, w)[half], (float)s, c);
 }
@@ -326,24 +335,48 @@ KVT_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
 }
 KVT_DEV _Float16 half_of(uint32_t bits) { return __builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu)); }
 
+// fp16 pair, round to nearest even (one v_cvt_pk_f16_f32): lo in bits 0-15.
+KVT_DEV uint32_t h2(float lo, float hi) { return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){lo, hi}, h2v)); }
+// fp16 pair of bf16(lo), bf16(hi).
+KVT_DEV uint32_t bf_h2(float lo, float hi) {
+  const uint32_t b = bf2(lo, hi);
+  return h2(__uint_as_float(b << 16), __uint_as_float(b & 0xffff0000u));
+}
+template <bool VH>
+KVT_DEV uint32_t pair_out(float lo, float hi) { return VH ? bf_h2(lo, hi) : bf2(lo, hi); }
+// -(magic base + o) * s: INT4 o = 8, INT8 o = 128
+template <bool VH>
+KVT_DEV float bias4(_Float16 s) { return (VH ? -8.0625f : -1032.0f) * (float)s; }
+template <bool VH>
+KVT_DEV float bias8(_Float16 s) { return (VH ? -9.0f : -1152.0f) * (float)s; }
+
 // 8 INT4 codes (one dword; byte j = channel 2 j in the low nibble, 2 j + 1 in the high one, stored as code + 8) ->
-// 4 bf16 pairs in channel order; c = -1032 s.  Word A holds channels 0 / 4, B 1 / 5, C 2 / 6, D 3 / 7.
+// 4 pairs in channel order; c = bias4(s).  Word A holds channels 0 / 4, B 1 / 5, C 2 / 6, D 3 / 7.
+template <bool VH>
 KVT_DEV void int4_pairs(uint32_t w, _Float16 s, float c, uint32_t out[4]) {
-  const uint32_t A = and_or(w, 0x000F000Fu, 0x64006400u), B = and_or(w >> 4, 0x000F000Fu, 0x64006400u);
-  const uint32_t C = and_or(w >> 8, 0x000F000Fu, 0x64006400u), D = and_or(w >> 12, 0x000F000Fu, 0x64006400u);
-  out[0] = bf2(mix(A, 0, s, c), mix(B, 0, s, c));
-  out[1] = bf2(mix(C, 0, s, c), mix(D, 0, s, c));
-  out[2] = bf2(mix(A, 1, s, c), mix(B, 1, s, c));
-  out[3] = bf2(mix(C, 1, s, c), mix(D, 1, s, c));
+  constexpr uint32_t m = VH ? 0x48004800u : 0x64006400u;
+  const uint32_t A = and_or(w, 0x000F000Fu, m), B = and_or(w >> 4, 0x000F000Fu, m);
+  const uint32_t C = and_or(w >> 8, 0x000F000Fu, m), D = and_or(w >> 12, 0x000F000Fu, m);
+  out[0] = pair_out<VH>(mix(A, 0, s, c), mix(B, 0, s, c));
+  out[1] = pair_out<VH>(mix(C, 0, s, c), mix(D, 0, s, c));
+  out[2] = pair_out<VH>(mix(A, 1, s, c), mix(B, 1, s, c));
+  out[3] = pair_out<VH>(mix(C, 1, s, c), mix(D, 1, s, c));
 }
 
-// 4 INT8 codes (one dword) -> 2 bf16 pairs; c = -1152 s.  u = code + 128 per byte; e holds channels 0 / 2, o 1 / 3.
+// 4 INT8 codes (one dword) -> 2 pairs; c = bias8(s).  u = code + 128 per byte; e holds channels 0 / 2, o 1 / 3.
+template <bool VH>
 KVT_DEV void int8_pairs(uint32_t w, _Float16 s, float c, uint32_t out[2]) {
+  constexpr uint32_t m = VH ? 0x48484848u : 0x64646464u;
   const uint32_t u = w ^ 0x80808080u;
-  const uint32_t e = __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u);
-  const uint32_t o = __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u);
-  out[0] = bf2(mix(e, 0, s, c), mix(o, 0, s, c));
-  out[1] = bf2(mix(e, 1, s, c), mix(o, 1, s, c));
+  const uint32_t e = __builtin_amdgcn_perm(m, u, 0x04020400u);
+  const uint32_t o = __builtin_amdgcn_perm(m, u, 0x04030401u);
+  out[0] = pair_out<VH>(mix(e, 0, s, c), mix(o, 0, s, c));
+  out[1] = pair_out<VH>(mix(e, 1, s, c), mix(o, 1, s, c));
+}
+
+// bf16 source pair -> fp16 pair of the values / 128 (exact as above)
+KVT_DEV uint32_t bf_src_h2(uint32_t w) {
+  return h2(__uint_as_float(w << 16) * 0.0078125f, __uint_as_float(w & 0xffff0000u) * 0.0078125f);
 }
 
 // Tier of a tile's dequantization: every key INT4, every key INT8, per key (the tile straddles hot_start), the bf16
@@ -357,15 +390,15 @@ struct TierTag {
 KVT_DEV void k_int8(const RawK& x, uint32_t o[8]) {
   const uint32_t w[4] = {x.b.x, x.b.y, x.b.z, x.b.w};
   const _Float16 s = half_of(x.s8);
-  const float c = -1152.0f * (float)s;
+  const float c = bias8<false>(s);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) int8_pairs(w[i], s, c, o + 2 * i);
+  for (int i = 0; i < 4; ++i) int8_pairs<false>(w[i], s, c, o + 2 * i);
 }
 KVT_DEV void k_int4(const RawK& x, uint32_t o[8]) {
   const _Float16 s = half_of(x.s4);
-  const float c = -1032.0f * (float)s;
-  int4_pairs(x.a4.x, s, c, o);
-  int4_pairs(x.a4.y, s, c, o + 4);
+  const float c = bias4<false>(s);
+  int4_pairs<false>(x.a4.x, s, c, o);
+  int4_pairs<false>(x.a4.y, s, c, o + 4);
 }
 
 // K row fragment -> LDS (bf16, natural order): channels 16 dc .. 16 dc + 15 of key row `key` (2 chunks).
@@ -394,21 +427,21 @@ KVT_DEV void store_k(const RawK& x, uint8_t* row, int key, int dc) {
 
 KVT_DEV void v_int8(const RawV& x, int t, uint32_t o[4]) {
   const _Float16 s = half_of(x.s8[t]);
-  const float cc = -1152.0f * (float)s;
-  int8_pairs(x.a8[t].x, s, cc, o);
-  int8_pairs(x.a8[t].y, s, cc, o + 2);
+  const float cc = bias8<true>(s);
+  int8_pairs<true>(x.a8[t].x, s, cc, o);
+  int8_pairs<true>(x.a8[t].y, s, cc, o + 2);
 }
 KVT_DEV void v_int4(const RawV& x, int t, uint32_t o[4]) {
   const _Float16 s = half_of(x.s4[t]);
-  const float cc = -1032.0f * (float)s;
-  int4_pairs(x.c4[t], s, cc, o);
+  const float cc = bias4<true>(s);
+  int4_pairs<true>(x.c4[t], s, cc, o);
 }
 
-// 8 channels of one V row -> 4 bf16 pairs (natural order).
+// 8 channels of one V row -> 4 fp16 pairs of the values / 128 (natural order).
 template <int TIER>
 KVT_DEV void v_row8(const RawV& x, int t, uint32_t o[4]) {
   if constexpr (TIER == kTierBf16) {
-    o[0] = x.a[t].x, o[1] = x.a[t].y, o[2] = x.a[t].z, o[3] = x.a[t].w;
+    o[0] = bf_src_h2(x.a[t].x), o[1] = bf_src_h2(x.a[t].y), o[2] = bf_src_h2(x.a[t].z), o[3] = bf_src_h2(x.a[t].w);
   } else if constexpr (TIER == kTierInt8) {
     v_int8(x, t, o);
   } else if constexpr (TIER == kTierInt4) {
@@ -452,12 +485,12 @@ KVT_DEV void k_step(int j, const RawK& x, uint32_t o[8], uint8_t* row, int key, 
   if constexpr (TIER == kTierInt8) {
     if (j < 4) {
       const _Float16 s = half_of(x.s8);
-      int8_pairs(word_of(x.b, j), s, -1152.0f * (float)s, o + 2 * j);
+      int8_pairs<false>(word_of(x.b, j), s, bias8<false>(s), o + 2 * j);
     }
   } else if constexpr (TIER == kTierInt4) {
     if (j < 2) {
       const _Float16 s = half_of(x.s4);
-      int4_pairs(j == 0 ? x.a4.x : x.a4.y, s, -1032.0f * (float)s, o + 4 * j);
+      int4_pairs<false>(j == 0 ? x.a4.x : x.a4.y, s, bias4<false>(s), o + 4 * j);
     }
   } else if constexpr (TIER == kTierBf16) {
     if (j == 0) {
@@ -486,7 +519,7 @@ KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t*
     if (j < 4) {
       const int t = j >> 1, hw = j & 1;
       const _Float16 s = half_of(x.s8[t]);
-      int8_pairs(hw ? x.a8[t].y : x.a8[t].x, s, -1152.0f * (float)s, (t ? b : a) + 2 * hw);
+      int8_pairs<true>(hw ? x.a8[t].y : x.a8[t].x, s, bias8<true>(s), (t ? b : a) + 2 * hw);
     }
   } else if constexpr (TIER == kTierInt4) {
     if (j < 2) v_int4(x, j, j ? b : a);
@@ -667,8 +700,9 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
           s[nt][r] = (kp <= qp && kp < kend) ? s[nt][r] : -INFINITY;
         }
     }
-    // ---- online softmax; P as the A operand of P.V (bf16 high part pa, remainder pb)
-    bf8 pa, pb;
+    // ---- online softmax; P as the A operand of P.V (fp16, rounded to nearest even; the row sum l adds the rounded
+    // values, so the weights of the output are exactly the weights of the products)
+    h8 pa;
     {
       float mloc = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), s[0][3], s[1][0]);
       mloc = vmax(vmax3(mloc, s[1][1], s[1][2]), s[1][3]);
@@ -690,40 +724,33 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       }
       // rows with no visible key yet keep m = -inf and contribute nothing
       const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float psum = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          s[nt][r] = __builtin_amdgcn_exp2f(fmaf(s[nt][r], qmul, -m_use));
-          psum += s[nt][r];
-        }
-      l_run += psum;
-      uint32_t hw[4], lw[4];
+        for (int r = 0; r < 4; ++r) s[nt][r] = __builtin_amdgcn_exp2f(fmaf(s[nt][r], qmul, -m_use));
+      uint32_t hw[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x0 = s[i >> 1][2 * (i & 1)], x1 = s[i >> 1][2 * (i & 1) + 1];
-        hw[i] = bf2(x0, x1);
-        lw[i] = bf2(x0 - __uint_as_float(hw[i] << 16), x1 - __uint_as_float(hw[i] & 0xffff0000u));
+        hw[i] = h2(s[i >> 1][2 * (i & 1)], s[i >> 1][2 * (i & 1) + 1]);
+        l_run = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, hw[i]), h2v{1.0f16, 1.0f16}, l_run, false);
       }
-      pa = __builtin_bit_cast(bf8, u4v{hw[0], hw[1], hw[2], hw[3]});
-      pb = __builtin_bit_cast(bf8, u4v{lw[0], lw[1], lw[2], lw[3]});
+      pa = __builtin_bit_cast(h8, u4v{hw[0], hw[1], hw[2], hw[3]});
     }
-    // ---- O += P V: B = dim 16 c + n16 of keys {4 kb .. +3, 16 + 4 kb .. +3}: two transposing 8-byte reads.
-    // Step c: the high-part product of dims 16 c .., the remainder product of dims 16 (c - 1) .., the V operand of
-    // step c + kAheadV read from LDS, one piece of tile it + 1's V rows.
+    // ---- O += P V / 128: B = dim 16 c + n16 of keys {4 kb .. +3, 16 + 4 kb .. +3}: two transposing 8-byte reads.
+    // Step c: the product of dims 16 c .., the V operand of step c + kAheadV read from LDS, one piece of tile
+    // it + 1's V rows.
     {
       constexpr bool kDq = TIER != kTierNone;
       const uint8_t* vbuf = lds.v[cb];
       uint8_t* v_next = lds.v[cb ^ 1];
       uint32_t va[4], vb[4];
-      bf8 vf[16];
+      h8 vf[16];
       auto vread = [&](int c) {
         const uint32_t a0 = (uint32_t)(uintptr_t)(vbuf + vlane + 32 * c);
         const auto lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(uintptr_t)a0);
         const auto hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(uintptr_t)(a0 + 16u * kVRow));
-        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-        vf[c] = __builtin_bit_cast(bf8, u4v{l2.x, l2.y, h2.x, h2.y});
+        const uint2 lw = __builtin_bit_cast(uint2, lo), hw = __builtin_bit_cast(uint2, hi);
+        vf[c] = __builtin_bit_cast(h8, u4v{lw.x, lw.y, hw.x, hw.y});
       };
 #pragma unroll
       for (int c = 0; c < kAheadV; ++c) vread(c);
@@ -731,14 +758,12 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
       for (int c = 0; c < 16; ++c) {
         if (c + kAheadV < 16) vread(c + kAheadV);
         acc[c] = mfma(pa, vf[c], acc[c]);
-        if (c > 0) acc[c - 1] = mfma(pb, vf[c - 1], acc[c - 1]);
         if constexpr (kDq) {
           v_step<TIER>(c, rv_next, va, vb, v_next, db, tp);
           if (c == kFetchV<TIER>) fetch_v_tile<FETCH, G8, BF16>(T, lds.pages, t2, FL, tp, db, rv_next);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      acc[15] = mfma(pb, vf[15], acc[15]);
     }
     __syncthreads();   // tile it + 1 is in LDS for everyone; nobody reads this tile's buffer any more
     ++it;
@@ -784,11 +809,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
         if (out_f32) {
           float* orow = reinterpret_cast<float*>(out) + o0;
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[c][i] / lr;
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = (acc[c][i] * 128.0f) / lr;
         } else {
           uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[c][i] / lr);
+          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne((acc[c][i] * 128.0f) / lr);
         }
       }
     }
