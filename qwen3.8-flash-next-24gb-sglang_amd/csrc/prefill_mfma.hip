@@ -705,12 +705,12 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     h8 pa;
     {
       float mloc = vmax3(vmax3(s[0][0], s[0][1], s[0][2]), s[0][3], s[1][0]);
-      mloc = vmax(vmax3(mloc, s[1][1], s[1][2]), s[1][3]);
-      mloc = vmax_xor16_32(mloc) * qmul;   // log2 units
+      mloc = vmax(vmax3(mloc, s[1][1], s[1][2]), s[1][3]) * qmul;   // this lane's 8 keys, log2 units
       // lazy rescale: the reference max moves (and the accumulators are rescaled) only when a row's max exceeds it
-      // by more than 8 (log2 units), so P = 2^(s qmul - m) <= 256
-      const float m_new = vmax(m_run, mloc);
-      if (__any(m_new > m_run + 8.0f)) {
+      // by more than 8 (log2 units), so P = 2^(s qmul - m) <= 256.  A row's max exceeds it iff one of the row's four
+      // lanes (n16 + 16 kb) does, so the cross-lane max is taken only then, for every row (m stays uniform per row).
+      if (__any(mloc > m_run + 8.0f)) {
+        const float m_new = vmax(m_run, vmax_xor16_32(mloc));
         const float alpha = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
         float arow[4];
