@@ -11,8 +11,8 @@ us/token over all layers, the roofline of the decode kernel (live HIP-event timi
 oracle timed on a bounded sample (one layer at the full context) as the baseline; its output also checks layer 0
 of the timed path against the oracle ("parity").  The same line carries "configs": compact figures of the other
 configurations (chunked prefill, quantize-append, decode with append, ragged decode, top-k sparse decode at 16 / 2
-and 24 / 2 heads, dense decode over the slot-indexed pool), measured after the headline; --no-sub-configs leaves them
-out.
+and 24 / 2 heads, dense decode over the slot-indexed pool, paged prefix-chunk attention at the reference's published
+timing case), measured after the headline; --no-sub-configs leaves them out.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--impl mfma|ref]
 """
@@ -591,6 +591,133 @@ def slots_workload(args) -> dict:
     }
 
 
+def _indexer_rows(q_len: int, prefix: int, topk: int, gen: torch.Generator) -> torch.Tensor:
+    """Index rows shaped like the indexer's output for a chunk of q_len queries after `prefix` positions (the timing
+    case of gemv/test_kv_paged_prefix.py:306-331): per query sorted distinct positions below its visible length,
+    -1 padding; about 3 % of the rows empty, 3 % only current-chunk positions, 4 % one position (at most 8 each) and
+    15 % a random shorter selection."""
+    idx = torch.full((q_len, topk), -1, dtype=torch.int32)
+    special = {"empty": 0, "chunk_only": 0, "single": 0}
+    for j in range(q_len):
+        visible = prefix + j + 1
+        n = min(topk, visible)
+        u = float(torch.rand(1, generator=gen))
+        if u < 0.03 and special["empty"] < 8:
+            special["empty"] += 1
+            continue
+        if u < 0.06 and prefix > 0 and special["chunk_only"] < 8:
+            special["chunk_only"] += 1
+            pos = torch.arange(prefix, visible)[:n]
+        elif u < 0.10 and special["single"] < 8:
+            special["single"] += 1
+            pos = torch.randint(0, visible, (1,), generator=gen)
+        else:
+            if u < 0.25:
+                n = int(torch.randint(0, n + 1, (1,), generator=gen))
+            pos = torch.randperm(visible, generator=gen)[:n].sort().values
+        idx[j, :pos.numel()] = pos.to(torch.int32)
+    return idx
+
+
+def paged_prefix_workload(args) -> dict:
+    """The reference's published timing case of its paged prefix-chunk attention (gemv/test_kv_paged_prefix.py:539-611;
+    figures in patches/kv_paged_prefix.py:42-45): one request with a 60,000-token prefix and a 1,024-query chunk,
+    1 KV head x 12 q heads, D 256, tiered pool (INT8-G64 ring of 8,192 rows over INT4-G32; position p in slot p, so
+    the newest 8,192 slots own the ring), topk 2,051 with the indexer-like rows of _indexer_rows.  Times
+    sparse_gqa_fwd_interface_paged: device time per call (HIP graph of back-to-back calls) and, as the reference
+    measures, the median host time of a synchronized call.  Byte model (the reference's): each valid selection's K
+    and V rows from the tier that serves it + 12 B of index, slot and owner reads.  Synthetic random codes and
+    scales; the CPU baseline (the oracle on 8 sampled queries) also gives the max-abs difference of those queries."""
+    import kvtier  # noqa: F401
+    from kvtier import sparse_attn as sa
+    PREFIX, CHUNK, R, TOPK, QH = 60_000, 1024, 8192, 2051, 12
+    ctx = PREFIX + CHUNK
+    h1 = 1
+    g = torch.Generator(device="cuda").manual_seed(51)
+    gc = torch.Generator().manual_seed(51)
+    pool = dict(
+        k4=torch.randint(0, 256, (ctx, h1, D // 2), dtype=torch.uint8, device="cuda", generator=g),
+        v4=torch.randint(0, 256, (ctx, h1, D // 2), dtype=torch.uint8, device="cuda", generator=g),
+        ks4=(0.05 + 0.3 * torch.rand(ctx, h1, D // 32, device="cuda", generator=g)).half(),
+        vs4=(0.05 + 0.3 * torch.rand(ctx, h1, D // 32, device="cuda", generator=g)).half(),
+        rk=torch.randint(-127, 128, (R, h1, D), dtype=torch.int8, device="cuda", generator=g),
+        rv=torch.randint(-127, 128, (R, h1, D), dtype=torch.int8, device="cuda", generator=g),
+        rks=(0.002 + 0.02 * torch.rand(R, h1, D // 64, device="cuda", generator=g)).half(),
+        rvs=(0.002 + 0.02 * torch.rand(R, h1, D // 64, device="cuda", generator=g)).half())
+    rows = torch.arange(R, dtype=torch.int64)
+    owner = torch.where(rows < ctx % R, rows + (ctx // R) * R, rows + (ctx // R - 1) * R).to(torch.int32).to("cuda")
+    r2t = torch.arange(ctx, dtype=torch.int32, device="cuda").reshape(1, ctx)
+    req_idx = torch.zeros(1, dtype=torch.int64, device="cuda")
+    kv_lens = torch.tensor([ctx], dtype=torch.int32, device="cuda")
+    cu_q = torch.tensor([0, CHUNK], dtype=torch.int64, device="cuda")
+    idx_cpu = _indexer_rows(CHUNK, PREFIX, TOPK, gc)
+    idx = idx_cpu.to("cuda")
+    sm_k = (0.5 + torch.rand(h1, D, device="cuda", generator=g)).half()
+    sm_v = (0.5 + torch.rand(h1, D, device="cuda", generator=g)).half()
+    q = (torch.randn(CHUNK, QH, D, device="cuda", generator=g) / 4).to(torch.bfloat16)
+    out = torch.empty(CHUNK, QH, D, dtype=torch.float32, device="cuda")
+
+    def call():
+        sa.sparse_gqa_fwd_interface_paged(q, idx, cu_q, kv_lens, r2t, req_idx, pool["k4"], pool["v4"], pool["ks4"],
+                                          pool["vs4"], sm_k, sm_v, D ** -0.5, CHUNK, 4, pool["rk"], pool["rv"],
+                                          pool["rks"], pool["rvs"], owner, R - 1, out=out)
+
+    t_dev = _graph_time(call, args.warmup, max(args.steps, 10))
+    host = []
+    for _ in range(10):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        call()
+        torch.cuda.synchronize()
+        host.append(time.perf_counter() - t0)
+    t_host = sorted(host)[len(host) // 2]
+    sel = idx_cpu[idx_cpu >= 0].long()               # every entry is below its query's visible length here
+    hot = owner.cpu().long()[sel & (R - 1)] == sel
+    n_sel, n_hot = sel.numel(), int(hot.sum())
+    row4, row8 = 2 * (D // 2 + 2 * (D // 32)), 2 * (D + 2 * (D // 64))
+    kv_bytes = h1 * ((n_sel - n_hot) * row4 + n_hot * row8) + 12 * n_sel
+    flops = 4.0 * D * QH * n_sel
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import ref
+        cores = _cpu_threads()
+        cp = {k: v.cpu() for k, v in pool.items()}
+        own, qc, smk, smv, oc = owner.cpu(), q.cpu(), sm_k.cpu(), sm_v.cpu(), out.cpu()
+        sample = [j for j in range(CHUNK - 1, -1, -127)][:8]
+        err = 0.0
+        t0 = time.perf_counter()
+        for j in sample:
+            slots = ref.prefill_selected_positions(idx_cpu[j], PREFIX + j + 1, ctx, TOPK)
+            kk, vv = ref.dequant_slots_tiered(slots, cp["k4"], cp["v4"], cp["ks4"], cp["vs4"], cp["rk"], cp["rv"],
+                                              cp["rks"], cp["rvs"], own, R - 1, smk, smv)
+            o = ref.attention_rows(qc[j], kk, vv, D ** -0.5)
+            err = max(err, float((o - oc[j]).abs().nan_to_num(0.0).max()))
+        dt = time.perf_counter() - t0
+        cpu = dict(value=round(dt / len(sample) * 1e3, 3), unit="ms per query", cores=cores, kind="port",
+                   sample=f"oracle/ref.py prefill_selected_positions + dequant_slots_tiered + attention_rows of "
+                          f"{len(sample)} queries of the chunk ({dt * 1e3:.1f} ms); max-abs vs the GPU rows {err:.2e}")
+    return {
+        "metric": "paged prefix-chunk attention over the tiered pool (prefix 60,000, chunk 1,024, 1 KV head x 12 "
+                  "q heads, topk 2,051): ms per call",
+        "value": round(t_dev * 1e3, 4), "unit": "ms", "higher_is_better": False, "steps": max(args.steps, 10),
+        "warmup": args.warmup, "dtype": "bf16-mfma/f32", "data": "synthetic",
+        "config": {"workload": "the reference's paged-prefix timing case: 1 request, prefix 60,000 + chunk 1,024 "
+                               "queries, 1 KV head x 12 q heads, D 256, tiered pool (INT8-G64 ring 8,192 over "
+                               "INT4-G32), topk 2,051, indexer-like rows",
+                   "selected_rows": n_sel, "hot_fraction": round(n_hot / max(n_sel, 1), 4)},
+        "host_median_ms_per_synchronized_call": round(t_host * 1e3, 4),
+        "reference_published_ms": {"paged_tiered": 6.10, "paged_int8": 3.19, "paged_int4": 4.21,
+                                   "materialised_gather_plus_kernel": 1.31,
+                                   "hardware": "RTX PRO 4000 Blackwell (~0.5 TB/s)"},
+        "kv_bytes_per_call": kv_bytes,
+        "TFLOPs": round(flops / t_dev / 1e12, 2),
+        "roofline": {"bound": "hbm", "achieved": round(kv_bytes / t_dev / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": round(kv_bytes / t_dev / PEAK_HBM, 4), "traffic": None,
+                     "kernel": "sparse_prefill (row requests; the 35 MB pool itself stays in the caches)"},
+        "cpu_baseline": cpu,
+    }
+
+
 def lazy_workload(args) -> dict:
     """Lazy backing of the tiered slot pool on HIP virtual memory at the full context: 262,144 slots x 12 layers
     (2 KV heads, D 256; INT8 ring of 8,192 rows eagerly allocated).  Times, host wall with the device synchronized:
@@ -857,7 +984,8 @@ def sub_configs(args) -> dict:
     """Compact figures of the other configurations, measured in the same process after the headline (whose cache
     is freed first): chunked prefill of a 10,001-token prompt, the 8,192-token quantize-append with eviction, decode
     with append at a 10,001-token context, ragged 8-sequence decode, the top-k sparse decode at 16 / 2 and 24 / 2
-    heads, and the dense decode over the slot-indexed pool.  Each runs without its CPU baseline; a failure is reported in place of its figures."""
+    heads, the dense decode over the slot-indexed pool and the paged prefix-chunk attention at the reference's published
+    timing case.  Each runs without its CPU baseline; a failure is reported in place of its figures."""
     sub = argparse.Namespace(**vars(args))
     sub.no_cpu_baseline, sub.steps, sub.warmup = True, 5, 1
     res = {}
@@ -892,6 +1020,10 @@ def sub_configs(args) -> dict:
     run("slots_dense_4x65k", slots_workload,
         lambda r: {"us_per_step": r["value"], "GBps": r["roofline"]["achieved"], "hbm_frac": r["roofline"]["frac"],
                    "scalar_kernel_us_per_step": r["scalar_kernel_us_per_step"]})
+    run("paged_prefix_60k", paged_prefix_workload,
+        lambda r: {"ms_per_call": r["value"], "host_ms": r["host_median_ms_per_synchronized_call"],
+                   "TFLOPs": r["TFLOPs"], "row_GBps": r["roofline"]["achieved"],
+                   "reference_published_ms": r["reference_published_ms"]["paged_tiered"]})
     return res
 
 
@@ -904,7 +1036,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fused-combine", action="store_true",
                     help="merge the split partials inside the split-K launch instead of in the combine kernel")
-    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "slots", "lazy"],
+    ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "slots", "paged_prefix", "lazy"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--hq", type=int, default=HQ, help="query heads of the sparse workload (2 KV heads)")
     ap.add_argument("--no-sub-configs", action="store_true",
@@ -926,7 +1058,8 @@ def main():
     if args.workload != "decode262k":
         fn = {"prefill10k": prefill_workload, "decode10k": lambda a: decode_steps_workload(a, False),
               "ragged": lambda a: decode_steps_workload(a, True), "append": append_workload,
-              "sparse": sparse_workload, "slots": slots_workload, "lazy": lazy_workload}[args.workload]
+              "sparse": sparse_workload, "slots": slots_workload, "paged_prefix": paged_prefix_workload,
+              "lazy": lazy_workload}[args.workload]
         line = fn(args)
         line["n_gpus"] = 1
         print(json.dumps(line))

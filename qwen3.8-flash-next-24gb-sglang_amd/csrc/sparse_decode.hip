@@ -102,17 +102,46 @@ KVT_DEV __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// The 4 codes of this lane's channels in a loaded word: INT8 rows give 4 bytes; INT4 rows give the 16-bit half
-// (lane & 1) of the dword holding channel pairs 4 (lane >> 1) .. + 3 (low nibble = even channel).
-KVT_DEV void codes4(bool hot, uint32_t w, int lane, float c[4]) {
+// Channels 4 lane .. 4 lane + 3 of one row, dequantized: bf16((c * s) * sm) for code c, the row's fp16 scale s
+// (bits sbits) and the channel's smoothing factor sm, as the gathers write them.  INT8 rows give 4 codes in the
+// loaded word; INT4 rows the 16-bit half (lane & 1) of the word holding channel pairs 4 (lane >> 1) .. + 3 (low
+// nibble = even channel), stored as c + 8.  A code with offset o (c + o >= 0) goes into the mantissa of an fp16 magic
+// value h = 1024 + (c + o) (v_perm_b32 for bytes, v_and_or_b32 for nibble pairs); v_fma_mix_f32 converts h and s and
+// computes h * s - (1024 + o) * s in one rounding, whose exact value c * s is representable (4 or 8 bits times the
+// scale's 11), so the fp32 product equals the plain c * s; the smoothing factor then multiplies in fp32 and
+// v_cvt_pk_bf16_f32 rounds each pair to nearest even.
+KVT_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(o));
+  return r;
+}
+KVT_DEV float mix(uint32_t w, int half, _Float16 s, float c) {
+  typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+  return fmaf((float)__builtin_bit_cast(h2v, w)[half], (float)s, c);
+}
+KVT_DEV uint2 dequant4(bool hot, uint32_t w, uint32_t sbits, int lane, const float sm[4]) {
+  const _Float16 s = __builtin_bit_cast(_Float16, (uint16_t)(sbits & 0xffffu));
+  uint32_t a, b;   // fp16 magic pairs: hot a = channels (0, 2), b = (1, 3); INT4 a = (0, 1), b = (2, 3)
+  float c;
   if (hot) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = (float)(int8_t)(w >> (8 * i));
+    const uint32_t u = w ^ 0x80808080u;
+    a = __builtin_amdgcn_perm(0x64646464u, u, 0x04020400u);
+    b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030401u);
+    c = -1152.0f * (float)s;
   } else {
-    const uint32_t h16 = w >> (16 * (lane & 1));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = (float)((int)((h16 >> (4 * i)) & 15u) - 8);
+    const uint32_t h = (w >> (16 * (lane & 1))) & 0xffffu;
+    const uint32_t x = h | (h << 12);   // nibble 1 at bits 16-19, nibble 3 at bits 24-27
+    a = and_or(x, 0x000F000Fu, 0x64006400u);
+    b = and_or(x >> 8, 0x000F000Fu, 0x64006400u);
+    c = -1032.0f * (float)s;
   }
+  float v[4];
+  if (hot) {
+    v[0] = mix(a, 0, s, c), v[1] = mix(b, 0, s, c), v[2] = mix(a, 1, s, c), v[3] = mix(b, 1, s, c);
+  } else {
+    v[0] = mix(a, 0, s, c), v[1] = mix(a, 1, s, c), v[2] = mix(b, 0, s, c), v[3] = mix(b, 1, s, c);
+  }
+  return uint2{bf16x2(v[0] * sm[0], v[1] * sm[1]), bf16x2(v[2] * sm[2], v[3] * sm[3])};
 }
 
 // One tile's raw row data for this lane (channels 4 lane .. + 3 of K and V, and their scales).
@@ -248,15 +277,8 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   // K rows into this wavefront's LDS rows (row-major); a wavefront's LDS accesses complete in order, so these
   // stores land after the previous tile's V reads
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const bool ht = (T.fl[r] & 2) != 0;
-    float c[4], x[4];
-    codes4(ht, T.kw[r], lane, c);
-    const float sk = f16_bits_to_f32((uint16_t)T.ks[r]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = c[i] * sk * smk[i];
-    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
-  }
+  for (int r = 0; r < kRows; ++r)
+    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = dequant4((T.fl[r] & 2) != 0, T.kw[r], T.ks[r], lane, smk);
   hook(1);
   // S^T = K Q^T: lane l holds rows 4 (l >> 4) + i of q head l & 15
   f4 s = {0.f, 0.f, 0.f, 0.f};
@@ -269,15 +291,8 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   hook(2);
   // V rows into the same LDS rows (the stores stay behind the K reads above, which may alias them)
 #pragma unroll
-  for (int r = 0; r < kRows; ++r) {
-    const bool ht = (T.fl[r] & 2) != 0;
-    float c[4], x[4];
-    codes4(ht, T.vw[r], lane, c);
-    const float sv = f16_bits_to_f32((uint16_t)T.vs[r]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = c[i] * sv * smv[i];
-    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = uint2{bf16x2(x[0], x[1]), bf16x2(x[2], x[3])};
-  }
+  for (int r = 0; r < kRows; ++r)
+    *reinterpret_cast<uint2*>(&kt[r * kKPitch + 4 * lane]) = dequant4((T.fl[r] & 2) != 0, T.vw[r], T.vs[r], lane, smv);
   // online softmax (log2 units): rows 4 kq + i of this lane's head, the other 12 rows in lanes n16 + 16 j
   constexpr float kLog2e = 1.4426950408889634f;
   const float cs = A.scale * kLog2e;
@@ -298,10 +313,16 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   }
   l_run = l_run * alpha + sum_xor16_32(lsum);
   m_run = m_new;
-  // o[n][i] is head 4 kq + i: its rescale factor lives in lane 4 kq + i
-  float ai[4];
+  // o[n][i] is head 4 kq + i: its rescale factor lives in lane 4 kq + i; only when some head's max has grown
+  if (__any(alpha != 1.0f)) {
+    float ai[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, 4 * kq + i, 64);
+    for (int i = 0; i < 4; ++i) ai[i] = __shfl(alpha, 4 * kq + i, 64);
+#pragma unroll
+    for (int n = 0; n < 16; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[n][i] *= ai[i];
+  }
   // P as bf16 high part + bf16 remainder (two products per step): P keeps ~16 significant bits, against 8 for a
   // plain bf16 cast, so a peaked softmax stays within the fp32 reference's tolerance
   const uint32_t h01 = bf16x2(p[0], p[1]), h23 = bf16x2(p[2], p[3]);
@@ -317,10 +338,7 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   for (int n = 0; n < 16; ++n) {
     const bf4 vop = __builtin_bit_cast(
         bf4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(uintptr_t)(vbase + 32u * (uint32_t)n)));
-    f4 acc = o[n];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] *= ai[i];
-    o[n] = mfma_bf16(pb, vop, mfma_bf16(pa, vop, acc));
+    o[n] = mfma_bf16(pb, vop, mfma_bf16(pa, vop, o[n]));
   }
 }
 
@@ -363,9 +381,9 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
 
   const int64_t req = load_idx(A.req_indices, A.req64, b);
   const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
-  // decode: the wavefront's one tile is resolved first, so that its chain of dependent loads runs beside the Q copy
+  // the wavefront's first tile is resolved first, so that its chain of dependent loads runs beside the Q copy
   TileCols tc0{};
-  const bool has_tile = !ROWS && c_begin + kRows * wave < c_end;
+  const bool has_tile = c_begin + kRows * wave < c_end;
   if (has_tile) tc0 = resolve_tile<KIND, G8>(A, c_begin + kRows * wave, c_end, idx_row, L, req, h, lane);
   // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
 #pragma unroll
@@ -410,12 +428,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
   f4 o[16];                               // O[head 4 (lane >> 4) + i][channel 16 n + (lane & 15)]
 #pragma unroll
   for (int n = 0; n < 16; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (ROWS) {
-    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
-      const TileCols tc = resolve_tile<KIND, G8>(A, c0, c_end, idx_row, L, req, h, lane);
-      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
-    }
-  } else if constexpr (MULTI) {
+  if constexpr (ROWS || MULTI) {
     // tiles c_begin + 16 wave + 64 k: the next tile's position, slot and owner loads go out beside this tile's
     // loads and math (for the last tile they have no active lane)
     TileCols tc = tc0;
