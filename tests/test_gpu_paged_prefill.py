@@ -177,3 +177,29 @@ def test_paged_prefill_per_head_indices(kvt_pkg):
     p = slot_pools(slots, R, 64, gen)
     c = _case(gen, [0, 3000, 1500], [96, 120, 64], slots, 16, per_head=True, topk=700)
     close(_run(c, "tiered", p, R, f32=True), _oracle(c, "tiered", p, R, 64))
+
+
+def test_paged_prefill_reference_timing_shape(kvt_pkg):
+    """The shape of the reference's published timing case (gemv/test_kv_paged_prefix.py:539-546): one request with a
+    60,000-position prefix and a 1,024-query chunk, 1 KV head x 12 q heads, tiered pool whose ring of 8,192 rows is
+    owned by the newest 8,192 slots (position p in slot p), topk 2,051 with indexer-like rows.  Sampled queries (the
+    first, the last, spread between, single-position and empty rows) against the oracle."""
+    gen = torch.Generator().manual_seed(61)
+    prefix, chunk, R, hq = 60_000, 1024, 8192, 12
+    ctx = prefix + chunk
+    p = slot_pools(ctx, R, 64, gen, H=1)
+    rows = torch.arange(R)
+    p["owner"] = torch.where(rows < ctx % R, rows + (ctx // R) * R, rows + (ctx // R - 1) * R).to(torch.int32)
+    c = _case(gen, [prefix], [chunk], ctx, hq)
+    got = _run(c, "tiered", p, R, f32=True)
+    empty = [j for j in range(chunk) if int(c["idx"][j, 0]) < 0][:2]
+    singles = [r for r, _, _, _ in c["singles"]][:2]
+    sample = sorted(set([0, 1, 2, chunk - 2, chunk - 1] + list(range(97, chunk, 101)) + empty + singles))
+    slot_row = c["r2t"][int(c["req_idx"][0])]
+    exp = torch.empty(len(sample), hq, D)
+    for i, j in enumerate(sample):
+        pos = ref.prefill_selected_positions(c["idx"][j], prefix + j + 1, ctx, TOPK)
+        kk, vv = slot_rows("tiered", p, slot_row[pos].long(), R, 64)
+        exp[i] = ref.attention_rows(c["q"][j], kk, vv, D ** -0.5)
+    assert empty and singles
+    close(got[sample], exp)
