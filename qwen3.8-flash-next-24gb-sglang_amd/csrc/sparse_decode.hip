@@ -160,13 +160,17 @@ struct PoolRsrc {
 // Issue the loads of the wavefront's tile: row r's byte offsets (codes and scales, in the row's tier) come from
 // lane r by readlane and go in the scalar offset of the loads, so every row costs a few scalar instructions and no
 // vector address math; the lane offsets are fixed per tier.
-template <int G8>
+// TIERS: the tile's rows are all INT8 (kRowsInt8), all INT4 (kRowsInt4) or each in its own tier (kRowsMixed: a
+// wavefront-uniform branch per row).
+enum { kRowsInt8 = 0, kRowsInt4 = 1, kRowsMixed = 2 };
+
+template <int G8, int TIERS>
 KVT_DEV void issue_tile(const PoolRsrc& P, int flags, uint32_t coff, uint32_t soff, int lane, TileLoads& L) {
   const uint32_t off8 = 4u * lane, off4 = 4u * (lane >> 1);
   const uint32_t soff8 = 2u * ((4u * lane) / G8), soff4 = 2u * (lane >> 3);
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
-    const int f = __builtin_amdgcn_readlane(flags, r);
+    const int f = TIERS == kRowsMixed ? __builtin_amdgcn_readlane(flags, r) : (TIERS == kRowsInt8 ? 2 : 0);
     L.fl[r] = f;
     const uint32_t co = (uint32_t)__builtin_amdgcn_readlane((int)coff, r);
     const uint32_t so = (uint32_t)__builtin_amdgcn_readlane((int)soff, r);
@@ -264,7 +268,7 @@ struct Resolver {
 // online softmax, O += P V.
 // hook(k) runs other work at three points: k = 0 before the tile's loads, 1 after its K rows are in LDS, 2 after
 // S^T.
-template <int KIND, int G8, typename Hook>
+template <int KIND, int G8, int TIERS, typename Hook>
 KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt, const TileCols& tc,
                          int lane, const float smk[4], const float smv[4], float& m_run, float& l_run, f4 o[16],
                          Hook&& hook) {
@@ -272,7 +276,7 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   const int flags = tc.flags;
   TileLoads T;
   hook(0);
-  issue_tile<G8>(P, flags, tc.coff, tc.soff, lane, T);
+  issue_tile<G8, TIERS>(P, flags, tc.coff, tc.soff, lane, T);
 
   // K rows into this wavefront's LDS rows (row-major); a wavefront's LDS accesses complete in order, so these
   // stores land after the previous tile's V reads
@@ -342,6 +346,27 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
   }
 }
 
+// A tile through the body for its rows' tiers: single-tier pools know them; in the tiered pool a tile whose 16 rows
+// all sit in one tier (most of them: the ring holds a small share of the slots) takes a body without a branch per row.
+template <int KIND, int G8, bool SPLIT, typename Hook>
+KVT_DEV void attend_tile_any(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt,
+                             const TileCols& tc, int lane, const float smk[4], const float smv[4], float& m_run,
+                             float& l_run, f4 o[16], Hook&& hook) {
+  if constexpr (KIND != 2) {
+    attend_tile<KIND, G8, KIND == 0 ? kRowsInt8 : kRowsInt4>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
+  } else if constexpr (!SPLIT) {
+    attend_tile<KIND, G8, kRowsMixed>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
+  } else {
+    const uint64_t hot = __builtin_amdgcn_ballot_w64((tc.flags & 2) != 0) & 0xffffu;
+    if (hot == 0)
+      attend_tile<KIND, G8, kRowsInt4>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
+    else if (hot == 0xffffu)
+      attend_tile<KIND, G8, kRowsInt8>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
+    else
+      attend_tile<KIND, G8, kRowsMixed>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
+  }
+}
+
 // LDS of a block: one tile buffer per wavefront (K rows until S is formed, then V rows; 42 KB per block), after the
 // tiles the same space holds the merge of the 4 wavefronts; and the group's q heads, bf16 (zero beyond gs)
 struct BlockLds {
@@ -349,7 +374,9 @@ struct BlockLds {
   uint16_t qs[kHeads * kKPitch];
 };
 
-template <int KIND, int G8, bool ROWS, bool MULTI = false>
+// SPLIT: tiles of the tiered pool take the single-tier bodies when they can (off in the 3-blocks-per-CU kernel, whose
+// 168 VGPRs do not hold the three bodies' registers without spilling)
+template <int KIND, int G8, bool ROWS, bool MULTI = false, bool SPLIT = true>
 KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
   auto& kv = S.kv;
   uint16_t* qs = S.qs;
@@ -435,7 +462,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
     Resolver<KIND, G8> rn;
     for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
       const int64_t c1 = c0 + kCols;
-      attend_tile<KIND, G8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [&](int k) {
+      attend_tile_any<KIND, G8, SPLIT>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [&](int k) {
         if (k == 0) rn.stage0(A, c1, c_end, idx_row, lane);
         if (k == 1) rn.stage1(A, L, req);
         if (k == 2) rn.stage2(A);
@@ -443,7 +470,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
       tc = rn.finish(A, h);
     }
   } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads
-    if (has_tile) attend_tile<KIND, G8>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o, [](int) {});
+    if (has_tile) attend_tile_any<KIND, G8, SPLIT>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o, [](int) {});
   }
 
   // merge the 4 wavefronts through LDS, 8 q heads per pass: wavefront w stores the O rows of the pass's heads and
@@ -538,7 +565,7 @@ template <int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3)))
 sparse_decode_multi_tiered_kernel(SparseArgs A) {
   __shared__ __align__(16) BlockLds S;
-  sparse_attn_block<2, G8, false, true>(A, S);
+  sparse_attn_block<2, G8, false, true, false>(A, S);
 }
 
 // prefill rows: a wavefront loops over its row's tiles with the accumulators live, 2 blocks per CU
