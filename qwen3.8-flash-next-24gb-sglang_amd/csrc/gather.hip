@@ -44,9 +44,11 @@ constexpr int kCompactRows = 2;
 constexpr int kPrefixRows = 4;
 constexpr int kWaves = 4;    // wavefronts per block
 
-// bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
+// bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32): lo in bits 0-15.
 KVT_DEV uint32_t bf16x2(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){lo, hi}, bf2v));
 }
 
 // The raw codes and scale of one unit of one row: INT4 (w.x, 8 nibbles) or INT8 (w.x, w.y, 8 bytes).

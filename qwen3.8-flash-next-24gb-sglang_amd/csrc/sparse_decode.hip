@@ -93,9 +93,11 @@ KVT_DEV int64_t load_idx(const void* p, int is64, int64_t i) {
 
 KVT_DEV f4 mfma_bf16(bf4 a, bf4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0); }
 
-// bf16 pair (round to nearest even, v_cvt_pk_bf16_f32): lo in bits 0-15.
+// bf16 pair (round to nearest even, one v_cvt_pk_bf16_f32): lo in bits 0-15.
 KVT_DEV uint32_t bf16x2(float lo, float hi) {
-  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2v __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2v){lo, hi}, bf2v));
 }
 
 KVT_DEV __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
@@ -369,15 +371,103 @@ KVT_DEV void attend_tile_any(const SparseArgs& A, const PoolRsrc& P, const uint1
 
 // LDS of a block: one tile buffer per wavefront (K rows until S is formed, then V rows; 42 KB per block), after the
 // tiles the same space holds the merge of the 4 wavefronts; and the group's q heads, bf16 (zero beyond gs)
+template <int CAP>
 struct BlockLds {
   uint16_t kv[kWaves][kRows * kKPitch];
   uint16_t qs[kHeads * kKPitch];
+  uint2 cols[CAP];             // prefill rows: the query's resolved columns, ring rows first and INT4 rows last
+  int counts[2 * kWaves];
 };
+constexpr int kRowCols = 4096;   // prefill rows: selected columns resolved per pass (74 KB of LDS per block)
+
+// The selected columns [k0, k1) (at most kRowCols) of a prefill block's query row, resolved by all its threads
+// together into the column table and partitioned by tier: ring (INT8) rows to cols[0 .. nh), INT4 rows to
+// cols[CAP - nc .. CAP) (from the end), unattended columns dropped (patches/kv_paged_prefix.py:199-229: position in
+// [0, L)).  J columns per thread, so the position, slot and owner loads of many columns are in flight at once; a
+// block scan of the per-thread counts places them, in an order fixed by the columns (thread, then j), so the result
+// does not depend on timing.  Every tile of 16 table entries then sits in one tier.
+template <int KIND, int G8, int CAP, int J>
+KVT_DEV void resolve_rows(const SparseArgs& A, int64_t k0, int64_t k1, const int32_t* idx_row, int64_t L,
+                          int64_t req, int h, BlockLds<CAP>& S, int& nh, int& nc) {
+  constexpr int kThreads = 64 * kWaves;
+  static_assert(J * kThreads >= CAP, "a pass covers the table");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t* r2t = A.req_to_token + req * A.req_stride;
+  int pos[J], slot[J], own[J];
+  bool live[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int64_t c = k0 + tid + (int64_t)j * kThreads;
+    pos[j] = c < k1 ? idx_row[c * A.si_n] : -1;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    live[j] = pos[j] >= 0 && (int64_t)pos[j] < L;
+    slot[j] = live[j] ? r2t[pos[j]] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) own[j] = (KIND == 2 && live[j]) ? A.owner[(int64_t)slot[j] & A.ring_mask] : -1;
+  bool hot[J];
+  int mh = 0, mc = 0;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    hot[j] = KIND == 0 || (KIND == 2 && live[j] && own[j] == slot[j]);
+    mh += (live[j] && hot[j]) ? 1 : 0;
+    mc += (live[j] && !hot[j]) ? 1 : 0;
+  }
+  // inclusive scan over the wavefront, then the wavefronts' totals through LDS
+  int sh = mh, sc = mc;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int th = __shfl_up(sh, d, 64), tc = __shfl_up(sc, d, 64);
+    if (lane >= d) sh += th, sc += tc;
+  }
+  if (lane == 63) S.counts[wave] = sh, S.counts[kWaves + wave] = sc;
+  __syncthreads();
+  int oh = sh - mh, oc = sc - mc;
+  nh = 0, nc = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int a = S.counts[w], c = S.counts[kWaves + w];
+    if (w < wave) oh += a, oc += c;
+    nh += a, nc += c;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    if (!live[j]) continue;
+    const int64_t row = hot[j] && KIND == 2 ? ((int64_t)slot[j] & A.ring_mask) : (int64_t)slot[j];
+    const int64_t rh = row * A.H + h;
+    const uint2 e = hot[j] ? uint2{(uint32_t)(rh * kD), (uint32_t)(rh * (kD / G8) * 2)}
+                           : uint2{(uint32_t)(rh * (kD / 2)), (uint32_t)(rh * (kD / kG4) * 2)};
+    if (hot[j])
+      S.cols[oh++] = e;
+    else
+      S.cols[CAP - 1 - oc++] = e;
+  }
+}
+
+// Tile t of a partitioned table: hot tiles 0 .. ceil(nh / 16) - 1 read entries 16 t .. from the front, the INT4
+// tiles after them entries from the end; lane r < 16 takes one entry (past the part's count: not attended).
+template <int CAP>
+KVT_DEV TileCols table_tile(const BlockLds<CAP>& S, int t, int th, int nh, int nc, int lane) {
+  const int r = lane & 15;
+  const bool hot = t < th;
+  const int i = hot ? 16 * t + r : 16 * (t - th) + r;
+  const bool ok = lane < kRows && i < (hot ? nh : nc);
+  TileCols x;
+  x.flags = ok ? (hot ? 3 : 1) : 0;
+  x.coff = kNoRow, x.soff = kNoRow;
+  if (ok) {
+    const uint2 e = S.cols[hot ? i : CAP - 1 - i];
+    x.coff = e.x, x.soff = e.y;
+  }
+  return x;
+}
 
 // SPLIT: tiles of the tiered pool take the single-tier bodies when they can (off in the 3-blocks-per-CU kernel, whose
 // 168 VGPRs do not hold the three bodies' registers without spilling)
-template <int KIND, int G8, bool ROWS, bool MULTI = false, bool SPLIT = true>
-KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
+template <int KIND, int G8, bool ROWS, bool MULTI, bool SPLIT, int CAP>
+KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   auto& kv = S.kv;
   uint16_t* qs = S.qs;
   const int lane = threadIdx.x & 63;
@@ -408,10 +498,16 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
 
   const int64_t req = load_idx(A.req_indices, A.req64, b);
   const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
-  // the wavefront's first tile is resolved first, so that its chain of dependent loads runs beside the Q copy
+  // the wavefront's first tile (prefill rows: the first pass of the column table) is resolved first, so that the
+  // chains of dependent loads run beside the Q copy
   TileCols tc0{};
   const bool has_tile = c_begin + kRows * wave < c_end;
-  if (has_tile) tc0 = resolve_tile<KIND, G8>(A, c_begin + kRows * wave, c_end, idx_row, L, req, h, lane);
+  int nh = 0, nc = 0;
+  if constexpr (ROWS)
+    resolve_rows<KIND, G8, CAP, CAP / (64 * kWaves)>(A, c_begin, c_begin + CAP < c_end ? c_begin + CAP : c_end, idx_row,
+                                                     L, req, h, S, nh, nc);
+  else if (has_tile)
+    tc0 = resolve_tile<KIND, G8>(A, c_begin + kRows * wave, c_end, idx_row, L, req, h, lane);
   // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
 #pragma unroll
   for (int i = threadIdx.x; i < kHeads * kD / 8; i += 64 * kWaves) {
@@ -455,7 +551,25 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
   f4 o[16];                               // O[head 4 (lane >> 4) + i][channel 16 n + (lane & 15)]
 #pragma unroll
   for (int n = 0; n < 16; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (ROWS || MULTI) {
+  if constexpr (ROWS) {
+    // passes of the column table (the first resolved above): wavefront w takes tiles w, w + 4, ..., ring tiles first
+    for (int64_t k0 = c_begin; k0 < c_end; k0 += CAP) {
+      const int64_t k1 = k0 + CAP < c_end ? k0 + CAP : c_end;
+      if (k0 > c_begin) {
+        __syncthreads();   // the previous pass's entries are read
+        resolve_rows<KIND, G8, CAP, CAP / (64 * kWaves)>(A, k0, k1, idx_row, L, req, h, S, nh, nc);
+        __syncthreads();
+      }
+      const int th = (nh + kRows - 1) / kRows, nt = th + (nc + kRows - 1) / kRows;
+      for (int t = wave; t < nt; t += kWaves) {
+        const TileCols tc = table_tile(S, t, th, nh, nc, lane);
+        if (t < th)
+          attend_tile<KIND, G8, kRowsInt8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
+        else
+          attend_tile<KIND, G8, kRowsInt4>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
+      }
+    }
+  } else if constexpr (MULTI) {
     // tiles c_begin + 16 wave + 64 k: the next tile's position, slot and owner loads go out beside this tile's
     // loads and math (for the last tile they have no active lane)
     TileCols tc = tc0;
@@ -549,8 +663,8 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds& S) {
 // decode: one tile per wavefront, 3 blocks per CU
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) sparse_decode_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds S;
-  sparse_attn_block<KIND, G8, false>(A, S);
+  __shared__ __align__(16) BlockLds<1> S;
+  sparse_attn_block<KIND, G8, false, false, true>(A, S);
 }
 
 // decode of long selections: a wavefront loops over A.tiles tiles with the accumulators live; 3 blocks per CU for
@@ -558,21 +672,21 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
 sparse_decode_multi_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds S;
-  sparse_attn_block<KIND, G8, false, true>(A, S);
+  __shared__ __align__(16) BlockLds<1> S;
+  sparse_attn_block<KIND, G8, false, true, true>(A, S);
 }
 template <int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3)))
 sparse_decode_multi_tiered_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds S;
+  __shared__ __align__(16) BlockLds<1> S;
   sparse_attn_block<2, G8, false, true, false>(A, S);
 }
 
 // prefill rows: a wavefront loops over its row's tiles with the accumulators live, 2 blocks per CU
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) sparse_prefill_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds S;
-  sparse_attn_block<KIND, G8, true>(A, S);
+  __shared__ __align__(16) BlockLds<kRowCols> S;
+  sparse_attn_block<KIND, G8, true, false, true>(A, S);
 }
 
 // Shared argument checks and pool resources of both entry points; returns KVT_OK or a status.
