@@ -12,8 +12,11 @@
 //     (0 <= idx < kv_len) among the first min(topk, j + kv_len - q_len + 1) of its index row
 //     (patches/kv_paged_prefix.py:199-229) and writes its normalized output (0/0 = NaN when nothing is attended).
 //
-// Inside a block, 4 wavefronts take 16-column tiles in turn.  A tile's K and V rows are dequantized into the
-// wavefront's LDS rows as bf16, then QK^T and P.V run as bf16 16x16x16 matrix-core steps with fp32 accumulation:
+// Inside a block, 4 wavefronts take 16-column tiles in turn.  Blocks with many columns (prefill rows, decode blocks
+// of several tiles per wavefront) first resolve all of them into an LDS column table partitioned by tier, so every
+// tile holds rows of one tier and padding columns cost nothing; a block of one tile per wavefront resolves its own
+// tile.  A tile's K and V rows are dequantized into the wavefront's LDS rows as bf16, then QK^T and P.V run as bf16
+// 16x16x16 matrix-core steps with fp32 accumulation:
 //   S^T[row][head] = K[row][:] . Q[head][:]   (A = K tile, B = Q^T; 16 steps over the 256 channels)
 //   O[head][ch]   += P[head][row] V[row][ch]  (A = P straight from S^T's accumulator layout as bf16 high part
 //                                               + bf16 remainder, B = V tile by the transposing LDS read)
@@ -228,43 +231,6 @@ KVT_DEV TileCols resolve_tile(const SparseArgs& A, int64_t c0, int64_t c_end, co
   return tc;
 }
 
-// The same resolve in three stages, so that its chain of loads can run beside the previous tile's loads and math:
-// stage 0 loads the position, stage 1 the slot, stage 2 the owner; finish() computes the tile's columns.
-template <int KIND, int G8>
-struct Resolver {
-  int64_t col, pos, slot;
-  int own;
-  bool live;
-  KVT_DEV void stage0(const SparseArgs& A, int64_t c0, int64_t c_end, const int32_t* idx_row, int lane) {
-    col = c0 + (lane & 15);
-    live = lane < kRows && col < c_end;
-    pos = live ? (int64_t)idx_row[col * A.si_n] : -1;
-  }
-  KVT_DEV void stage1(const SparseArgs& A, int64_t L, int64_t req) {
-    live = live && pos >= 0 && pos < L;
-    slot = live ? (int64_t)A.req_to_token[req * A.req_stride + pos] : 0;
-  }
-  KVT_DEV void stage2(const SparseArgs& A) {
-    if constexpr (KIND == 2) own = live ? A.owner[slot & A.ring_mask] : -1;
-  }
-  KVT_DEV TileCols finish(const SparseArgs& A, int h) const {
-    bool hot = KIND == 0;
-    int64_t row = slot;
-    if constexpr (KIND == 2) {
-      if (live && (int64_t)own == slot) {
-        hot = true;
-        row = slot & A.ring_mask;
-      }
-    }
-    const int64_t rh = row * A.H + h;
-    TileCols tc;
-    tc.flags = (live ? 1 : 0) | (hot ? 2 : 0);
-    tc.coff = !live ? kNoRow : (uint32_t)(hot ? rh * kD : rh * (kD / 2));
-    tc.soff = !live ? kNoRow : (uint32_t)(hot ? rh * (kD / G8) * 2 : rh * (kD / kG4) * 2);
-    return tc;
-  }
-};
-
 // One resolved 16-column tile of a wavefront, folded into its running softmax state (m, l per q head n16 of this
 // lane, o): load and dequantize K into the wavefront's LDS rows, S^T = K Q^T, dequantize V into the same rows,
 // online softmax, O += P V.
@@ -350,14 +316,12 @@ KVT_DEV void attend_tile(const SparseArgs& A, const PoolRsrc& P, const uint16_t*
 
 // A tile through the body for its rows' tiers: single-tier pools know them; in the tiered pool a tile whose 16 rows
 // all sit in one tier (most of them: the ring holds a small share of the slots) takes a body without a branch per row.
-template <int KIND, int G8, bool SPLIT, typename Hook>
+template <int KIND, int G8, typename Hook>
 KVT_DEV void attend_tile_any(const SparseArgs& A, const PoolRsrc& P, const uint16_t* qs, uint16_t* kt,
                              const TileCols& tc, int lane, const float smk[4], const float smv[4], float& m_run,
                              float& l_run, f4 o[16], Hook&& hook) {
   if constexpr (KIND != 2) {
     attend_tile<KIND, G8, KIND == 0 ? kRowsInt8 : kRowsInt4>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
-  } else if constexpr (!SPLIT) {
-    attend_tile<KIND, G8, kRowsMixed>(A, P, qs, kt, tc, lane, smk, smv, m_run, l_run, o, hook);
   } else {
     const uint64_t hot = __builtin_amdgcn_ballot_w64((tc.flags & 2) != 0) & 0xffffu;
     if (hot == 0)
@@ -379,6 +343,7 @@ struct BlockLds {
   int counts[2 * kWaves];
 };
 constexpr int kRowCols = 4096;   // prefill rows: selected columns resolved per pass (74 KB of LDS per block)
+constexpr int kMultiCols = 1024; // decode blocks of several tiles per wavefront (50 KB of LDS per block)
 
 // The selected columns [k0, k1) (at most kRowCols) of a prefill block's query row, resolved by all its threads
 // together into the column table and partitioned by tier: ring (INT8) rows to cols[0 .. nh), INT4 rows to
@@ -464,9 +429,9 @@ KVT_DEV TileCols table_tile(const BlockLds<CAP>& S, int t, int th, int nh, int n
   return x;
 }
 
-// SPLIT: tiles of the tiered pool take the single-tier bodies when they can (off in the 3-blocks-per-CU kernel, whose
-// 168 VGPRs do not hold the three bodies' registers without spilling)
-template <int KIND, int G8, bool ROWS, bool MULTI, bool SPLIT, int CAP>
+// ROWS: prefill rows (one query row per block) instead of decode splits; MULTI: a decode block of several tiles per
+// wavefront; CAP > 1: the block resolves its columns into a column table of CAP entries partitioned by tier first.
+template <int KIND, int G8, bool ROWS, bool MULTI, int CAP>
 KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   auto& kv = S.kv;
   uint16_t* qs = S.qs;
@@ -503,7 +468,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   TileCols tc0{};
   const bool has_tile = c_begin + kRows * wave < c_end;
   int nh = 0, nc = 0;
-  if constexpr (ROWS)
+  if constexpr (CAP > 1)
     resolve_rows<KIND, G8, CAP, CAP / (64 * kWaves)>(A, c_begin, c_begin + CAP < c_end ? c_begin + CAP : c_end, idx_row,
                                                      L, req, h, S, nh, nc);
   else if (has_tile)
@@ -551,7 +516,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   f4 o[16];                               // O[head 4 (lane >> 4) + i][channel 16 n + (lane & 15)]
 #pragma unroll
   for (int n = 0; n < 16; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
-  if constexpr (ROWS) {
+  if constexpr (CAP > 1) {
     // passes of the column table (the first resolved above): wavefront w takes tiles w, w + 4, ..., ring tiles first
     for (int64_t k0 = c_begin; k0 < c_end; k0 += CAP) {
       const int64_t k1 = k0 + CAP < c_end ? k0 + CAP : c_end;
@@ -569,22 +534,8 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
           attend_tile<KIND, G8, kRowsInt4>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
       }
     }
-  } else if constexpr (MULTI) {
-    // tiles c_begin + 16 wave + 64 k: the next tile's position, slot and owner loads go out beside this tile's
-    // loads and math (for the last tile they have no active lane)
-    TileCols tc = tc0;
-    Resolver<KIND, G8> rn;
-    for (int64_t c0 = c_begin + kRows * wave; c0 < c_end; c0 += kCols) {
-      const int64_t c1 = c0 + kCols;
-      attend_tile_any<KIND, G8, SPLIT>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [&](int k) {
-        if (k == 0) rn.stage0(A, c1, c_end, idx_row, lane);
-        if (k == 1) rn.stage1(A, L, req);
-        if (k == 2) rn.stage2(A);
-      });
-      tc = rn.finish(A, h);
-    }
   } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads
-    if (has_tile) attend_tile_any<KIND, G8, SPLIT>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o, [](int) {});
+    if (has_tile) attend_tile_any<KIND, G8>(A, P, qs, kv[wave], tc0, lane, smk, smv, m_run, l_run, o, [](int) {});
   }
 
   // merge the 4 wavefronts through LDS, 8 q heads per pass: wavefront w stores the O rows of the pass's heads and
@@ -664,29 +615,24 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) sparse_decode_kernel(SparseArgs A) {
   __shared__ __align__(16) BlockLds<1> S;
-  sparse_attn_block<KIND, G8, false, false, true>(A, S);
+  sparse_attn_block<KIND, G8, false, false, 1>(A, S);
 }
 
-// decode of long selections: a wavefront loops over A.tiles tiles with the accumulators live; 3 blocks per CU for
-// the tiered pool (168 VGPRs), 2 for the single-tier pools (about 200)
+// decode of long selections: the block's 64 A.tiles columns resolved into its column table, a wavefront looping over
+// its tiles with the accumulators live; 2 blocks per CU
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2)))
 sparse_decode_multi_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds<1> S;
-  sparse_attn_block<KIND, G8, false, true, true>(A, S);
-}
-template <int G8>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3)))
-sparse_decode_multi_tiered_kernel(SparseArgs A) {
-  __shared__ __align__(16) BlockLds<1> S;
-  sparse_attn_block<2, G8, false, true, false>(A, S);
+  __shared__ __align__(16) BlockLds<kMultiCols> S;
+  sparse_attn_block<KIND, G8, false, true, kMultiCols>(A, S);
 }
 
-// prefill rows: a wavefront loops over its row's tiles with the accumulators live, 2 blocks per CU
+// prefill rows: the query's selection resolved into the column table, a wavefront looping over its tiles with the
+// accumulators live; 2 blocks per CU
 template <int KIND, int G8>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) sparse_prefill_kernel(SparseArgs A) {
   __shared__ __align__(16) BlockLds<kRowCols> S;
-  sparse_attn_block<KIND, G8, true, false, true>(A, S);
+  sparse_attn_block<KIND, G8, true, false, kRowCols>(A, S);
 }
 
 // Shared argument checks and pool resources of both entry points; returns KVT_OK or a status.
@@ -708,8 +654,6 @@ int launch(int kind, int group8, dim3 grid, hipStream_t st, const SparseArgs& A)
   do {                                                                                                     \
     if constexpr (ROWS)                                                                                    \
       hipLaunchKernelGGL((sparse_prefill_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);           \
-    else if (A.tiles > 1 && KIND_ == 2)                                                                    \
-      hipLaunchKernelGGL((sparse_decode_multi_tiered_kernel<G_>), grid, dim3(64 * kWaves), 0, st, A);      \
     else if (A.tiles > 1)                                                                                  \
       hipLaunchKernelGGL((sparse_decode_multi_kernel<KIND_, G_>), grid, dim3(64 * kWaves), 0, st, A);      \
     else                                                                                                   \

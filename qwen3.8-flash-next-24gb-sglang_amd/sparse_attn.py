@@ -264,12 +264,11 @@ def qwen_sparse_decode_attn(
     _lib.require_device(q, k, v, req_to_token, indices, out)
     scale = float(dim ** -0.5) if scale is None else float(scale)
     # blocks of 64 selected columns (a 16-column tile per wavefront) while the launch holds at most 1,024 of them;
-    # longer selections take `tiles` tiles per wavefront in about one block per resident slot (3 per CU for the
-    # tiered pool, 2 for the others), each partial then covering 64 x tiles columns
+    # longer selections take `tiles` tiles per wavefront in about one block per resident slot (2 per CU), each
+    # partial then covering 64 x tiles columns
     tiles64 = (int(topk) + 63) // 64
     blocks = batch * heads * tiles64
-    slots_ = 768 if kind == _KIND_TIERED else 512
-    tiles = 1 if blocks <= 1024 else -(-blocks // slots_)
+    tiles = 1 if blocks <= 1024 else -(-blocks // 512)
     n_splits = -(-tiles64 // tiles) if splits is None else int(splits)
     assert n_splits >= 1
     ws = workspace if workspace is not None else {}
