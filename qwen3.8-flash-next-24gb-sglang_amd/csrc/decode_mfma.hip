@@ -203,10 +203,12 @@ KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
 // 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
 // statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.
 // Inline assembly rather than the builtin so that the compiler does not treat every later LDS read as dependent on
-// the copy: completion is tracked explicitly with wait_vmcnt by the caller.
+// the copy: completion is tracked explicitly with wait_vmcnt by the caller.  The loads are non-temporal (nt): a
+// layer streams 155 MB through the caches once, and marked as streaming it leaves the small per-step metadata every
+// layer starts from (sequence lengths, ring placement, page ids) cached (step 0.516 -> 0.505 ms, measured A/B).
 KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
                : "memory");
 }
 
