@@ -245,9 +245,17 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
  * sequence b, or, when k_bf16 / v_bf16 are given (batch 1, a chunk without a prefix), from those bf16
  * [positions, H, D] rows (the reference attends to fresh bf16 K/V there; |V| <= 128 * 65504).  out: bf16 or fp32
  * (out_f32) with the layout of q.  Replaces sparse_gqa_fwd_interface_paged (patches/kv_paged_prefix.py:267-365) for dense causal
- * chunks.  Hq / H <= 16, D = 256; pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte
- * offsets are 32-bit, else KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
- * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device). */
+ * chunks.  Hq / H <= 16, D = 256; q 16-byte aligned with sq_n, sq_h multiples of 8 (Q rows are read 16 bytes at a
+ * time); pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte offsets are 32-bit, else
+ * KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
+ * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device).
+ * spread_blocks > 0: that many blocks share the launch's key tiles equally (query tiles are split where a share
+ * ends; the block that finishes a query tile's last piece merges the pieces in piece order), instead of one block
+ * per query tile -- the latest query tiles of a causal chunk see up to a chunk length more keys than the earliest,
+ * so one block per CU with equal shares ends them all together.  It needs `work`, at least kvt_prefill_work_bytes
+ * bytes, whose counter area (its first bytes) is zero before the first call -- each call leaves it at zero again;
+ * calls that share a workspace must not overlap; at most 4,096 query tiles (batch x H x tiles of 128 rows), else
+ * KVT_ERANGE.  The output does not depend on which block merges. */
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
                      const void* v4, const void* ks4, const void* vs4, const void* rk, const void* rv,
@@ -255,7 +263,13 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
                      const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                      const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
                      int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
-                     void* stream);
+                     int spread_blocks, void* work, int64_t work_bytes, void* stream);
+
+/* Bytes of the kvt_prefill_attn workspace for these shapes and spread_blocks (0 for spread_blocks 0): a zeroed
+ * 4-byte counter per (sequence, KV head, query tile of 128 rows), padded to 256 bytes, and a 132,096-byte state
+ * slot (O, m, l of 128 rows in fp32) per query tile plus one per block beyond the first.  No counterpart in the
+ * reference (its prefill kernel takes one block per query row). */
+int kvt_prefill_work_bytes(int batch, int H, int Hq, int max_q, int spread_blocks, int64_t* bytes);
 
 /* ----------------------------------------------------------------------------- lazy backing (HIP VMM) */
 

@@ -52,7 +52,8 @@ SIGNATURES = {
                                 _L, _F, _I, _P, _I, _P, _I, _P, _P, _L, _P],
     "kvt_decode_combine": [_P, _P, _I, _I, _I, _I, _I, _L, _P, _P, _P, _P, _L, _P],
     "kvt_prefill_attn": [_P, _L, _L, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                         _P, _L, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _I, _L, _L, _P],
+                         _P, _L, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _I, _L, _L, _I, _P, _L, _P],
+    "kvt_prefill_work_bytes": [_I, _I, _I, _I, _I, _P],
     "kvt_vmm_granularity": [_I, _P],
     "kvt_vmm_reserve": [_I, _U, _P, _P],
     "kvt_vmm_commit": [_P, _U],

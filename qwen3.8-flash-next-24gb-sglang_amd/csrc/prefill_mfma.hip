@@ -87,6 +87,7 @@ struct __align__(16) Lds {
   uint8_t k[2][kT * kKPitch];    // double-buffered: tile i + 1 is dequantized while tile i is in use
   uint8_t v[2][kT * kVRow];
   int32_t pages[kMaxLdsPages];
+  int flag;                      // segments: "this block merges"
 };
 
 KVT_DEV f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
@@ -129,6 +130,32 @@ KVT_DEV uint2 ld64(Rsrc r, uint32_t off) {
   return make_uint2((uint32_t)x.x, (uint32_t)x.y);
 }
 KVT_DEV uint32_t ld16(Rsrc r, uint32_t off) { return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0); }
+
+// Segments.  A spread launch splits the key tiles of a query tile into segments held by different blocks, so that
+// every block gets the same number of key tiles (the latest query tiles of a causal chunk see up to a chunk length
+// more keys than the earliest).  A block writes a segment's (m, l, O) -- the online softmax state of its 128 rows
+// over the segment -- into the segment's slot and counts itself on the query tile's counter; the block that counts
+// last merges the nseg states in segment order, writes the output, and resets the counter to zero for the next
+// call.  Slots and counters cross XCDs (each has its own L2): they are
+// written and read with device-scope accesses (through to the coherence point past the L2), and a block waits for
+// its slot stores to complete before it counts itself.  The merge is a fixed sum over the segments, so the output
+// does not depend on which block merges; no block ever waits for another.
+// Slot layout (floats): O at ((wave * 16 + c) * 64 + lane) * 4 + i (accumulator acc[c][i]: one 16-byte store per
+// column block, 1 KB per wavefront store), then (m, l) of row r of wavefront w at kSlotO + 2 (16 w + r).
+constexpr int kSc1 = 16;   // cache-policy operand of the raw buffer builtins: sc1 (device scope, past the L2)
+constexpr int kSlotO = 8 * 64 * 64;
+constexpr int kSlotFloats = kSlotO + 8 * 16 * 2;
+KVT_DEV void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+KVT_DEV float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KVT_DEV void st_dev_i32(int32_t* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+KVT_DEV int ld_dev_i32(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+KVT_DEV int add_dev_i32(int32_t* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // This block's view of the key source: buffer resources over the INT4 pool, the sequence's ring rows and the bf16
 // source, the tier boundary and the key range.  Every key fetch issues the loads of both tiers unconditionally
@@ -537,31 +564,39 @@ KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t*
 constexpr int kAheadK = 3, kAheadV = 4;   // LDS operand reads issued this many matrix steps ahead
 constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 16 rows (16 / gs queries x gs heads)
 
+// The queries of one query tile (qb queries of sequence b) and the keys they see.
+struct QTile {
+  int64_t qs, q_len, L, q_pos0, qt0, key_end;
+  int ntiles;   // key tiles of 32 positions (0: no query of the sequence falls in this tile)
+};
+KVT_DEV QTile qtile_of(const void* cu_q, int cu_q_is_int64, const int32_t* kv_lens, int b, int qt, int qb) {
+  QTile Q;
+  Q.qs = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b] : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b];
+  const int64_t qe = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b + 1]
+                                   : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b + 1];
+  Q.q_len = qe - Q.qs;
+  Q.L = kv_lens[b];
+  Q.q_pos0 = Q.L - Q.q_len;   // position of the chunk's first query
+  Q.qt0 = (int64_t)qt * qb;
+  Q.key_end = min(Q.L, Q.q_pos0 + min(Q.q_len, Q.qt0 + qb));   // keys visible to the tile's last query
+  Q.ntiles = Q.qt0 < Q.q_len && Q.key_end > 0 ? (int)((Q.key_end + kT - 1) / kT) : 0;
+  return Q;
+}
+
+// One segment: key tiles [i0, i1) of query tile Q of (sequence b, KV head h).  nseg segments make up the tile, this
+// is number `ord`; with nseg > 1 their states go through slots[0 .. nseg) and *count (see kSlotO), and the
+// segment that finishes last writes the output.
 template <int G8, bool BF16>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
-prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
-                    const int32_t* kv_lens, int H, int gs, int n_qtiles, float scale, void* out, int out_f32,
-                    int64_t so_n, int64_t so_h) {
+KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const QTile& Q, int b,
+                            int h, int H, int gs, int i0, int i1, int nseg, int ord, float* slots, int32_t* count,
+                            float scale, void* out, int out_f32, int64_t so_n, int64_t so_h) {
   __shared__ Lds lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, kb = lane >> 4;
-  const int qt = n_qtiles - 1 - (int)blockIdx.x;   // latest (heaviest) query tiles first
-  const int qpw = 16 / gs;                         // queries per wavefront
-  const int qb = kWaves * qpw;                     // queries per block
-  const int b = blockIdx.y / H;
-  const int h = blockIdx.y - b * H;
-  const int64_t qs = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b]
-                                   : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b];
-  const int64_t qe = cu_q_is_int64 ? reinterpret_cast<const int64_t*>(cu_q)[b + 1]
-                                   : (int64_t)reinterpret_cast<const int32_t*>(cu_q)[b + 1];
-  const int64_t q_len = qe - qs;
-  const int64_t L = kv_lens[b];
-  const int64_t q_pos0 = L - q_len;   // position of the chunk's first query
-  const int64_t qt0 = (int64_t)qt * qb;
-  if (qt0 >= q_len) return;
-  const int64_t key_end = min(L, q_pos0 + min(q_len, qt0 + qb));   // keys visible to the tile's last query
+  const int qpw = 16 / gs;   // queries per wavefront
+  const int64_t qs = Q.qs, q_len = Q.q_len, L = Q.L, q_pos0 = Q.q_pos0, qt0 = Q.qt0, key_end = Q.key_end;
   constexpr uint32_t NG8 = kD / G8;
   Tier T;
   T.H = H;
@@ -598,7 +633,17 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   }
   __syncthreads();
 
-  // ---- Q operands: row j of the wavefront's 16 = query qt0 + qpw wave + j / gs, head j % gs
+  // dequantization, the same for every thread t: 16 channels (16 (t & 15) ..) of K row t >> 4, and 8 channels
+  // (8 (t >> 4) ..) of V rows 2 (t & 15), 2 (t & 15) + 1
+  const int tk = tid >> 4, dc = tid & 15;
+  const int tp = tid & 15, db = tid >> 4;
+  constexpr int kFirst = BF16 ? kTierBf16 : kTierMixed;
+  // the first tile's codes go out before the Q rows, so that storing the tile waits for its own loads only
+  RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, i0 * kT + tk, dc);
+  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, i0 * kT + tp, db);
+
+  // ---- Q operands: row j of the wavefront's 16 = query qt0 + qpw wave + j / gs, head j % gs; channels
+  // 32 st + 8 kb .. + 7 of the row in one 16-byte load per st (the host checks the 16-byte alignment)
   bf8 qop[8];
   int64_t qpos;   // position of this lane's query row (as the S^T column)
   const float qmul = scale * kLog2e;
@@ -607,12 +652,11 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
     const bool ok = rq < qpw && qi < q_len;
     qpos = q_pos0 + qi;
-    const uint16_t* qr = q + (qs + (ok ? qi : 0)) * sq_n + (int64_t)(h * gs + (ok ? hq : 0)) * sq_h;
+    const uint16_t* qr = q + (qs + (ok ? qi : 0)) * sq_n + (int64_t)(h * gs + (ok ? hq : 0)) * sq_h + 8 * kb;
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        qop[st][e] = __builtin_bit_cast(__bf16, (uint16_t)(ok ? qr[32 * st + 8 * kb + e] : 0));
+      const u4v w = ok ? *reinterpret_cast<const u4v*>(qr + 32 * st) : u4v{0u, 0u, 0u, 0u};
+      qop[st] = __builtin_bit_cast(bf8, w);
     }
   }
 
@@ -621,18 +665,10 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   for (int c = 0; c < 16; ++c) acc[c] = f4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // dequantization, the same for every thread t: 16 channels (16 (t & 15) ..) of K row t >> 4, and 8 channels
-  // (8 (t >> 4) ..) of V rows 2 (t & 15), 2 (t & 15) + 1
-  const int tk = tid >> 4, dc = tid & 15;
-  const int tp = tid & 15, db = tid >> 4;
-  const int ntiles = (int)((key_end + kT - 1) / kT);
-  constexpr int kFirst = BF16 ? kTierBf16 : kTierMixed;
-  RawK rk_next = fetch_k<G8, BF16>(T, lds.pages, tk, dc);
-  RawV rv_next = fetch_v<G8, BF16>(T, lds.pages, tp, db);
-  store_k<kFirst>(rk_next, lds.k[0] + tk * kKPitch, tk, dc);
-  store_v<kFirst>(rv_next, lds.v[0], db, tp);
-  rk_next = fetch_k<G8, BF16>(T, lds.pages, kT + tk, dc);   // (past the end it rereads the last key)
-  rv_next = fetch_v<G8, BF16>(T, lds.pages, kT + tp, db);
+  store_k<kFirst>(rk_next, lds.k[i0 & 1] + tk * kKPitch, tk, dc);
+  store_v<kFirst>(rv_next, lds.v[i0 & 1], db, tp);
+  rk_next = fetch_k<G8, BF16>(T, lds.pages, (i0 + 1) * kT + tk, dc);   // (past the end it rereads the last key)
+  rv_next = fetch_v<G8, BF16>(T, lds.pages, (i0 + 1) * kT + tp, db);
   __syncthreads();
   const int qmin = (int)(q_pos0 + qt0);   // the block's first query position: tiles below it need no causal mask
   const int qp = (int)qpos, kend = (int)key_end;
@@ -649,7 +685,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   for (int j = 0; j < 4; ++j) koff[j] = k_chunk(n16, 4 * j + kb);
   const uint32_t vlane = (uint32_t)(4 * kb + (n16 >> 2)) * kVRow + 8u * (uint32_t)(n16 & 3);
   const FetchLane FL = fetch_lane<G8, BF16>(T, tk, dc, tp, db);
-  int it = 0;
+  int it = i0;
   auto body = [&](auto tag, auto ftag) {
     constexpr int TIER = decltype(tag)::value;
     constexpr int FETCH = decltype(ftag)::value;
@@ -770,7 +806,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   };
   // Iteration it converts tile it + 1 and fetches tile it + 2; a whole-tile fetch needs tile it + 2 to end at or
   // before the key end (it + 3 <= kend / kT) and, for INT4, at or before hot_start.
-  const int nd = ntiles - 1;           // iterations that convert a tile (tile it + 1)
+  const int nd = i1 - 1;               // iterations that convert a tile (tile it + 1)
   const int me = kend / kT - 2;        // iterations whose tile it + 2 ends at or before the key end
   using KeysF = TierTag<kFetchKeys>;
   // s_waitcnt vmcnt(0) before a loop: loads of an earlier loop still in flight into registers this loop reuses would
@@ -793,36 +829,266 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     while (it < nd) body(TierTag<kTierInt8>{}, KeysF{});
   }
   drain();
-  while (it < ntiles) body(TierTag<kTierNone>{}, TierTag<kFetchNone>{});
+  while (it < i1) body(TierTag<kTierNone>{}, TierTag<kFetchNone>{});
 
-  // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
-  // column n16 of block c = dim 16 c + n16
-  {
-    const float l = sum_xor16_32(l_run);
+  // ---- the row sums of accumulator rows 4 kb + i (m_run and l are uniform over the four lanes of a row)
+  const float l = sum_xor16_32(l_run);
+  float lrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lrow[i] = __shfl(l, 4 * kb + i, 64);
+  if (nseg > 1) {   // ---- publish this segment's state, or merge every segment's if it is the last
+    const Rsrc rs = make_rsrc(slots, (uint32_t)nseg * kSlotFloats * 4u);
+    const uint32_t olane = (uint32_t)(wave * 16 * 64 + lane) * 16u;   // + 1024 c: this lane's O of column block c
+    if (tid == 0) lds.flag = ld_dev_i32(count) == nseg - 1;   // every other segment is in: merge at once
+    __syncthreads();
+    if (lds.flag == 0) {
+      const uint32_t mine = (uint32_t)ord * kSlotFloats * 4u;
+#pragma unroll
+      for (int c = 0; c < 16; ++c)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[c]), rs, (int)(mine + olane + 1024u * c),
+                                               0, kSc1);
+      if (kb == 0) {
+        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave + n16)], m_run);
+        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave + n16) + 1], l);
+      }
+      drain();          // the stores have reached the coherence point
+      __syncthreads();  // (and every thread has read lds.flag)
+      if (tid == 0) lds.flag = add_dev_i32(count, 1) == nseg - 1;
+      __syncthreads();
+      if (lds.flag == 0) return;   // a later segment merges
+    }
+    if (tid == 0) st_dev_i32(count, 0);   // every segment has counted: ready for the next call
+    // merge: weight of segment o in row r 2^(m_o - M), M the max over the segments (log2 units; -inf: no visible
+    // key); sums over o = 0 .. nseg - 1 in order (this segment's state from registers, the others' from their
+    // slots), so the result does not depend on which segment merges
+    float mo[4], M[4], Ls[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float lr = __shfl(l, 4 * kb + i, 64);
-      const int r = 4 * kb + i, rq = r / gs, hq = r - rq * gs;
-      const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
-      if (rq < qpw && qi < q_len) {
-        const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
-        if (out_f32) {
-          float* orow = reinterpret_cast<float*>(out) + o0;
+      mo[i] = __shfl(m_run, 4 * kb + i, 64);
+      M[i] = -INFINITY;
+      Ls[i] = 0.f;
+    }
+    const int mlrow = kSlotO + 2 * (16 * wave + 4 * kb);
+    if (nseg == 2) {   // (the common case) every load of the other segment at once
+      const int oth = 1 - ord;
+      float mx[4], lx[4];
+      f4 x[16];
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = (acc[c][i] * 128.0f) / lr;
-        } else {
-          uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
+      for (int i = 0; i < 4; ++i) {
+        mx[i] = ld_dev(&slots[oth * kSlotFloats + mlrow + 2 * i]);
+        lx[i] = ld_dev(&slots[oth * kSlotFloats + mlrow + 2 * i + 1]);
+      }
 #pragma unroll
-          for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne((acc[c][i] * 128.0f) / lr);
+      for (int c = 0; c < 16; ++c)
+        x[c] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                          rs, (int)((uint32_t)oth * kSlotFloats * 4u + olane + 1024u * c), 0, kSc1));
+      float w0[4], w1[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float m0 = ord == 0 ? mo[i] : mx[i], m1 = ord == 0 ? mx[i] : mo[i];
+        const float mm = fmaxf(m0, m1);
+        w0[i] = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - mm);
+        w1[i] = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+        const float l0 = ord == 0 ? lrow[i] : lx[i], l1 = ord == 0 ? lx[i] : lrow[i];
+        lrow[i] = fmaf(w1[i], l1, w0[i] * l0);
+      }
+      if (ord == 0) {
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[c][i] = fmaf(w1[i], x[c][i], w0[i] * acc[c][i]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[c][i] = fmaf(w1[i], acc[c][i], w0[i] * x[c][i]);
+      }
+    } else {
+      for (int o = 0; o < nseg; ++o)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          M[i] = fmaxf(M[i], o == ord ? mo[i] : ld_dev(&slots[o * kSlotFloats + mlrow + 2 * i]));
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {   // column blocks in two halves of 8
+        f4 O[8];
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) O[cc] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int o = 0; o < nseg; ++o) {
+          const bool me = o == ord;
+          float wg[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float m = me ? mo[i] : ld_dev(&slots[o * kSlotFloats + mlrow + 2 * i]);
+            wg[i] = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M[i]);
+            if (hf == 0) Ls[i] += wg[i] * (me ? lrow[i] : ld_dev(&slots[o * kSlotFloats + mlrow + 2 * i + 1]));
+          }
+#pragma unroll
+          for (int cc = 0; cc < 8; ++cc) {
+            const int c = 8 * hf + cc;
+            const f4 xo = me ? acc[c]
+                             : __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          rs, (int)((uint32_t)o * kSlotFloats * 4u + olane + 1024u * c),
+                                                          0, kSc1));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) O[cc][i] += wg[i] * xo[i];
+          }
         }
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) acc[8 * hf + cc] = O[cc];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lrow[i] = Ls[i];
+    }
+  }
+  // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
+  // column n16 of block c = dim 16 c + n16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * kb + i, rq = r / gs, hq = r - rq * gs;
+    const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
+    if (rq < qpw && qi < q_len) {
+      const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
+      if (out_f32) {
+        float* orow = reinterpret_cast<float*>(out) + o0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = (acc[c][i] * 128.0f) / lrow[i];
+      } else {
+        uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne((acc[c][i] * 128.0f) / lrow[i]);
       }
     }
   }
 }
 
+// Spread launches: the work of all query tiles, laid end to end (items j = (sequence, KV head) j / n_qtiles, query
+// tile j % n_qtiles, in that order) in units of one key tile, is cut into equal shares, one per block; a block
+// walks the segments of its share (the end of one query tile, whole tiles, the start of another).  An item costs
+// kItemCost units (a segment's Q load, first tile and output: about what 8 key tiles take) followed by one unit per
+// key tile, so a share of many short query tiles holds fewer key tiles.  Every block computes the same prefix sums
+// of the item costs.  Block w takes units [T w / G, T (w + 1) / G); the block holding unit t is ((t + 1) G - 1) / T;
+// a segment is a share's part of an item's key tile units.  Segment (item j, block w) uses slot j + w: that sum
+// grows along the segments, so slots are distinct, at most n_items + G - 1 of them.
+constexpr int kMaxItems = 4096;   // items of a spread launch (the prefix sums live in LDS)
+constexpr int kItemCost = 8;      // units of an item before its key tiles
+constexpr int kMinShare = 16;     // units per block at least: shorter launches use fewer blocks
+
+template <int G8, bool BF16>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
+                    const int32_t* kv_lens, int H, int gs, int n_qtiles, int bh_n, int spread, float* part,
+                    int32_t* ctr, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h) {
+  static_assert(kWaves == 8, "slot layout");
+  __shared__ int pfx[kMaxItems + 1];
+  __shared__ int wsum[kWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qb = kWaves * (16 / gs);
+  const int n_items = bh_n * n_qtiles;
+  int w = (int)blockIdx.x, G = 0, j;
+  int64_t pos = 0, e = 0, T = 0;
+  if (spread) {
+    // prefix sums of the items' key tile counts: thread t counts items per t .. per t + per - 1
+    const int per = (n_items + 64 * kWaves - 1) / (64 * kWaves);   // <= 8
+    int cnt[8], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int jj = tid * per + k;
+      cnt[k] = 0;
+      if (k < per && jj < n_items) {
+        const int bh = jj / n_qtiles, b = bh / H;
+        const int nt = qtile_of(cu_q, cu_q_is_int64, kv_lens, b, jj - bh * n_qtiles, qb).ntiles;
+        cnt[k] = nt > 0 ? kItemCost + nt : 0;
+      }
+      sum += cnt[k];
+    }
+    int x = sum;   // inclusive scan over the wavefront
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int base = 0;
+    for (int v = 0; v < wave; ++v) base += wsum[v];
+    int excl = base + x - sum;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int jj = tid * per + k;
+      if (k < per && jj < n_items) pfx[jj] = excl;
+      excl += cnt[k];
+    }
+    if (tid == 64 * kWaves - 1) pfx[n_items] = base + x;
+    __syncthreads();
+    T = pfx[n_items];
+    if (T == 0) return;
+    G = (int)min((int64_t)gridDim.x, max((int64_t)1, T / kMinShare));
+    if (w >= G) return;
+    pos = T * w / G;
+    e = T * (w + 1) / G;
+    int lo = 0, hi = n_items;   // the item holding tile pos: pfx[lo] <= pos < pfx[lo + 1]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pfx[mid] <= pos) lo = mid; else hi = mid;
+    }
+    j = lo;
+  } else {   // one block per item, the latest (heaviest) query tiles first
+    j = (w % bh_n) * n_qtiles + n_qtiles - 1 - w / bh_n;
+  }
+  for (;;) {
+    const int bh = j / n_qtiles, qt = j - bh * n_qtiles, b = bh / H, h = bh - b * H;
+    const QTile Q = qtile_of(cu_q, cu_q_is_int64, kv_lens, b, qt, qb);
+    int64_t p1 = Q.ntiles;
+    int i0 = 0, nseg = 1, ord = 0;
+    float* slots = nullptr;
+    if (spread) {
+      const int64_t t0 = pfx[j] + kItemCost;   // units of the item's key tiles: [t0, p1)
+      p1 = pfx[j + 1];
+      if (max(pos, t0) >= min(e, p1)) return;   // the share ends before the item's first key tile
+      const int wf = (int)(((t0 + 1) * G - 1) / T);   // the blocks holding the item's first and last key tile
+      const int wl = (int)((p1 * G - 1) / T);
+      i0 = (int)(max(pos, t0) - t0);
+      nseg = wl - wf + 1;
+      ord = w - wf;
+      slots = part + (int64_t)(j + wf) * kSlotFloats;
+      p1 = min(e, p1) - t0;
+    } else if (Q.ntiles == 0) {
+      return;
+    }
+    attend_segment<G8, BF16>(S, q, sq_n, sq_h, Q, b, h, H, gs, i0, (int)p1, nseg, ord, slots, ctr + (spread ? j : 0), scale, out,
+                             out_f32, so_n, so_h);
+    if (!spread) return;
+    p1 = pfx[j + 1];
+    pos = min(e, p1);
+    if (pos >= e) return;
+    do ++j; while (pfx[j + 1] == pfx[j]);   // the next item with tiles (pos < e <= T: one exists)
+    __syncthreads();                        // the segment's LDS is free again
+  }
+}
+
+// query tiles of a launch, and the counter area at the start of the spread workspace (256-byte aligned)
+int prefill_qtiles(int max_q, int H, int Hq) {
+  const int qb = kWaves * (16 / (Hq / H));   // queries per block
+  return (max_q + qb - 1) / qb;
+}
+int64_t prefill_counter_bytes(int bh_n, int n_qtiles) { return ((int64_t)bh_n * n_qtiles * 4 + 255) & ~(int64_t)255; }
+
 }  // namespace
 
 extern "C" {
+
+int kvt_prefill_work_bytes(int batch, int H, int Hq, int max_q, int spread_blocks, int64_t* bytes) {
+  if (bytes == nullptr || batch < 0 || H <= 0 || Hq % H != 0 || Hq / H > 16 || max_q < 0 || spread_blocks < 0)
+    return KVT_EINVAL;
+  if (spread_blocks == 0 || batch == 0 || max_q == 0) {
+    *bytes = 0;
+    return KVT_OK;
+  }
+  const int64_t n_items = (int64_t)batch * H * prefill_qtiles(max_q, H, Hq);
+  if (n_items > kMaxItems || spread_blocks > (1 << 20)) return KVT_ERANGE;
+  *bytes = prefill_counter_bytes((int)n_items, 1) + (n_items + spread_blocks - 1) * kSlotFloats * 4;
+  return KVT_OK;
+}
 
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,
                      const void* kv_lens, int batch, int max_q, int H, int Hq, int D, int group8, const void* k4,
@@ -831,8 +1097,11 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
                      const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                      const void* k_bf16, const void* v_bf16, int64_t kb_rows, int64_t kb_n, int64_t kb_h,
                      int64_t vb_n, int64_t vb_h, float scale, void* out, int out_f32, int64_t so_n, int64_t so_h,
-                     void* stream) {
+                     int spread_blocks, void* work, int64_t work_bytes, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD || Hq / H > 16 || max_q < 0) return KVT_EINVAL;
+  if (spread_blocks < 0) return KVT_EINVAL;
+  // Q rows are read 8 channels (16 bytes) at a time
+  if ((reinterpret_cast<uintptr_t>(q) & 15) != 0 || sq_n % 8 != 0 || sq_h % 8 != 0) return KVT_EINVAL;
   if ((k_bf16 == nullptr) != (v_bf16 == nullptr)) return KVT_EINVAL;
   const bool bf16 = k_bf16 != nullptr;
   // 32-bit byte offsets inside each buffer
@@ -846,13 +1115,26 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
           (const int64_t*)ring_base, (const int32_t*)ring_len, (const int64_t*)ring_start,
           (const int32_t*)page_table, pt_stride,               (uint32_t)pool_rows,      (const uint16_t*)k_bf16,
           (const uint16_t*)v_bf16,   kb_n, kb_h, vb_n, vb_h, kb_rows};
-  const int qb = kWaves * (16 / (Hq / H));   // queries per block
-  const int n_qtiles = (max_q + qb - 1) / qb;
-  const dim3 grid((unsigned)n_qtiles, (unsigned)(batch * H));
+  const int n_qtiles = prefill_qtiles(max_q, H, Hq);
+  const int bh_n = batch * H;
+  float* part = nullptr;
+  int32_t* ctr = nullptr;
+  if (spread_blocks > 0) {
+    int64_t need = 0;
+    const int rc = kvt_prefill_work_bytes(batch, H, Hq, max_q, spread_blocks, &need);
+    if (rc != KVT_OK) return rc;
+    if (work == nullptr || work_bytes < need) return KVT_EINVAL;
+    ctr = static_cast<int32_t*>(work);
+    part = reinterpret_cast<float*>(static_cast<char*>(work) + prefill_counter_bytes(bh_n, n_qtiles));
+  } else if ((int64_t)n_qtiles * bh_n > 0x7fffffffLL) {
+    return KVT_ERANGE;
+  }
+  const dim3 grid((unsigned)(spread_blocks > 0 ? spread_blocks : n_qtiles * bh_n));
   hipStream_t st = (hipStream_t)stream;
 #define KVT_PF(G, B)                                                                                              \
   hipLaunchKernelGGL((prefill_mfma_kernel<G, B>), grid, dim3(64 * kWaves), 0, st, S, (const uint16_t*)q, sq_n, sq_h, cu_q,  \
-                     cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, scale, out, out_f32, so_n, so_h)
+                     cu_q_is_int64, (const int32_t*)kv_lens, H, Hq / H, n_qtiles, bh_n, spread_blocks > 0, part, ctr,  \
+                     scale, out, out_f32, so_n, so_h)
   if (bf16) {
     KVT_PF(64, true);
   } else if (group8 == 64) {

@@ -15,6 +15,7 @@ random order and are recorded in a per-sequence page table (int32 [S, max_pages]
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
@@ -562,16 +563,47 @@ def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, 
     return out
 
 
+_prefill_ws: dict = {}   # device index -> zeroed kvt_prefill_attn workspace (counters stay zero between calls)
+_cu_count: dict = {}
+PREFILL_MAX_ITEMS = 4096   # (sequence, KV head, query tile) items of a spread prefill launch
+
+
+def prefill_spread_blocks(items: int, device: torch.device) -> int:
+    """Blocks of a spread prefill launch: one per CU (a block fills a CU), for launches of at most
+    PREFILL_MAX_ITEMS query tiles; 0 (one block per query tile) beyond."""
+    if items > PREFILL_MAX_ITEMS:
+        return 0
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _cu_count:
+        _cu_count[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _cu_count[idx]
+
+
+def prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The device's cached prefill workspace, at least nbytes, zeroed when (re)allocated.  Calls on one stream
+    share it; calls that may overlap (several streams) pass their own `work`."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _prefill_ws.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _prefill_ws[idx] = ws
+    return ws
+
+
 def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: torch.Tensor,
                      kv_lens: Optional[torch.Tensor] = None, max_q: Optional[int] = None,
                      k_src: Optional[torch.Tensor] = None, v_src: Optional[torch.Tensor] = None,
-                     out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+                     spread: Optional[int] = None, work: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal prefill attention of the chunk queries q (bf16 [total_q, Hq, D]; sequence b = cache sequence b owns
     rows cu_q[b] .. cu_q[b+1]) over the tiered cache of `layer`, which must already hold the chunk: the queries sit
     at positions kv_lens[b] - q_len .. kv_lens[b] - 1 (kv_lens defaults to the cache lengths) and each attends to
     every position up to its own (patches/kv_paged_prefix.py:200).  k_src / v_src (bf16 [positions, H, D], batch 1):
-    read keys from these rows instead, as the reference does for a chunk without a prefix.  Returns out
-    ([total_q, Hq, D], bf16 like the reference or fp32)."""
+    read keys from these rows instead, as the reference does for a chunk without a prefix.  spread: blocks that
+    share the launch's key tiles equally, splitting query tiles where a share ends and merging the pieces in the
+    kernel (0: one block per query tile, the latest first; default prefill_spread_blocks); work: a zeroed uint8
+    workspace of kvt_prefill_work_bytes (default: the device's cached one, allocated on first use -- call once
+    before a graph capture).  Returns out ([total_q, Hq, D], bf16 like the reference or fp32)."""
     assert q.dim() == 3 and q.dtype == torch.bfloat16 and q.stride(2) == 1 and q.shape[2] == cache.D
     assert cu_q.dtype in (torch.int32, torch.int64) and cu_q.is_contiguous() and cu_q.is_cuda
     batch = cu_q.shape[0] - 1
@@ -595,9 +627,19 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
             raise ValueError("k_src / v_src hold fewer rows than the context length")
     elif max((cache.hot_start(s) for s in range(batch)), default=0) > 8192 * 64:
         raise ValueError("kvt_prefill_attn: paged key ranges beyond 524,288 positions are not supported")
-    _lib.require_device(q, out, k_src, v_src)
+    _lib.require_device(q, out, k_src, v_src, work)
+    if q.data_ptr() % 16 or q.stride(0) % 8 or q.stride(1) % 8:
+        raise ValueError("kvt_prefill_attn: q rows must start at 16-byte boundaries (strides multiples of 8)")
     if batch == 0 or max_q == 0:
         return out
+    if spread is None:
+        spread = prefill_spread_blocks(-(-max_q // (8 * (16 // (Hq // H)))) * batch * H, q.device)
+    need = ctypes.c_int64(0)
+    _lib.call("kvt_prefill_work_bytes", batch, H, Hq, int(max_q), int(spread), ctypes.byref(need))
+    if need.value and work is None:
+        work = prefill_workspace(q.device, need.value)
+    if work is not None and (work.dtype != torch.uint8 or not work.is_contiguous() or work.numel() < need.value):
+        raise ValueError(f"kvt_prefill_attn: work must be a contiguous uint8 tensor of at least {need.value} bytes")
     _lib.call("kvt_prefill_attn", q.data_ptr(), q.stride(0), q.stride(1), cu_q.data_ptr(),
               int(cu_q.dtype == torch.int64), kv_lens.data_ptr(), batch, max_q, H, Hq, D, cache.group8,
               cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
@@ -609,5 +651,5 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
               k_src.stride(0) if k_src is not None else 0, k_src.stride(1) if k_src is not None else 0,
               v_src.stride(0) if v_src is not None else 0, v_src.stride(1) if v_src is not None else 0,
               1.0 / math.sqrt(D), out.data_ptr(), int(out.dtype == torch.float32), out.stride(0), out.stride(1),
-              _lib.stream())
+              int(spread), _lib.ptr(work), work.numel() if work is not None else 0, _lib.stream())
     return out

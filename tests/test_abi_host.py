@@ -19,6 +19,31 @@ def test_library_exports_header_symbols(kvt_pkg):
     lib.lib()   # binding with argtypes succeeds
 
 
+def test_prefill_work_bytes(kvt_pkg):
+    """Workspace of a spread prefill launch: a 4-byte counter per (sequence, KV head, query tile of 128 rows), padded
+    to 256 bytes, then one 132,096-byte slot (O of 128 rows x 256 dims, m and l of 128 rows, fp32) per query tile
+    and per block beyond the first."""
+    lib = kvt_pkg._lib
+    need = ctypes.c_int64(-1)
+
+    def work(*args):
+        lib.call("kvt_prefill_work_bytes", *args, ctypes.byref(need))
+        return need.value
+
+    slot = (128 * 256 + 128 * 2) * 4
+    assert slot == 132_096
+    assert work(1, 2, 16, 2048, 0) == 0                        # one block per query tile: no workspace
+    assert work(1, 2, 16, 2048, 256) == 1024 + (256 + 255) * slot
+    # 24 / 2 heads: a wavefront's 16 rows hold one query (12 rows), so a tile is 8 queries: 13 tiles of 100
+    assert work(3, 2, 24, 100, 7) == 512 + (6 * 13 + 6) * slot
+    assert work(2, 2, 16, 0, 3) == 0
+    for bad in ((1, 2, 16, 64, -1), (1, 2, 15, 64, 2), (1, 1, 32, 64, 2)):
+        with pytest.raises(ValueError):
+            work(*bad)
+    with pytest.raises(ValueError):   # more than 4,096 query tiles
+        work(17, 2, 16, 2048, 256)
+
+
 def test_ring_slots_from_env(kvt_pkg, monkeypatch):
     from kvtier.tiered_kv_pool import ring_slots_from_env
     for bad in ("0", "-8", "100", "abc"):

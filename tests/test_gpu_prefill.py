@@ -173,8 +173,11 @@ def test_prefill_tail_of_small_weights(kvt_pkg):
         assert float(e2.max()) < 2e-3 and float(e2.mean()) < 1e-3, (src, float(e2.max()))
 
 
-def test_prefill_two_sequences_cache(kvt_pkg):
-    """Two sequences with their own rings and interleaved pages, chunks of 50 and 33 queries (int64 cu_q)."""
+@pytest.mark.parametrize("spread", [None, 0, 5])
+def test_prefill_two_sequences_cache(kvt_pkg, spread):
+    """Two sequences with their own rings and interleaved pages, chunks of 50 and 33 queries (int64 cu_q); spread
+    launches by the default rule (one block per CU), none, and 5 blocks (shares that cross from one sequence to the
+    other; the shorter sequence's last query tile has no queries and no key tiles)."""
     from kvtier.kvt import PosTieredCache, kvt_prefill_attn
     gen = torch.Generator().manual_seed(13)
     och = ref.outlier_channels(H, D, 8, gen)
@@ -205,13 +208,49 @@ def test_prefill_two_sequences_cache(kvt_pkg):
     nq = [50, 33]
     q = ref.make_q(HQ, D, gen, n=sum(nq))
     cu = torch.tensor([0, 50, 83], dtype=torch.int64, device=dev)
-    out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32).cpu()
+    out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32, spread=spread).cpu()
     for s, (q0, q1) in enumerate(((0, 50), (50, 83))):
         kk, vv = oc.rows(s)
         L = kk.shape[0]
         exp = _oracle_chunk(q[q0:q1], L - (q1 - q0), kk, vv)
         err = (out[q0:q1] - exp).abs()
         assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (s, float(err.max()), float(err.mean()))
+
+
+@pytest.mark.parametrize("spread", [0, 7, 256, 1000])
+def test_prefill_spread(kvt_pkg, spread):
+    """Spread launches (blocks sharing the key tiles equally, query tiles split where a share ends and merged in the
+    kernel by the block that finishes last): chunks of 400 and 600 queries over ring 256, so the second chunk's
+    query tiles read up to 32 key tiles across INT4 pages and the ring (hot_start 744, inside a tile), and the
+    first chunk's come from the bf16 source.  7 blocks: every block walks many query tiles; 1,000: fewer blocks are
+    used (at least 8 key tiles each), query tiles split into several pieces.  Every case matches the oracle; a
+    repeated call and a call with a fresh workspace give the same bits (the merge is a fixed sum over the pieces,
+    whichever block merges); the counters are back at zero after each call."""
+    from kvtier.kvt import kvt_prefill_attn
+    import ctypes
+    from kvtier import _lib
+    for a, n, xk, xv, dc, oc, gen in _chunked([400, 600], 256, seed=31):
+        q = ref.make_q(HQ, D, gen, n=n).to(dev)
+        cu = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        src = dict(k_src=xk.to(dev), v_src=xv.to(dev)) if a == 0 else {}
+        kk, vv = (xk, xv) if a == 0 else oc.rows(0)
+        exp = _oracle_chunk(q.cpu(), a, kk, vv)
+        need = ctypes.c_int64(0)
+        _lib.call("kvt_prefill_work_bytes", 1, H, HQ, n, spread, ctypes.byref(need))
+        work = torch.zeros(max(need.value, 1), dtype=torch.uint8, device=dev)
+        out = kvt_prefill_attn(dc, 0, q, cu, out_dtype=torch.float32, spread=spread, work=work, **src)
+        err = (out.cpu() - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (a, spread, float(err.max()), float(err.mean()))
+        n_ctr = H * -(-n // 16)
+        for _ in range(2):
+            again = kvt_prefill_attn(dc, 0, q, cu, out_dtype=torch.float32, spread=spread, work=work, **src)
+            assert torch.equal(again, out), (a, spread)
+            assert int(work[:4 * n_ctr].count_nonzero()) == 0, (a, spread)
+        fresh = torch.zeros(max(need.value, 1), dtype=torch.uint8, device=dev)
+        assert torch.equal(kvt_prefill_attn(dc, 0, q, cu, out_dtype=torch.float32, spread=spread, work=fresh, **src),
+                           out), (a, spread)
+        outb = kvt_prefill_attn(dc, 0, q, cu, spread=spread, work=work, **src)
+        assert torch.equal(outb, out.to(torch.bfloat16)), (a, spread)
 
 
 BIG_POS = (5, 40, 150, 250, 300)
