@@ -250,7 +250,7 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
  * KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
  * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device).
  * spread_blocks > 0: that many blocks share the launch's key tiles equally (query tiles are split where a share
- * ends; the block that finishes a query tile's last piece merges the pieces in piece order), instead of one block
+ * ends; of a query tile's pieces, the one that finishes last merges them in piece order), instead of one block
  * per query tile -- the latest query tiles of a causal chunk see up to a chunk length more keys than the earliest,
  * so one block per CU with equal shares ends them all together.  It needs `work`, at least kvt_prefill_work_bytes
  * bytes, whose counter area (its first bytes) is zero before the first call -- each call leaves it at zero again;

@@ -223,7 +223,7 @@ def test_prefill_spread(kvt_pkg, spread):
     kernel by the block that finishes last): chunks of 400 and 600 queries over ring 256, so the second chunk's
     query tiles read up to 32 key tiles across INT4 pages and the ring (hot_start 744, inside a tile), and the
     first chunk's come from the bf16 source.  7 blocks: every block walks many query tiles; 1,000: fewer blocks are
-    used (at least 8 key tiles each), query tiles split into several pieces.  Every case matches the oracle; a
+    used (shares of at least 16 units: key tiles plus 8 per query tile), query tiles split into several pieces.  Every case matches the oracle; a
     repeated call and a call with a fresh workspace give the same bits (the merge is a fixed sum over the pieces,
     whichever block merges); the counters are back at zero after each call."""
     from kvtier.kvt import kvt_prefill_attn
