@@ -253,6 +253,55 @@ def test_prefill_spread(kvt_pkg, spread):
         assert torch.equal(outb, out.to(torch.bfloat16)), (a, spread)
 
 
+@pytest.mark.parametrize("spread", [None, 3, 64])
+def test_prefill_spread_three_sequences(kvt_pkg, spread):
+    """Three sequences (rings 64 / 128 / 256, histories of 700 / 1,500 / 300 positions, mostly in INT4 pages) with
+    chunks of 300 / 40 / 520 queries in one launch: spread shares cross from one sequence (and KV head) to the next,
+    the short chunk's later query tiles are empty, and 3 blocks each walk many query tiles; every query against the
+    oracle."""
+    from kvtier.kvt import PosTieredCache, kvt_prefill_attn
+    gen = torch.Generator().manual_seed(41)
+    och = ref.outlier_channels(H, D, 8, gen)
+    rings, hist, nq = [64, 128, 256], [700, 1500, 300], [300, 40, 520]
+    n_pages = 64
+    dc = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=sum(rings), max_seqs=3, max_pages=48, device=dev,
+                        page_seed=5)
+    oc = ref.PosTieredCache(H, D, n_pages=n_pages, ring_total=sum(rings))
+    alloc = ref.PageAllocator(n_pages, seed=5)
+    base = 0
+    for r in rings:
+        dc.add_seq(r)
+        oc.add_seq(base, r)
+        base += r
+    left = [h + n for h, n in zip(hist, nq)]
+    while any(left):   # appends of at most 64 positions per sequence and step (never more than a ring)
+        seqs = [s for s in range(3) if left[s] > 0]
+        cnt = [min(64, left[s]) for s in seqs]
+        plan = dc.plan_append(seqs, cnt)
+        ks, vs = [], []
+        for s_, m in zip(seqs, cnt):
+            xk, xv = ref.make_kv(m, H, D, gen, och)
+            oc.plan_pages(s_, m, alloc)
+            oc.append(s_, xk, xv)
+            ks.append(xk)
+            vs.append(xv)
+            left[s_] -= m
+        dc.append(0, plan, torch.cat(ks).to(dev), torch.cat(vs).to(dev))
+        dc.commit(plan)
+    q = ref.make_q(HQ, D, gen, n=sum(nq))
+    cu = torch.tensor([0, nq[0], nq[0] + nq[1], sum(nq)], dtype=torch.int32, device=dev)
+    out = kvt_prefill_attn(dc, 0, q.to(dev), cu, out_dtype=torch.float32, spread=spread).cpu()
+    q0 = 0
+    for s_ in range(3):
+        kk, vv = oc.rows(s_)
+        L = kk.shape[0]
+        assert L == hist[s_] + nq[s_]
+        exp = _oracle_chunk(q[q0:q0 + nq[s_]], L - nq[s_], kk, vv)
+        err = (out[q0:q0 + nq[s_]] - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (s_, spread, float(err.max()), float(err.mean()))
+        q0 += nq[s_]
+
+
 BIG_POS = (5, 40, 150, 250, 300)
 
 
