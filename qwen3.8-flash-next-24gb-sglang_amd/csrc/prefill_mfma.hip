@@ -726,6 +726,10 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[nt][r] = d[nt][r];
     }
+    // the softmax (scores -> row max -> exponentials -> P) is the chain every P.V product waits for: at a higher
+    // wave priority its instructions issue ahead of the other wavefront's conversion and products on the SIMD
+    // (3 % less time per prompt than without)
+    __builtin_amdgcn_s_setprio(1);
     // causal / end mask, only on the tiles that reach the block's first query or the key end
     if (t0 + kT > qmin || t0 + kT > kend) {
 #pragma unroll
@@ -772,6 +776,7 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
       }
       pa = __builtin_bit_cast(h8, u4v{hw[0], hw[1], hw[2], hw[3]});
     }
+    __builtin_amdgcn_s_setprio(0);
     // ---- O += P V / 128: B = dim 16 c + n16 of keys {4 kb .. +3, 16 + 4 kb .. +3}: two transposing 8-byte reads.
     // Step c: the product of dims 16 c .., the V operand of step c + kAheadV read from LDS, one piece of tile
     // it + 1's V rows.
