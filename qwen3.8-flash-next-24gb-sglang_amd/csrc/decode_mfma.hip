@@ -567,8 +567,10 @@ KVT_DEV void cold_step(const ColdCtx& C, WaveArea& W, const ColdRound& Q, ColdHa
   cold_qk(W.cold[S ^ 1], M.qop, M.kbias, M.bexp, M.cscale, M.nm, s);
   wait_lgkm0();                           // ta's V reads are done before its stage takes new V copies
   cold_issue_v(C, W.cold[S], rowc);       // unconditional: no branch splits the math above
+  __builtin_amdgcn_s_setprio(1);   // the softmax chain ahead of the other wavefront's work on the SIMD
   cold_mask(s, Q.n(hd.tb));
   p16 = cold_softmax(s, acc, m_run, l_run);
+  __builtin_amdgcn_s_setprio(0);
   hd.ta = hd.tb;
   hd.tb = hd.tc;
   hd.tc = hd.td;
@@ -781,6 +783,7 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
   float s[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) s[r] = (4 * kb + r) < n ? sc[r] * cscale : -INFINITY;
+  __builtin_amdgcn_s_setprio(1);   // (as on the paged tiles)
   // ---- online softmax over the tile
   float mloc = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
   mloc = max_xor16_32(mloc);
@@ -804,6 +807,7 @@ KVT_DEV void hot_compute(const HotCtx& C, const HotStage& st, int64_t p0, int n,
     psum += s[r];
   }
   l_run += psum;
+  __builtin_amdgcn_s_setprio(0);
   // ---- P.V on 16x16x16 (k = tokens 4 kb .. + 3 of the lane's block), same accumulator layout as the paged tiles:
   // acc[a] += (P * s_v(t, g(a))) * V(t, 16 a + j).  B from ds_read_b64_tr_b8: source lane 2 k8 + p supplies 8 bytes
   // (channels 16 a + 8 p ..) of token 4 kb + (k8 & 3), block a = a0 (k8 < 4) or a0 + 4; lane j then holds channel
