@@ -992,7 +992,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   int w = (int)blockIdx.x, G = 0, j;
   int64_t pos = 0, e = 0, T = 0;
   if (spread) {
-    // prefix sums of the items' key tile counts: thread t counts items per t .. per t + per - 1
+    // prefix sums of the item costs (units): thread t counts items per t .. per t + per - 1
     const int per = (n_items + 64 * kWaves - 1) / (64 * kWaves);   // <= 8
     int cnt[8], sum = 0;
 #pragma unroll
@@ -1031,7 +1031,7 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     if (w >= G) return;
     pos = T * w / G;
     e = T * (w + 1) / G;
-    int lo = 0, hi = n_items;   // the item holding tile pos: pfx[lo] <= pos < pfx[lo + 1]
+    int lo = 0, hi = n_items;   // the item holding unit pos: pfx[lo] <= pos < pfx[lo + 1]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (pfx[mid] <= pos) lo = mid; else hi = mid;
@@ -1060,8 +1060,8 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
     } else if (Q.ntiles == 0) {
       return;
     }
-    attend_segment<G8, BF16>(S, q, sq_n, sq_h, Q, b, h, H, gs, i0, (int)p1, nseg, ord, slots, ctr + (spread ? j : 0), scale, out,
-                             out_f32, so_n, so_h);
+    attend_segment<G8, BF16>(S, q, sq_n, sq_h, Q, b, h, H, gs, i0, (int)p1, nseg, ord, slots,
+                             ctr + (spread ? j : 0), scale, out, out_f32, so_n, so_h);
     if (!spread) return;
     p1 = pfx[j + 1];
     pos = min(e, p1);
