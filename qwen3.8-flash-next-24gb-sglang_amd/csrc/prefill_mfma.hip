@@ -561,7 +561,7 @@ KVT_DEV void v_step(int j, const RawV& x, uint32_t a[4], uint32_t b[4], uint8_t*
   if (j == w0 + 1) *reinterpret_cast<uint4*>(vrows + (tp + 16) * kVRow + 16 * db) = make_uint4(b[0], b[1], b[2], b[3]);
 }
 
-constexpr int kAheadK = 3, kAheadV = 4;   // LDS operand reads issued this many matrix steps ahead
+constexpr int kAheadK = 2, kAheadV = 4;   // LDS operand reads issued this many matrix steps ahead
 constexpr int kWaves = 8;               // 2 per SIMD: each wavefront 16 rows (16 / gs queries x gs heads)
 
 // The queries of one query tile (qb queries of sequence b) and the keys they see.
