@@ -947,20 +947,22 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
   }
   // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
   // column n16 of block c = dim 16 c + n16
+  // (one correctly rounded division per row: 128 / l, exact for a single visible key, where l = 1)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * kb + i, rq = r / gs, hq = r - rq * gs;
     const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
     if (rq < qpw && qi < q_len) {
       const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
+      const float rl = 128.0f / lrow[i];
       if (out_f32) {
         float* orow = reinterpret_cast<float*>(out) + o0;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = (acc[c][i] * 128.0f) / lrow[i];
+        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[c][i] * rl;
       } else {
         uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
 #pragma unroll
-        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne((acc[c][i] * 128.0f) / lrow[i]);
+        for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[c][i] * rl);
       }
     }
   }
