@@ -183,16 +183,15 @@ def pmc_sample(impl: str) -> None:
     """The workload run under `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE): 12 eager decode layers (split-K +
     combine) after a warm-up, then one device copy of CAL_BYTES whose counter reading calibrates the counter."""
     import kvtier  # noqa: F401
-    from kvtier.kvt import kvt_decode_attn
+    from kvtier.kvt import kvt_decode_attn, kvt_decode_plan
     cache, q = build_cache()
     ws = {}
     out = torch.empty(1, HQ, D, dtype=torch.float32, device="cuda")
-    for layer in range(LAYERS):
-        kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws)
-    torch.cuda.synchronize()
-    for layer in range(LAYERS):
-        kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws)
-    torch.cuda.synchronize()
+    for _ in range(2):
+        plan = kvt_decode_plan(cache, HQ, workspace=ws) if impl == "mfma" else None
+        for layer in range(LAYERS):
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws, plan=plan, check_q=False)
+        torch.cuda.synchronize()
     src = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -837,7 +836,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     the decode launches as timed by events around the eager calls, and the decode of the final state replayed as a
     HIP graph (the device's own rate)."""
     import kvtier  # noqa: F401
-    from kvtier.kvt import PosTieredCache, kvt_decode_attn
+    from kvtier.kvt import PosTieredCache, kvt_decode_attn, kvt_decode_plan
     layers = LAYERS if ragged else 1
     if ragged:
         gl = torch.Generator().manual_seed(4)
@@ -899,8 +898,9 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         for layer in range(layers):
             cache.append(layer, plan, knew, vnew)
         cache.commit(plan)
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
         for layer in range(layers):
-            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 
     for _ in range(args.warmup):
         host_step()
@@ -919,8 +919,9 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         cache.launch_plan(dplan)
         for layer in range(layers):
             cache.append(layer, dplan, knew, vnew)
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
         for layer in range(layers):
-            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 
     dev_step()
     torch.cuda.synchronize()
@@ -946,8 +947,9 @@ def decode_steps_workload(args, ragged: bool) -> dict:
 
     # decode alone over the final state (every layer, one graph): the device's decode rate
     def dec_only():
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
         for layer in range(layers):
-            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws)
+            kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 
     dec_only()   # (eagerly first: the split map of the final lengths)
     torch.cuda.synchronize()
@@ -969,7 +971,8 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         "metric": name + ": us per step", "value": round(wall * 1e6, 1), "unit": "us", "higher_is_better": False,
         "steps": steps, "warmup": args.warmup, "dtype": "f16-mfma/f32", "data": "synthetic",
         "config": {"workload": name, "lens": lens, "rings": rings, "impl": args.impl,
-                   "step": "device plan + append of every layer + decode of every layer, one HIP graph per step"},
+                   "step": "device append plan + append of every layer + decode plan + decode of every layer, one "
+                           "HIP graph per step"},
         "device_us_per_step": round(dev_s * 1e6, 1),
         "wall_over_device": round(wall / dev_s, 3),
         "host_planned_eager_us_per_step": round(wall_host * 1e6, 1),
@@ -1034,8 +1037,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--impl", default=os.environ.get("KVT_DECODE_IMPL", "mfma"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--fused-combine", action="store_true",
-                    help="merge the split partials inside the split-K launch instead of in the combine kernel")
     ap.add_argument("--workload", default="decode262k", choices=["decode262k", "prefill10k", "decode10k", "ragged", "append", "sparse", "slots", "paged_prefix", "lazy"],
                     help="decode262k (default): the headline line; the others measure the remaining configurations")
     ap.add_argument("--hq", type=int, default=HQ, help="query heads of the sparse workload (2 KV heads)")
@@ -1065,16 +1066,19 @@ def main():
         print(json.dumps(line))
         return
     import kvtier  # noqa: F401
-    from kvtier.kvt import kvt_decode_attn
+    from kvtier.kvt import kvt_decode_attn, kvt_decode_plan
 
     cache, q = build_cache()
     ws = {}
     outs = [torch.empty(1, HQ, D, dtype=torch.float32, device="cuda") for _ in range(LAYERS)]
 
     def step(events=None):
+        # the step's decode plan (every block's ranges and first tile rows, shared by the 12 layers), then per layer
+        # the split-K launch + the combine; the synthetic queries are in the fp16 range (no per-call host check)
+        plan = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
         for layer in range(LAYERS):
             kvt_decode_attn(cache, layer, q[layer], out=outs[layer], impl=args.impl, workspace=ws, events=events,
-                            fused_combine=args.fused_combine)
+                            plan=plan, check_q=False)
 
     for _ in range(args.warmup):
         step()
@@ -1144,7 +1148,8 @@ def main():
             "workload": "decode 262144-token context x 12 layers: 16 Q / 2 KV heads, D 256, INT8-G64 ring 8192 + "
                         "253952 tokens in 3968 INT4-G32 pages (permuted), batch 1",
             "impl": args.impl,
-            "combine": "fused (in the split-K launch)" if args.fused_combine else "combine kernel",
+            "kernel": ("full-row split-K (both KV heads per wavefront) with the step's decode plan + combine"
+                       if args.impl == "mfma" else "reference-precision split-K + combine"),
             "kv_bytes_per_layer": bytes_layer,
             "kv_bytes_per_step": bytes_step,
         },

@@ -180,33 +180,44 @@ int kvt_decode_ref(int mode, const void* q, int64_t q_stride_b, const void* seq_
                    const void* owner, int64_t ring_mask, float scale, int chunk, int n_chunks, void* part_o,
                    void* part_ml, void* stream);
 
-/* Split-K GQA decode attention on the matrix cores (v_mfma_f32_16x16x32_f16) over position rings + page tables
- * (the mode-0 layout of kvt_decode_ref): QK^T with exact fp16 integer codes and the per-group scales folded in
- * fp32; P.V with the raw INT4 codes as exact fp16 values and the V scale folded into fp16 P; fp32 accumulation.
- * Each split is one block of 8 wavefronts (one block per CU) over a position range of equal cost; its 32-position
- * tiles go to the wavefronts either first come (flags & KVT_DECODE_DYNAMIC: the wavefronts finish together; the
- * fp32 summation order, and so the last bits of the result, then depend on timing) or in a fixed order
- * (bit-reproducible).  split_map NULL: every (sequence, KV head) gets n_splits splits; otherwise split_map (int32
- * [n_map][3] = {sequence, split index, splits of that sequence}) lists the splits (per-sequence counts for ragged
- * batches) and n_splits is the partial slot stride per (sequence, head).  Partials in the layout of kvt_decode_ref;
- * merge them with kvt_decode_combine(chunk = 0, split_counts).  Hq / H <= 16, D = 256, q and q_stride_b 16-byte
- * aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte offsets are 32-bit: pool_rows * H * D / 2 <
- * 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the compact gather + FA2 pair (flat patch
- * sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode.
- * counters non-NULL (int32 [batch * H * 4], zero before the first call; every call leaves them zero): the launch
- * also merges the partials into out_f32 and/or out_bf16 ([batch, Hq, D], batch stride out_stride_b elements), so no
- * kvt_decode_combine is needed: after the work blocks the grid holds 8 fixup blocks per (sequence, KV head); a work
- * block writes its partial with device-coherent stores and counts itself, a fixup block waits (bounded poll) for its
- * item's count and merges 1/8 of the item's output over all partials in a fixed order (deterministic with the fixed
- * tile order).  Fixup blocks start only on CUs that work blocks have left (every work block is dispatched first).
- * Calls sharing counters must not run concurrently. */
+/* Split-K GQA decode attention on the matrix cores over position rings + page tables (the mode-0 layout of
+ * kvt_decode_ref): QK^T with exact fp16 integer codes and the per-group scales folded in fp32; P.V with the raw INT4
+ * codes as exact fp16 values and the V scale folded into fp16 P; fp32 accumulation.  Each split is one block of 8
+ * wavefronts (one block per CU) over a position range of equal cost; its tiles go to the wavefronts either first come
+ * (flags & KVT_DECODE_DYNAMIC: the wavefronts finish together; the fp32 summation order, and so the last bits of the
+ * result, then depend on timing) or in a fixed order (bit-reproducible).
+ * Two kernels: for H = 2 and Hq / H <= 8 (unless flags & KVT_DECODE_HEADWISE) a block covers both KV heads of its
+ * positions and reads whole pool rows (16-position tiles of both heads per wavefront); otherwise a block covers one
+ * (sequence, KV head) (32-position tiles).  split_map NULL: every item -- a sequence for the full-row kernel, a
+ * (sequence, KV head) for the head-wise one -- gets n_splits splits; otherwise split_map (int32 [n_map][3] =
+ * {sequence, split index, splits of that sequence}) lists the splits (per-sequence counts for ragged batches), the
+ * grid has n_map blocks (full-row) or n_map x H (head-wise), and n_splits is the partial slot stride.  Partials in the
+ * layout of kvt_decode_ref (n_splits slots per (sequence, KV head)); merge them with kvt_decode_combine(chunk = 0,
+ * split_counts).  plan (full-row kernel only; NULL or a kvt_decode_plan output for the same grid): each block starts
+ * from its plan entry (ranges and first tile rows: one load before the first copies); an entry made for another
+ * length or ring placement of its sequence is detected and the block computes its ranges itself.  The plan's tile
+ * rows come from the page table at planning time: re-plan after the page table changes.  Hq / H <= 16, D = 256,
+ * group8 64 or 256, q and q_stride_b 16-byte aligned (else KVT_EINVAL); pool_rows = rows of the INT4 pool (byte
+ * offsets are 32-bit: pool_rows * H * D / 2 < 2^31, else KVT_ERANGE).  No reference counterpart: it replaces the
+ * compact gather + FA2 pair (flat patch sglang/qwen4exp-serving-73a255206f.patch:1832-1882) for dense decode. */
 #define KVT_DECODE_DYNAMIC 1
+#define KVT_DECODE_HEADWISE 2
 int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int batch, int H, int Hq, int D,
                     int group8, const void* k4, const void* v4, const void* ks4, const void* vs4, const void* rk,
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    int flags, void* counters, void* out_f32, void* out_bf16, int64_t out_stride_b, void* stream);
+                    int flags, const void* plan, void* stream);
+
+/* The decode plan of one step for the full-row kvt_decode_mfma grid (batch sequences x n_splits splits, or the n_map
+ * entries of split_map): per block 64 int32 words -- sequence, split, split count, ring length, length, ring start,
+ * ring base, first ring position, range [w0, w1), and the pool rows of the block's first 16 paged tiles -- computed
+ * from the device state (one thread per block, one small launch; capturable).  Shared by every layer of the step:
+ * a block's first copies then wait for one load instead of the length -> range -> page-table chain.  plan: int32
+ * [blocks * 64].  No reference counterpart (the reference's decode is FA2 over a gathered scratch). */
+int kvt_decode_plan(const void* seq_lens, const void* ring_len, const void* ring_start, const void* ring_base,
+                    const void* page_table, int64_t pt_stride, int batch, int n_splits, const void* split_map,
+                    int n_map, void* plan, void* stream);
 
 /* Merge the split-K partials: out[b, hq, :] = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c (fp32 and/or bf16
  * output, either may be NULL; batch stride out_stride_b elements).  chunk > 0: split c covers positions
@@ -224,7 +235,7 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
  * the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  The partials need batch * H * n_splits * (Hq / H) * (D + 2) * 4 bytes
  * (the o part rounded up to 256 bytes); more than 8 MiB returns KVT_ERANGE before anything is launched (the
- * 262,144-position headline at 128 splits per KV head needs 2.0 MiB).  split_map and split_counts (int32 [batch],
+ * 262,144-position headline at 256 splits needs 4.0 MiB).  split_map and split_counts (int32 [batch],
  * the splits of each sequence) go together, as for the pair of calls this replaces; out_f32 and / or out_bf16 as
  * kvt_decode_combine.  Every call on a GPU shares that GPU's scratch: calls that overlap on one GPU (concurrent
  * streams, other threads) race and must be serialized by the caller. */

@@ -47,7 +47,8 @@ SIGNATURES = {
     "kvt_decode_ref": [_I, _P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                        _L, _P, _L, _P, _P, _L, _F, _I, _I, _P, _P, _P],
     "kvt_decode_mfma": [_P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _F,
-                        _I, _P, _I, _P, _P, _I, _P, _P, _P, _L, _P],
+                        _I, _P, _I, _P, _P, _I, _P, _P],
+    "kvt_decode_plan": [_P, _P, _P, _P, _P, _L, _I, _I, _P, _I, _P, _P],
     "kvt_decode_mfma_noalloc": [_P, _L, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                                 _L, _F, _I, _P, _I, _P, _I, _P, _P, _L, _P],
     "kvt_decode_combine": [_P, _P, _I, _I, _I, _I, _I, _L, _P, _P, _P, _P, _L, _P],

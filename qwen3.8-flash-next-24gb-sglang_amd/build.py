@@ -7,7 +7,7 @@ Every .hip file under csrc/ is compiled to an object with hipcc (in parallel), t
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                               no packed fp32 VALU instructions
   no -ffast-math: rounding must follow IEEE round-to-nearest-even.
-Per file: decode_mfma.hip and decode_ref.hip preload the first kernel-argument dwords into SGPRs
+Per file: decode_mfma.hip, decode_rows.hip and decode_ref.hip preload the first kernel-argument dwords into SGPRs
 (-mllvm -amdgpu-kernarg-preload-count=16; the split-K kernel's arguments are ordered for it).
 """
 from __future__ import annotations
@@ -43,6 +43,7 @@ CFLAGS = [
 EXTRA_CFLAGS = {
     "decode_mfma.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
     "decode_ref.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "decode_rows.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

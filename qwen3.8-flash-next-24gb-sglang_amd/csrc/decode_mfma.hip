@@ -40,12 +40,13 @@
 // through fp16 P * s (P <= 1, so P * s stays in the fp16 range of the scale itself); fp32 accumulation.  A single
 // position returns exactly code * scale.
 
-#include "kvt_common.h"
+#include "decode_common.h"
 #include "kvtier.h"
 
 #include <mutex>
 
 using namespace kvt;
+using namespace kvt::dec;
 
 // Split partials of kvt_decode_mfma_noalloc: a file-scope device array (each GPU the library runs on holds its own
 // copy until the process ends).  Host code never uses this name as an address: scratch_base() resolves the device
@@ -55,19 +56,11 @@ static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u4v __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef int v2i __attribute__((ext_vector_type(2)));
-
 constexpr int kWaves = 8;          // wavefronts per block (one block per CU: all of the CU's LDS)
 constexpr int kD = 256;
 constexpr int kHotCost4 = 7;       // cost of a ring position when blocks split a sequence; a paged position costs 4
                                    // (measured: with 5 the blocks that hold ring positions finish last)
 constexpr int kBlockPages = 896;   // page ids of a block's paged range staged in LDS per round (14 x 64)
-constexpr float kLog2e = 1.4426950408889634f;
 
 struct PosArgs {
   const uint8_t* k4;
@@ -84,51 +77,6 @@ struct PosArgs {
   const int32_t* page_table;
   int64_t pt_stride;
 };
-
-KVT_DEV f4 mfma(h8 a, h8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0); }
-
-KVT_DEV h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
-KVT_DEV uint32_t as_u32(h2 h) { return __builtin_bit_cast(uint32_t, h); }
-KVT_DEV h8 as_h8(u4v u) { return __builtin_bit_cast(h8, u); }
-KVT_DEV u4v as_u4(h8 h) { return __builtin_bit_cast(u4v, h); }
-
-// (a & m) | o: one v_and_or_b32 when m and o are VGPR values the compiler cannot fold into literals (see
-// NibbleMasks).  Plain code, not inline assembly, so that the compiler's hazard checks see every write (an MFMA may
-// still be reading its source registers when the next instruction overwrites them).
-KVT_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t o) { return (a & m) | o; }
-
-// A value in a VGPR that the compiler treats as unknown (no literal folding, no instruction emitted here).
-KVT_DEV uint32_t opaque_vgpr(uint32_t x) {
-  asm("" : "+v"(x));
-  return x;
-}
-
-// Masks of the magic-number code conversion, held in VGPRs once per wavefront.
-struct NibbleMasks {
-  uint32_t lo, hi, magic;
-};
-KVT_DEV NibbleMasks nibble_masks() {
-  return NibbleMasks{opaque_vgpr(0x000F000Fu), opaque_vgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
-}
-
-// 8 INT4 codes (one dword, channels c0..c7 = nibbles 0..7) -> raw magic values in the order
-// [c0, c4, c1, c5, c2, c6, c3, c7]: 1024 + n for even channels, 1024 + 16 n for odd ones.
-KVT_DEV h8 int4_codes_raw(uint32_t w, uint32_t mlo, uint32_t mhi, uint32_t magic) {
-  const uint32_t w8 = w >> 8;
-  const u4v r = {and_or(w, mlo, magic), and_or(w, mhi, magic), and_or(w8, mlo, magic), and_or(w8, mhi, magic)};
-  return as_h8(r);
-}
-
-// 8 INT8 codes (two dwords, natural channel order) -> fp16 exact.
-KVT_DEV h8 int8_codes_to_h8(uint32_t w0, uint32_t w1) {
-  const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;   // b + 128 as unsigned bytes
-  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-  const h2 a = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) + off;
-  const h2 b = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) + off;
-  const h2 c = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) + off;
-  const h2 d = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) + off;
-  return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
-}
 
 // One 32-token tile of one KV head in LDS (cold path).
 struct ColdStage {
@@ -162,15 +110,6 @@ struct MergeArea {
   float o[kWaves * merge_pitch<true>()];
 };
 
-// A fixup block's per-wavefront merge of 64 output float4s (in-kernel merge of the splits).
-struct FixArea {
-  float m[kWaves][64];
-  float l[kWaves][64];
-  float o[kWaves][64][4];
-  int ok;
-  int n_b;
-};
-
 // Block-wide data: the group's q heads (copied once; rows beyond the group read as zero) and the work handed out
 // inside the block (the next paged tile of the current round, the next ring tile, the round's page ids).
 struct BlockQueue {
@@ -184,57 +123,9 @@ struct Lds {
   union {
     WaveArea w[kWaves];
     MergeArea merge;
-    FixArea fix;
   };
   BlockQueue q;
 };
-
-// Raw buffer resource over [p, p + bytes): loads beyond the range return zero instead of faulting.
-KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
-  const uint64_t a = (uint64_t)p;
-  i32x4 r;
-  r.x = (int)(uint32_t)a;
-  r.y = (int)(uint32_t)(a >> 32);
-  r.z = (int)bytes;
-  r.w = 0x00020000;
-  return r;
-}
-
-// 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
-// statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.
-// Inline assembly rather than the builtin so that the compiler does not treat every later LDS read as dependent on
-// the copy: completion is tracked explicitly with wait_vmcnt by the caller.  The loads are non-temporal (nt): a
-// layer streams 155 MB through the caches once, and marked as streaming it leaves the small per-step metadata every
-// layer starts from (sequence lengths, ring placement, page ids) cached (step 0.516 -> 0.505 ms, measured A/B).
-KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
-               : "memory");
-}
-
-// 4 bytes per lane from rsrc + voffset into lds + 4 * lane (same conventions).
-KVT_DEV void copy4_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "{m0}"(base)
-               : "memory");
-}
-
-// s_waitcnt vmcnt(<= n) leaving the other counters alone (gfx9 encoding).
-template <int N>
-KVT_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  asm volatile("" ::: "memory");
-}
-
-// Compiler-level ordering point for LDS traffic inside one wavefront (the hardware executes a wavefront's LDS
-// instructions in order, so no memory fence is needed).
-KVT_DEV void wave_sync() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_wave_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Channels 32 g + 8 kb .. + 7 (g = 0..7) of one q head row as fp32, natural order.  Every load is unconditional (a
 // lane whose head is beyond the group reads head 0 of the group and zeroes the values afterwards), so the loads go out
@@ -372,11 +263,6 @@ KVT_DEV void cold_scatter_vs(ColdStage& st) {
   }
 }
 
-// 32-bit LDS address of a pointer into the shared block, and back.
-typedef __attribute__((address_space(3))) uint32_t lds_u32;
-typedef __attribute__((address_space(3))) v2i lds_v2i;
-KVT_DEV uint32_t lds_off(const void* p) { return (uint32_t)(uintptr_t)p; }
-
 // QK^T of one staged tile.  Block nt (0, 1) of 16 A rows: row i is token 8 (i >> 2) + 4 nt + (i & 3), so that the
 // D layout leaves lane (n16, kb) with the scores of q head n16 % 8 for tokens 8 kb + 4 nt + r in s[4 nt + r]: the
 // lane's 8 scores are tokens 8 kb .. 8 kb + 7 in natural order, the A operand of P.V.  Scores in log2 units.
@@ -491,27 +377,6 @@ KVT_DEV void cold_pv(const ColdStage& st, u4v p16, NibbleMasks nm, f4 acc[16]) {
   }
 }
 
-// s_waitcnt lgkmcnt(0): every LDS read of this wavefront has returned.
-KVT_DEV void wait_lgkm0() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xC07F);
-  asm volatile("" ::: "memory");
-}
-
-// The next tile of this wavefront: from the block's shared counter (dyn: the wavefronts that run ahead take more
-// tiles, so the block's wavefronts finish together; the floating-point summation order then depends on timing) or in
-// the fixed order w, w + kWaves, w + 2 kWaves, ... (bit-reproducible).
-KVT_DEV int take_tile(int32_t* next, bool dyn, int& taken) {
-  int t = 0;
-  if (dyn) {
-    if ((threadIdx.x & 63) == 0) t = atomicAdd(next, 1);
-  } else {
-    t = (int)(threadIdx.x >> 6) + kWaves * taken;
-  }
-  ++taken;
-  return __builtin_amdgcn_readfirstlane(t);
-}
-
 // One round of a block's paged range: positions [c0, c1) (c0 32-aligned) in 32-position tiles, handed out one at
 // a time from the block's counter; the round's page ids sit in LDS.
 struct ColdRound {
@@ -521,7 +386,7 @@ struct ColdRound {
   const int32_t* pages;
   bool dyn;           // tiles from the shared counter (first come), else wavefront w takes w, w + kWaves, ...
   mutable int taken;  // tiles this wavefront has taken (static order)
-  KVT_DEV int grab() const { return take_tile(next, dyn, taken); }
+  KVT_DEV int grab() const { return take_tile<kWaves>(next, dyn, taken); }
   KVT_DEV uint32_t row0(int t) const {
     const int64_t p = c0 + 32 * (int64_t)t;
     const uint32_t page = (uint32_t)__builtin_amdgcn_readfirstlane(pages[(p >> 6) - pg0]);
@@ -701,10 +566,6 @@ KVT_DEV void cold_block(const PosArgs& A, const ColdCtx& C, Lds& L, int wave, in
 
 // ---- ring (hot) tiles: 16 positions, INT8 codes, scale groups of G8 channels
 
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-
-KVT_DEV f4 mfma16(h4 a, h4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0); }
-
 struct HotCtx {
   i32x4 rk, rv, rks, rvs;   // buffer resources over this sequence's ring rows (codes K/V, scales K/V)
   uint32_t rowbytes;        // H * 256
@@ -851,7 +712,7 @@ KVT_DEV void hot_block(const HotCtx& C, WaveArea& W, int32_t* next, bool dyn, in
                        const uint16_t* qrow, bool qvalid, float cscale, f4 acc[16], float& m_run, float& l_run) {
   const int ntiles = (int)((p1 - p0 + 15) >> 4);
   int taken = 0;
-  auto grab = [&]() -> int { return take_tile(next, dyn, taken); };
+  auto grab = [&]() -> int { return take_tile<kWaves>(next, dyn, taken); };
   auto tile_n = [&](int t) -> int { return (int)min((int64_t)16, p1 - p0 - 16 * (int64_t)t); };
   int ta = grab();
   if (ta >= ntiles) return;
@@ -881,125 +742,9 @@ KVT_DEV void hot_block(const HotCtx& C, WaveArea& W, int32_t* next, bool dyn, in
   }
 }
 
-// ---- split merge inside the kernel (counters != nullptr): fixup blocks.  The grid holds, after every work block in
-// dispatch order, kFixPerItem fixup blocks per (sequence, KV head).  A work block writes its partial (the slot of its
-// split, as for the combine kernel) and counts itself on its (sequence, KV head) counter.  Fixup blocks start on the
-// CUs that work blocks leave (a work block takes a whole CU's LDS, so they start as the first work blocks finish and
-// never hold a CU a work block still needs: all work blocks were dispatched first), wait until their item's count
-// reaches its split count (a bounded poll), and each merges one slice of the output -- 1 / kFixPerItem of the item's
-// q heads x 256 dims -- over all partials in a fixed order, so the result does not depend on the arrival order.  The
-// last fixup block of an item resets its counters for the next call.
-constexpr int kFixPerItem = 8;       // fixup blocks per (sequence, KV head)
-constexpr int kSc1 = 16;             // cache-policy operand of the raw buffer builtins: sc1 (device-coherent)
-constexpr int kSpinLimit = 1 << 20;  // polls of a waiting fixup block (each ~1 us)
-constexpr int kCounterStride = 4;    // counter words per (sequence, KV head): partials written, fixups done, -, -
-constexpr int kFixLoads = 16;        // partials a lane has in flight at once
-
-KVT_DEV __amdgpu_buffer_rsrc_t rsrc_dev(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
-// Partials cross XCDs (each has its own L2): they are written and read with device-coherent accesses (sc1: written
-// through to, and read from, the coherence point past the L2), so neither side needs a whole-L2 writeback or
-// invalidate; a wait for the stores' completion (vmcnt 0) orders them before the count.
+// Partials cross XCDs (each has its own L2): they are written with device-coherent stores (sc1: written through to
+// the coherence point past the L2), which the combine kernel reads after the kernel boundary.
 KVT_DEV void st_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-KVT_DEV void st_dev_i32(int32_t* p, int v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-KVT_DEV int ld_dev_i32(const int32_t* p) {
-  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-KVT_DEV int add_dev_i32(int32_t* p, int v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Fixup block `part` of item (b, h): waits for the item's n_b partials (slots sbase ..), then merges output float4s
-// [f0, f1) of its gs x 64 (float4 j = q head j / 64, dims 4 (j % 64) ..): wavefront w merges partials w, w + 8, ...
-// (kFixLoads in flight per lane), the 8 wavefronts' results merge through LDS in wavefront order.  out = o / l;
-// an empty whole gives 0 / 0 = NaN (as the combine kernel); a poll that runs out leaves NaN as well.
-KVT_DEV void fixup_block(FixArea& F, const float* part_o, const float* part_ml, int32_t* ctr, int64_t sbase, int n_b,
-                         int gs, int part, float* out_f32, uint16_t* out_bf16, int64_t row0) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid == 0) {
-    int ok = 0;
-    for (int it = 0; it < kSpinLimit; ++it) {
-      if (ld_dev_i32(&ctr[0]) >= n_b) {
-        ok = 1;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    F.ok = ok;
-  }
-  __syncthreads();
-  const bool ok = F.ok != 0;
-  const uint32_t rows = (uint32_t)n_b * gs;
-  const auto rml = rsrc_dev(part_ml + sbase * gs * 2, rows * 8u);
-  const auto ro = rsrc_dev(part_o + sbase * gs * kD, rows * (uint32_t)(kD * 4));
-  const uint32_t none = 0x80000000u;   // beyond the range: the load returns zeros
-  const int nf4 = gs * (kD / 4);
-  const int f0 = nf4 * part / kFixPerItem, f1 = nf4 * (part + 1) / kFixPerItem;
-  for (int j0 = f0; j0 < f1; j0 += 64) {
-    const int j = j0 + lane;
-    const bool act = j < f1;
-    const int hq = act ? j / (kD / 4) : 0, d4 = act ? j % (kD / 4) : 0;
-    float M = -INFINITY, Ls = 0.f;
-    f4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int c0 = wave; c0 < n_b; c0 += kWaves * kFixLoads) {
-      v2i ml[kFixLoads];
-      f4 ov[kFixLoads];
-#pragma unroll
-      for (int k = 0; k < kFixLoads; ++k) {
-        const int c = c0 + kWaves * k;
-        const bool in = act && c < n_b;
-        ml[k] = __builtin_amdgcn_raw_buffer_load_b64(rml, in ? (uint32_t)((c * gs + hq) * 8) : none, 0, kSc1);
-        ov[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
-                                           ro, in ? (uint32_t)(((c * gs + hq) * kD + 4 * d4) * 4) : none, 0, kSc1));
-      }
-#pragma unroll
-      for (int k = 0; k < kFixLoads; ++k) {
-        const int c = c0 + kWaves * k;
-        const float mc = (act && c < n_b) ? __int_as_float(ml[k].x) : -INFINITY;
-        if (mc == -INFINITY) continue;
-        const float Mn = fmaxf(M, mc);
-        const float a = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((M - Mn) * kLog2e);
-        const float wc = __builtin_amdgcn_exp2f((mc - Mn) * kLog2e);
-        o = o * a + ov[k] * wc;
-        Ls = Ls * a + __int_as_float(ml[k].y) * wc;
-        M = Mn;
-      }
-    }
-    F.m[wave][lane] = M;
-    F.l[wave][lane] = Ls;
-    *reinterpret_cast<f4*>(&F.o[wave][lane][0]) = o;
-    __syncthreads();
-    if (wave == 0 && act) {
-      float Mt = -INFINITY, Lt = 0.f;
-      f4 ot = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = F.m[w][lane];
-        if (mw == -INFINITY) continue;
-        const float Mn = fmaxf(Mt, mw);
-        const float a = Mt == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((Mt - Mn) * kLog2e);
-        const float wc = __builtin_amdgcn_exp2f((mw - Mn) * kLog2e);
-        ot = ot * a + *reinterpret_cast<const f4*>(&F.o[w][lane][0]) * wc;
-        Lt = Lt * a + F.l[w][lane] * wc;
-        Mt = Mn;
-      }
-      const int64_t row = row0 + (int64_t)hq * kD + 4 * d4;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float r = ok ? ot[i] / Lt : __builtin_nanf("");
-        if (out_f32 != nullptr) out_f32[row + i] = r;
-        if (out_bf16 != nullptr) out_bf16[row + i] = bf16_rne(r);
-      }
-    }
-    __syncthreads();
-  }
-  if (tid == 0 && add_dev_i32(&ctr[1], 1) == kFixPerItem - 1) {   // the item's last fixup: every count was read
-    st_dev_i32(&ctr[0], 0);
-    st_dev_i32(&ctr[1], 0);
-  }
-}
 
 template <int G8, bool WIDE>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -1008,31 +753,13 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
                    int gs, int flags, const uint16_t* q, int64_t q_stride_b, const int64_t* ring_base,
                    const uint8_t* k4, const uint8_t* v4, const uint16_t* ks4, const uint16_t* vs4, const int8_t* rk,
                    const int8_t* rv, const uint16_t* rks, const uint16_t* rvs, float scale, float* part_o,
-                   float* part_ml, uint32_t pool_rows, int32_t* counters, float* out_f32,
-                   uint16_t* out_bf16, int64_t out_stride_b, int work_rows, int batch, int n_map) {
+                   float* part_ml, uint32_t pool_rows, int n_map) {
   // (the arguments the start-up chain needs come first: the first 16 dwords are preloaded into SGPRs)
   const PosArgs A{k4, v4, ks4, vs4, rk, rv, rks, rvs, ring_base, ring_len, ring_start, page_table, pt_stride};
   __shared__ __align__(128) Lds lds;
-  // 1-D grid: work block i = (row i / gx, split i % gx) for i < work_rows * gx, then the fixup blocks
+  // 1-D grid: block i = (row i / gx, split i % gx)
   const int gx = split_map != nullptr ? n_map : n_splits;
   const int bid = (int)blockIdx.x;
-  if (bid >= work_rows * gx) {   // a fixup block (counters != nullptr): after every work block
-    const int f = bid - work_rows * gx;
-    const int item = f / kFixPerItem;
-    const int fb = item / H, fh = item - fb * H;
-    int fn = n_splits;
-    if (split_map != nullptr) {   // the sequence's split count, from any of its split map entries
-      if (threadIdx.x == 0) lds.fix.n_b = 0;
-      __syncthreads();
-      for (int i = threadIdx.x; i < n_map; i += 64 * kWaves)
-        if (split_map[3 * i] == fb) lds.fix.n_b = split_map[3 * i + 2];
-      __syncthreads();
-      fn = lds.fix.n_b;
-    }
-    fixup_block(lds.fix, part_o, part_ml, counters + (int64_t)item * kCounterStride, (int64_t)item * n_splits, fn,
-                gs, f - item * kFixPerItem, out_f32, out_bf16, (int64_t)fb * out_stride_b + (int64_t)fh * gs * kD);
-    return;
-  }
   const bool dyn = (flags & KVT_DECODE_DYNAMIC) != 0;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1132,7 +859,6 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
   wait_vmcnt<0>();                        // (a block without positions still has its Q copy in flight)
   __syncthreads();                        // every wavefront is done with its staging area
   const int tid = threadIdx.x;
-  const bool fused = counters != nullptr;
   if (kb == 0 && n16 < kRows) {
     lds.merge.m[wave][n16] = m_run;
     lds.merge.l[wave][n16] = l_run;
@@ -1194,11 +920,6 @@ decode_mfma_kernel(const int32_t* seq_lens, const int32_t* ring_len, const int64
     st_dev(&part_ml[(item * gs + tid) * 2 + 0], mb);
     st_dev(&part_ml[(item * gs + tid) * 2 + 1], lb);
   }
-  if (!fused) return;
-  // ---- count the partial for the fixup blocks (see fixup_block)
-  wait_vmcnt<0>();                                         // the partial has reached the coherence point
-  __syncthreads();
-  if (tid == 0) add_dev_i32(counters + ((int64_t)b * H + h) * kCounterStride, 1);
 }
 
 }  // namespace
@@ -1210,39 +931,42 @@ int kvt_decode_mfma(const void* q, int64_t q_stride_b, const void* seq_lens, int
                     const void* rv, const void* rks, const void* rvs, const void* ring_base, const void* ring_len,
                     const void* ring_start, const void* page_table, int64_t pt_stride, int64_t pool_rows,
                     float scale, int n_splits, const void* split_map, int n_map, void* part_o, void* part_ml,
-                    int flags, void* counters, void* out_f32, void* out_bf16, int64_t out_stride_b, void* stream) {
+                    int flags, const void* plan, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || D != kD) return KVT_EINVAL;
   if ((((uintptr_t)q) | (uintptr_t)(q_stride_b * 2)) & 15) return KVT_EINVAL;   // Q rows are copied in 16-byte pieces
   if (pool_rows <= 0 || pool_rows * H * (kD / 2) > 0x7fffffffLL) return KVT_ERANGE;   // 32-bit byte offsets
   const int gs = Hq / H;
   if (gs > 16 || n_splits <= 0 || (split_map != nullptr && n_map <= 0)) return KVT_EINVAL;
-  if (counters != nullptr && out_f32 == nullptr && out_bf16 == nullptr) return KVT_EINVAL;
-  // grid: the work blocks (rows 0 .. work_rows - 1), then, with counters, rows of fixup blocks
+  if (group8 != 64 && group8 != 256) return KVT_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  // both KV heads per wavefront (full pool rows) where the shape allows it
+  if (H == 2 && gs <= 8 && (flags & KVT_DECODE_HEADWISE) == 0)
+    return rows_launch(q, q_stride_b, seq_lens, batch, gs, group8, k4, v4, ks4, vs4, rk, rv, rks, rvs, ring_base,
+                       ring_len, ring_start, page_table, pt_stride, pool_rows, scale, n_splits, split_map, n_map,
+                       part_o, part_ml, flags, plan, st);
+  // grid: one block per (split, sequence x KV head) or per (split map entry, KV head)
   const unsigned gx = split_map != nullptr ? (unsigned)n_map : (unsigned)n_splits;
   const int work_rows = split_map != nullptr ? H : batch * H;
-  const int64_t n_blocks = (int64_t)work_rows * gx + (counters == nullptr ? 0 : (int64_t)batch * H * kFixPerItem);
+  const int64_t n_blocks = (int64_t)work_rows * gx;
   if (n_blocks > 0x7fffffff) return KVT_ERANGE;
 #define KVT_DECODE_ARGS                                                                                          \
   (const int32_t*)seq_lens, (const int32_t*)ring_len, (const int64_t*)ring_start, (const int32_t*)page_table,       \
       pt_stride, (const int32_t*)split_map, H, n_splits, gs, flags, (const uint16_t*)q, q_stride_b,                \
       (const int64_t*)ring_base, (const uint8_t*)k4, (const uint8_t*)v4, (const uint16_t*)ks4, (const uint16_t*)vs4, \
       (const int8_t*)rk, (const int8_t*)rv, (const uint16_t*)rks, (const uint16_t*)rvs, scale, (float*)part_o,     \
-      (float*)part_ml, (uint32_t)pool_rows, (int32_t*)counters, (float*)out_f32, (uint16_t*)out_bf16,             \
-      out_stride_b, work_rows, batch, n_map
+      (float*)part_ml, (uint32_t)pool_rows, n_map
   const dim3 grid((unsigned)n_blocks);
-  hipStream_t st = (hipStream_t)stream;
   const bool wide = gs > 8;
   if (group8 == 64 && !wide) {
     hipLaunchKernelGGL((decode_mfma_kernel<64, false>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else if (group8 == 64) {
     hipLaunchKernelGGL((decode_mfma_kernel<64, true>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
-  } else if (group8 == 256 && !wide) {
+  } else if (!wide) {
     hipLaunchKernelGGL((decode_mfma_kernel<256, false>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
-  } else if (group8 == 256) {
-    hipLaunchKernelGGL((decode_mfma_kernel<256, true>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   } else {
-    return KVT_EINVAL;
+    hipLaunchKernelGGL((decode_mfma_kernel<256, true>), grid, dim3(64 * kWaves), 0, st, KVT_DECODE_ARGS);
   }
+#undef KVT_DECODE_ARGS
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }
@@ -1283,7 +1007,7 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
   if (st != KVT_OK) return st;
   const int s1 = kvt_decode_mfma(q, q_stride_b, seq_lens, batch, H, Hq, D, group8, k4, v4, ks4, vs4, rk, rv, rks, rvs,
                                  ring_base, ring_len, ring_start, page_table, pt_stride, pool_rows, scale, n_splits,
-                                 split_map, n_map, base, base + o_floats, flags, nullptr, nullptr, nullptr, 0, stream);
+                                 split_map, n_map, base, base + o_floats, flags, nullptr, stream);
   if (s1 != KVT_OK) return s1;
   return kvt_decode_combine(base, base + o_floats, batch, H, Hq, D, n_splits, 0, seq_lens, split_counts, out_f32,
                             out_bf16, out_stride_b, stream);

@@ -172,14 +172,14 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 }
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
-// grid (D / 64, Hq, batch), 256 threads = 4 wavefronts: lane l of wavefront w holds dims 4 (l & 15) .. + 3 of the
-// block's 64 and merges splits c = 16 k + 4 (l >> 4) + w, k < 8, of each round of 128 (8 16-byte loads of o and 8
-// of (m, l) per lane, all in flight at once), with a running max: (m, num, den) <- (max(m, m_c),
-// num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')).  The 16 merges of a dim quad then combine
-// across lanes (xor 16, 32) and wavefronts (LDS).  An empty context gives 0/0 = NaN
+// grid (D / 32, Hq, batch), 256 threads = 4 wavefronts: lane l of wavefront w holds dims 4 (l & 7) .. + 3 of the
+// block's 32 and merges splits c = 32 k + 4 (l >> 3) + w, k < 8, of each round of 256 (8 16-byte loads of o and 8
+// of (m, l) per lane, all in flight at once: one round for up to 256 splits), with a running max: (m, num, den) <-
+// (max(m, m_c), num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')).  The 32 merges of a dim quad
+// then combine across lanes (xor 8, 16, 32) and wavefronts (LDS).  An empty context gives 0/0 = NaN
 // (gemv/test_kv_paged_prefix.py:524-526).
-constexpr int kCombDims = 64;
-constexpr int kCombRound = 128;   // splits per round
+constexpr int kCombDims = 32;     // dims per block
+constexpr int kCombRound = 256;   // splits per round
 
 typedef float f4c __attribute__((ext_vector_type(4)));
 
@@ -198,13 +198,14 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
     const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
     int64_t out_stride_b) {
-  __shared__ float red[4][16][6];
+  __shared__ float red[4][8][6];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int dq = lane & 15, sub = lane >> 4;
+  const int dq = lane & 7, sub = lane >> 3;
   const int d0 = blockIdx.x * kCombDims + 4 * dq;
+  const int sl = 4 * sub + w;   // the lane's split in each group of 32
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
   float m = -INFINITY, den = 0.0f;
   f4c num = {0.f, 0.f, 0.f, 0.f};
@@ -216,7 +217,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
     float mv[8], lv[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int c = r0 + 16 * k + 4 * sub + w;
+      const int c = r0 + 32 * k + sl;
       const int64_t it = (base + (c < n_chunks ? c : 0)) * gs + j;
       ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
       mv[k] = part_ml[it * 2];
@@ -231,13 +232,13 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {   // (slots beyond `used` may hold anything, NaN included: select, not scale)
-      const int c = r0 + 16 * k + 4 * sub + w;
+      const int c = r0 + 32 * k + sl;
       if (c < used) merge_into(m, num, den, mv[k], ov[k], lv[k]);
     }
     if (r0 + kCombRound >= used) break;
   }
 #pragma unroll
-  for (int x = 16; x < 64; x <<= 1) {
+  for (int x = 8; x < 64; x <<= 1) {
     f4c no;
 #pragma unroll
     for (int i = 0; i < 4; ++i) no[i] = __shfl_xor(num[i], x, 64);

@@ -104,6 +104,7 @@ KVT_DEV uint32_t pack_pair(float qe, float qo) {
 #define KVT_ENOMEM -5       // the HIP runtime could not provide address space or physical memory
 #define KVT_EHIP -6         // another HIP runtime call failed
 #define KVT_DECODE_DYNAMIC 1   // kvt_decode_mfma flag: tiles to wavefronts first come
+#define KVT_DECODE_HEADWISE 2  // kvt_decode_mfma flag: one KV head per block even where both fit one wavefront
 
 #define KVT_CHECK_LAUNCH()                                   \
   do {                                                       \

@@ -108,6 +108,11 @@ class PosTieredCache:
         self.plan_status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._dev_head = 0
         self._ring_used = 0
+        # bumped by every change of the sequence state (lengths, rings, page table); a decode plan records it
+        self.version = 0
+        # set once launch_plan has been captured into a graph: from then on replays may advance the device state past
+        # the host mirror at any time, so host-side planning first reads the device state back (sync_host)
+        self._device_may_advance = False
         # host mirror
         self.h_len: List[int] = []
         self.h_ring: List[tuple] = []       # (base, len, start)
@@ -124,6 +129,8 @@ class PosTieredCache:
         shared_pages (physical INT4 pages already holding a common prefix; paged-prefix reuse)."""
         assert ring_len > 0 and ring_len & (ring_len - 1) == 0, "ring_len must be a power of two"
         assert len(shared_pages) * PAGE >= ring_start and ring_start % PAGE == 0
+        self._catch_up()
+        self.version += 1
         s = self.n_seqs
         assert s < self.max_seqs
         if self._ring_used + ring_len > self.ring_total:
@@ -152,6 +159,8 @@ class PosTieredCache:
         time are popped from the allocator and written into the device page table (one small launch)."""
         if len(set(seqs)) != len(list(seqs)):
             raise ValueError("a plan lists each sequence once")
+        self._catch_up()
+        self.version += 1
         sid, pos, upd_s, upd_l, upd_p = [], [], [], [], []
         for s, n in zip(seqs, counts):
             base, R, start = self.h_ring[s]
@@ -209,6 +218,13 @@ class PosTieredCache:
         lp0 = (e0 + PAGE - 1) // PAGE
         return range(lp0, (e1 + PAGE - 1) // PAGE) if e1 > e0 else range(lp0, lp0)
 
+    def _catch_up(self) -> None:
+        """Before planning on the host: if graph replays of a captured device plan may have advanced the lengths, page
+        table and free-list head, read them back first (the host mirror and allocator would otherwise hand out pages
+        the device already gave away)."""
+        if self._device_may_advance and not torch.cuda.is_current_stream_capturing():
+            self.sync_host()
+
     def _push_free_head(self) -> None:
         """Make the device free-list head equal the host allocator's position (pages popped on the host)."""
         if self._dev_head != self.alloc.next:
@@ -221,7 +237,11 @@ class PosTieredCache:
         host planner) and then advances the host mirror (lengths, pages) in closed form; under graph capture the
         mirror is left as it is -- sync_host() reads the device state back after replays."""
         capturing = torch.cuda.is_current_stream_capturing()
-        if not capturing:
+        self.version += 1
+        if capturing:
+            self._device_may_advance = True
+        else:
+            self._catch_up()
             need = sum(len(self._new_pages(s, n)) for s, n in zip(plan.seqs, plan.counts))
             if need > self.alloc.n_free:
                 raise RuntimeError("INT4 page pool exhausted")
@@ -257,6 +277,7 @@ class PosTieredCache:
             self.h_pages[s] = [int(p) for p in pt[s][:self._page_count(s)]]
         self.alloc.next = int(self.free_head.item())
         self._dev_head = self.alloc.next
+        self.version += 1
 
     def _page_count(self, s: int) -> int:
         """Entries of sequence s's page-table row: its shared prefix pages, or every page an evicted position has
@@ -285,6 +306,7 @@ class PosTieredCache:
             return
         for s, n in zip(plan.seqs, plan.counts):
             self.h_len[s] += n
+        self.version += 1
         idx = torch.tensor(plan.seqs, dtype=torch.int64)
         add = torch.tensor(plan.counts, dtype=torch.int32)
         self.seq_lens.index_add_(0, idx.to(self.device), add.to(self.device))
@@ -319,19 +341,91 @@ def _choose_chunk(max_len: int, items: int, lo: int = 64, hi: int = 512) -> int:
     return int(min(hi, 1 << (c - 1).bit_length()))
 
 
-def _choose_splits_mfma(max_len: int, items: int, blocks: int = 256) -> int:
-    """Splits per (sequence, KV head) of the MFMA kernel: about `blocks` blocks in all (one 8-wavefront block per CU
-    on 256 CUs), each with at least 256 positions."""
+ROWS_MIN_POS = 64   # positions per split of the full-row kernel at least (a block has 8 wavefronts)
+
+
+def _rows_kernel(H: int, Hq: int) -> bool:
+    """The full-row split-K kernel serves two KV heads with up to 8 q heads each (a wavefront computes both heads of a
+    position); other shapes take the head-wise kernel."""
+    return H == 2 and Hq % H == 0 and Hq // H <= 8
+
+
+def _choose_splits_mfma(max_len: int, items: int, blocks: int = 256, min_pos: int = 256) -> int:
+    """Splits per work item of the MFMA kernels (an item is a sequence for the full-row kernel, a (sequence, KV head)
+    for the head-wise one): about `blocks` blocks in all (one 8-wavefront block per CU on 256 CUs), each with at least
+    min_pos positions."""
     n = -(-blocks // max(1, items))
-    return int(max(1, min(n, -(-max_len // 256))))
+    return int(max(1, min(n, -(-max_len // min_pos))))
 
 
-def _split_counts_mfma(lens: Sequence[int], H: int, blocks: int = 256) -> List[int]:
-    """Per-sequence split counts of the MFMA kernel for a ragged batch: about `blocks` blocks in all, shared in
-    proportion to the context lengths (each sequence at least 1, each wavefront at least 64 positions)."""
-    per_head = max(1, blocks // max(1, H))
+def _split_counts_mfma(lens: Sequence[int], items_per_seq: int, blocks: int = 256, min_pos: int = 256) -> List[int]:
+    """Per-sequence split counts of the MFMA kernels for a ragged batch: about `blocks` blocks in all, shared in
+    proportion to the context lengths (each sequence at least 1, each split at least min_pos positions)."""
+    per_item = max(1, blocks // max(1, items_per_seq))
     tot = max(1, sum(lens))
-    return [int(max(1, min(-(-L // 256), round(per_head * L / tot)))) for L in lens]
+    return [int(max(1, min(-(-L // min_pos), round(per_item * L / tot)))) for L in lens]
+
+
+def _decode_grid(cache: "PosTieredCache", Hq: int, splits: Optional[int], ws: dict, device):
+    """(n_chunks, split_map, split_counts, n_map, rows) of an MFMA decode: uniform splits, or for more than one
+    sequence a split map with counts in proportion to the lengths; rows = the full-row kernel serves the shape."""
+    S, H = cache.n_seqs, cache.H
+    rows = _rows_kernel(H, Hq)
+    items, min_pos = (1, ROWS_MIN_POS) if rows else (H, 256)
+    if splits is None and S > 1:
+        counts = _split_counts_mfma(cache.h_len[:S], items, min_pos=min_pos)
+        split_map, split_counts, counts = _split_map(counts, ws, device)
+        return max(counts), split_map, split_counts, sum(counts), rows
+    max_len = max(cache.h_len) if S else 0
+    n = splits if splits is not None else _choose_splits_mfma(max_len, S * items, min_pos=min_pos)
+    return int(n), None, None, 0, rows
+
+
+def decode_split_counts(cache: "PosTieredCache", Hq: int) -> List[int]:
+    """The per-sequence split counts kvt_decode_attn(impl="mfma") gives a ragged batch of the cache's current lengths
+    (for callers that prepare a split map themselves, e.g. for the no-allocation entry point)."""
+    rows = _rows_kernel(cache.H, Hq)
+    items, min_pos = (1, ROWS_MIN_POS) if rows else (cache.H, 256)
+    return _split_counts_mfma(cache.h_len[:cache.n_seqs], items, min_pos=min_pos)
+
+
+@dataclass
+class DecodePlan:
+    """One decode step's plan for the full-row kernel (kvt_decode_plan): every block's position ranges and the pool
+    rows of its first tiles, built on the device from the cache's current lengths, ring placement and page table, and
+    shared by the step's layers.  Valid until the cache's sequence state changes (an append, a new sequence, a page
+    table change): kvt_decode_attn refuses a plan older than the cache (ValueError), and a block whose plan entry does
+    not match the sequence's current length or ring placement computes its ranges itself."""
+    entries: torch.Tensor                  # int32 [blocks, 64]
+    n_chunks: int                          # partial slots per (sequence, KV head)
+    split_map: Optional[torch.Tensor]
+    split_counts: Optional[torch.Tensor]
+    n_map: int
+    Hq: int
+    version: int
+
+
+def kvt_decode_plan(cache: "PosTieredCache", Hq: int, splits: Optional[int] = None,
+                    workspace: Optional[dict] = None) -> DecodePlan:
+    """Build the decode plan of the cache's current state for queries of Hq heads (one small launch; capturable: in a
+    HIP graph the plan is rebuilt from the device state at every replay).  Plans exist for the full-row kernel's
+    shapes (two KV heads, up to 8 q heads each)."""
+    S = cache.n_seqs
+    if not _rows_kernel(cache.H, Hq):
+        raise ValueError(f"decode plans serve the full-row kernel (2 KV heads, <= 8 q heads each), not {Hq} / {cache.H}")
+    if S == 0:
+        raise ValueError("decode plan of an empty cache")
+    ws = workspace if workspace is not None else {}
+    n_chunks, split_map, split_counts, n_map, _ = _decode_grid(cache, Hq, splits, ws, cache.device)
+    blocks = n_map if split_map is not None else S * n_chunks
+    ent = ws.get("decode_plan")
+    if ent is None or ent.numel() < blocks * 64 or ent.device != cache.device:
+        ent = torch.empty(blocks * 64, dtype=torch.int32, device=cache.device)
+        ws["decode_plan"] = ent
+    _lib.call("kvt_decode_plan", cache.seq_lens.data_ptr(), cache.ring_len.data_ptr(), cache.ring_start.data_ptr(),
+              cache.ring_base.data_ptr(), cache.page_table.data_ptr(), cache.page_table.stride(0), S, n_chunks,
+              _lib.ptr(split_map), n_map, ent.data_ptr(), _lib.stream())
+    return DecodePlan(ent, n_chunks, split_map, split_counts, n_map, Hq, cache.version)
 
 
 def _split_map(counts: List[int], ws: dict, device) -> Tuple[torch.Tensor, torch.Tensor, List[int]]:
@@ -355,25 +449,27 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                     impl: str = "ref", chunk: Optional[int] = None, max_len: Optional[int] = None,
                     out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
                     events: Optional[list] = None, splits: Optional[int] = None,
-                    deterministic: bool = False, fused_combine: bool = False,
-                    tile_order: Optional[str] = None) -> torch.Tensor:
+                    deterministic: bool = False, tile_order: Optional[str] = None,
+                    plan: Optional[DecodePlan] = None, headwise: bool = False, check_q: bool = True) -> torch.Tensor:
     """Decode attention of one query token per sequence over the tiered cache of `layer`.
 
     q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
     every position of each sequence, K/V dequantized from the INT4 pages (positions < hot_start) and the INT8 ring.
-    impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per (sequence, KV head), or, by
-    default for more than one sequence, split counts in proportion to each sequence's length.
+    impl "ref": splits of `chunk` positions; impl "mfma": `splits` equal-cost splits per sequence (full-row kernel:
+    two KV heads with up to 8 q heads each, both heads per block) or per (sequence, KV head) (head-wise kernel: the
+    other shapes, or headwise=True), or, by default for more than one sequence, split counts in proportion to each
+    sequence's length.
+    plan (impl "mfma", full-row kernel): the step's DecodePlan (kvt_decode_plan) -- its grid replaces `splits`, and
+    every block starts from its plan entry instead of computing its ranges; a plan older than the cache's state raises
+    ValueError.
     events: if a list, timing events (start, after the split-K kernel, after the combine) are appended.
     deterministic (impl "mfma"): bit-identical results from call to call: tiles go to the wavefronts of a block in
     a fixed order and the combine kernel merges the splits.  By default tiles go first come (the block's wavefronts
-    finish together, about 4 % faster at 262,144 positions) and the fp32 summation order varies in the last bits.
+    finish together) and the fp32 summation order varies in the last bits.
     tile_order ("fixed" / "dynamic", impl "mfma"): overrides the tile order alone.
-    fused_combine (impl "mfma"): the split-K launch merges its own partials and writes `out`: fixup blocks queued
-    after the work blocks wait for every partial of their (sequence, KV head) and each merges 1/8 of its output in a
-    fixed order.  One launch instead of two, but the cross-XCD handshake (coherent stores, counter, poll, coherent
-    loads) costs more than the kernel boundary and the combine launch: at 262,144 positions 47.5 against 39.0 + 4.3
-    us per layer, hence off by default.  The merge counters live in the workspace and return to zero after every
-    call; concurrent calls must not share a workspace.
+    check_q (impl "mfma"): the matrix-core kernels take Q in fp16; outside a graph capture a Q with an entry beyond the
+    fp16 range (|q| > 65504) or not finite raises ValueError (one device reduction and synchronization).  Under
+    capture the check is skipped and such a Q gives non-finite outputs.
     """
     S = cache.n_seqs
     assert q.dim() == 3 and q.shape[0] == S and q.shape[2] == cache.D and q.dtype == torch.bfloat16
@@ -387,19 +483,35 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     ws = workspace if workspace is not None else {}
     split_map = split_counts = None
     n_map = 0
+    flags = 0
     if impl == "mfma":
         chunk = 0   # every split holds a partial
-        if splits is None and S > 1:
-            counts = _split_counts_mfma(cache.h_len[:S], H)
-            split_map, split_counts, counts = _split_map(counts, ws, q.device)
-            n_chunks, n_map = max(counts), sum(counts)
+        if plan is not None:
+            if headwise or not _rows_kernel(H, Hq) or plan.Hq != Hq:
+                raise ValueError("a decode plan serves the full-row kernel at the q head count it was made for")
+            if plan.version != cache.version:
+                raise ValueError("stale decode plan: the cache's sequence state changed after kvt_decode_plan")
+            n_chunks, split_map, split_counts, n_map = plan.n_chunks, plan.split_map, plan.split_counts, plan.n_map
+        elif headwise and _rows_kernel(H, Hq):
+            # the head-wise kernel's grid (the A/B reference of the full-row kernel)
+            if splits is None and S > 1:
+                counts = _split_counts_mfma(cache.h_len[:S], H)
+                split_map, split_counts, counts = _split_map(counts, ws, q.device)
+                n_chunks, n_map = max(counts), sum(counts)
+            else:
+                n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)
         else:
-            n_chunks = splits if splits is not None else _choose_splits_mfma(max_len, S * H)
+            n_chunks, split_map, split_counts, n_map, _ = _decode_grid(cache, Hq, splits, ws, q.device)
+        fixed_order = (tile_order or ("fixed" if deterministic else "dynamic")) == "fixed"
+        flags = (0 if fixed_order else 1) | (2 if headwise else 0)
+        if check_q and not torch.cuda.is_current_stream_capturing():
+            if not bool(torch.isfinite(q).all()) or float(q.abs().max()) > 65504.0:
+                raise ValueError("kvt_decode_attn (impl 'mfma'): q has entries beyond the fp16 range the matrix-core "
+                                 "kernels take (|q| > 65504 or not finite)")
     else:
         if chunk is None:
             chunk = _choose_chunk(max_len, S * H)
         n_chunks = max(1, -(-max_len // chunk))
-    fused = impl == "mfma" and fused_combine
     n_slots = n_chunks   # partial slots per (sequence, KV head)
     need_o = S * H * n_slots * gs * D
     po = ws.get("part_o")
@@ -428,28 +540,14 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     elif impl == "mfma":
         if cache.rk[layer].numel() >= 2 ** 31:
             raise ValueError("kvt_decode_mfma: ring buffers beyond 2^31 bytes per layer are not supported")
-        fixed_order = (tile_order or ("fixed" if deterministic else "dynamic")) == "fixed"
-        ctr = None
-        if fused:
-            # 4 words per (sequence, KV head): partials written, fixup blocks done (zero between calls)
-            ctr = ws.get("merge_counters")
-            if ctr is None or ctr.numel() < S * H * 4 or ctr.device != q.device:
-                ctr = torch.zeros(max(S * H * 4, 64), dtype=torch.int32, device=q.device)
-                ws["merge_counters"] = ctr
         _lib.call("kvt_decode_mfma", q.data_ptr(), q.stride(0), cache.seq_lens.data_ptr(), S, H, Hq, D, cache.group8,
                   cache.k4[layer].data_ptr(), cache.v4[layer].data_ptr(), cache.ks4[layer].data_ptr(),
                   cache.vs4[layer].data_ptr(), cache.rk[layer].data_ptr(), cache.rv[layer].data_ptr(),
                   cache.rks[layer].data_ptr(), cache.rvs[layer].data_ptr(), cache.ring_base.data_ptr(),
                   cache.ring_len.data_ptr(), cache.ring_start.data_ptr(), cache.page_table.data_ptr(),
                   cache.page_table.stride(0), cache.k4[layer].shape[0], scale, n_chunks, _lib.ptr(split_map), n_map,
-                  po.data_ptr(), pml.data_ptr(), 0 if fixed_order else 1, _lib.ptr(ctr),
-                  out.data_ptr() if fused and out.dtype == torch.float32 else None,
-                  out.data_ptr() if fused and out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
-        if fused:
-            if events is not None:
-                ev1.record()
-                events.append((ev0, ev1, ev1))
-            return out
+                  po.data_ptr(), pml.data_ptr(), flags, None if plan is None else plan.entries.data_ptr(),
+                  _lib.stream())
     else:
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
@@ -484,7 +582,12 @@ def kvt_decode_attn_noalloc(cache: PosTieredCache, layer: int, q: torch.Tensor, 
         assert split_counts.dtype == torch.int32 and split_counts.numel() >= S
     else:
         n_map = 0
-        n_chunks = splits if splits is not None else _choose_splits_mfma(max(cache.h_len) if S else 0, S * H)
+        if splits is not None:
+            n_chunks = splits
+        elif _rows_kernel(H, Hq):
+            n_chunks = _choose_splits_mfma(max(cache.h_len) if S else 0, S, min_pos=ROWS_MIN_POS)
+        else:
+            n_chunks = _choose_splits_mfma(max(cache.h_len) if S else 0, S * H)
     _lib.require_device(q, out)
     rows = S * H * n_chunks * (Hq // H)
     need = ((rows * D + 63) // 64 * 64 + rows * 2) * 4

@@ -78,22 +78,20 @@ def test_decode_pos_rings(kvt_pkg, impl, tol, mtol):
 
 @pytest.mark.parametrize("hq", [20, 24, 32])
 def test_decode_mfma_wide_groups(kvt_pkg, hq):
-    """Groups of more than 8 q heads per KV head (10, 12 -- the served model's 24 / 2 -- and 16): one head per MFMA
-    column, Q rows read by every wavefront.  Three sequences through the split map and at fixed split counts, the
-    combine kernel and the in-kernel merge, against the oracle; the scalar reference kernel too."""
+    """Groups of more than 8 q heads per KV head (10, 12 -- the served model's 24 / 2 -- and 16): the head-wise kernel,
+    one head per MFMA column, Q rows read by every wavefront.  Three sequences through the split map and at fixed
+    split counts against the oracle; the scalar reference kernel too."""
     from kvtier.kvt import kvt_decode_attn
     dc, oc, q = _build([5000, 2100, 700], [2048, 1024, 256], seed=51, hq=hq)
     qd = q.to(dev)
     exp = _oracle_out(oc, q)
     outs = {"map": kvt_decode_attn(dc, 0, qd, impl="mfma"),
             "splits17": kvt_decode_attn(dc, 0, qd, impl="mfma", splits=17, deterministic=True),
-            "fused17": kvt_decode_attn(dc, 0, qd, impl="mfma", splits=17, tile_order="fixed", fused_combine=True),
             "ref": kvt_decode_attn(dc, 0, qd, impl="ref")}
     for name, out in outs.items():
         assert out.shape == (3, hq, D), name
         err = (out.cpu() - exp).abs()
         assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (hq, name, float(err.max()), float(err.mean()))
-    assert float((outs["fused17"] - outs["splits17"]).abs().max()) < 1e-5
 
 
 @pytest.mark.parametrize("splits", [1, 3, 17, 64])
@@ -107,52 +105,88 @@ def test_decode_mfma_splits(kvt_pkg, splits):
     assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (splits, float(err.max()), float(err.mean()))
 
 
-@pytest.mark.parametrize("splits", [1, 2, 16, 17, 40, 200])
-def test_decode_fused_merge(kvt_pkg, splits):
-    """The in-kernel merge of the split partials (fixup blocks after the work blocks, each merging 1/8 of the
-    output over all partials in a fixed order) against the separate combine kernel (same math, another fp32
-    summation order: 1e-5; both with the fixed tile order) and the oracle, over several calls: after each, the merge
-    counters are back to zero and, with the fixed tile order, the output is bit-identical from call to call; bf16
-    output = the fp32 result rounded (up to that order)."""
+@pytest.mark.parametrize("splits", [None, 1, 3, 17, 300])
+def test_decode_rows_vs_headwise(kvt_pkg, splits):
+    """The full-row kernel (both KV heads of a position per wavefront: 16 / 2 heads) against the head-wise kernel
+    (headwise=True) and the oracle: three sequences through the split map (splits None) or at fixed split counts
+    (one block for a whole sequence up to more blocks than 16-position tiles); both kernels within the oracle
+    tolerance, and within 2e-4 of each other (the same products in another fp32 summation order)."""
     from kvtier.kvt import kvt_decode_attn
-    dc, oc, q = _build([5000, 2100], [2048, 1024], seed=31)
+    dc, oc, q = _build([5000, 2100, 700], [2048, 1024, 256], seed=41)
     qd = q.to(dev)
-    ws = {}
-    sep = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, deterministic=True)
-    first = None
-    for rep in range(3):
-        fused = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, workspace=ws, tile_order="fixed",
-                                fused_combine=True)
-        assert int(ws["merge_counters"].abs().sum()) == 0, rep
-        assert float((fused - sep).abs().max()) < 1e-5, (splits, rep)
-        if first is None:
-            first = fused.clone()
-        assert torch.equal(fused, first), (splits, rep)
-    fb = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, workspace=ws, out_dtype=torch.bfloat16,
-                         tile_order="fixed", fused_combine=True)
-    assert bool(((fb.float() - fused).abs() <= fused.abs() * 2.0 ** -8 + 1e-6).all())
-    err = (fused.cpu() - _oracle_out(oc, q)).abs()
-    assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (splits, float(err.max()))
+    exp = _oracle_out(oc, q)
+    rows = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits)
+    head = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, headwise=True)
+    for name, out in (("rows", rows), ("head", head)):
+        err = (out.cpu() - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, (splits, name, float(err.max()))
+    assert float((rows - head).abs().max()) <= 2e-4, splits
 
 
-def test_decode_fused_merge_ragged(kvt_pkg):
-    """Ragged batch through the split map: per-sequence split counts from 1 up (the fixup blocks read each
-    sequence's count from the map), in the fused merge against the combine kernel and the oracle; the same workspace
-    then serves a call with another split layout."""
-    from kvtier.kvt import kvt_decode_attn
-    lens = [40000, 300, 9000, 2500]
-    dc, oc, q = _build(lens, [2048, 256, 1024, 1024], seed=37)
+@pytest.mark.parametrize("lens,rings,splits", [([3000], [512], None), ([20000], [256], 7), ([20000], [256], 300),
+                                               ([5000, 2100, 700, 65], [2048, 1024, 256, 64], None), ([17], [16], None)])
+def test_decode_plan(kvt_pkg, lens, rings, splits):
+    """A decode plan (kvt_decode_plan: every block's ranges and first tile rows, built on the device) gives the same
+    result as blocks that compute their ranges themselves -- bit for bit with the fixed tile order -- for one sequence
+    at several split counts and a ragged batch through the split map; and within the oracle tolerance."""
+    from kvtier.kvt import kvt_decode_attn, kvt_decode_plan
+    dc, oc, q = _build(lens, rings, seed=43)
     qd = q.to(dev)
     ws = {}
-    sep = kvt_decode_attn(dc, 0, qd, impl="mfma", deterministic=True)
-    for rep in range(2):
-        fused = kvt_decode_attn(dc, 0, qd, impl="mfma", workspace=ws, tile_order="fixed", fused_combine=True)
-        assert float((fused - sep).abs().max()) < 1e-5, rep
-    err = (fused.cpu() - _oracle_out(oc, q)).abs()
+    plan = kvt_decode_plan(dc, HQ, splits=splits, workspace=ws)
+    with_plan = kvt_decode_attn(dc, 0, qd, impl="mfma", plan=plan, workspace=ws, deterministic=True)
+    without = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=splits, deterministic=True)
+    assert torch.equal(with_plan, without)
+    dyn = kvt_decode_attn(dc, 0, qd, impl="mfma", plan=plan, workspace=ws)
+    assert float((dyn - without).abs().max()) <= 2e-4
+    err = (with_plan.cpu() - _oracle_out(oc, q)).abs()
     assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3, float(err.max())
-    fused2 = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=33, workspace=ws, fused_combine=True)
-    sep2 = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=33, deterministic=True)
-    assert float((fused2 - sep2).abs().max()) < 2e-4
+
+
+def test_decode_plan_stale(kvt_pkg):
+    """A plan older than the cache's sequence state is refused on the host (ValueError); a stale plan that reaches
+    the kernel anyway (its version forged here) is caught there: every block whose entry was made for another length
+    computes its ranges itself, so the result equals a decode without plan bit for bit (fixed tile order)."""
+    from kvtier.kvt import kvt_decode_attn, kvt_decode_plan
+    dc, oc, q = _build([6000], [1024], seed=45)
+    qd = q.to(dev)
+    ws = {}
+    plan = kvt_decode_plan(dc, HQ, workspace=ws)
+    g = torch.Generator().manual_seed(46)
+    xk, xv = ref.make_kv(3, H, D, g, ref.outlier_channels(H, D, 8, g))
+    ap = dc.plan_append([0], [3])
+    dc.append(0, ap, xk.to(dev), xv.to(dev))
+    dc.commit(ap)
+    with pytest.raises(ValueError):
+        kvt_decode_attn(dc, 0, qd, impl="mfma", plan=plan, workspace=ws)
+    plan.version = dc.version
+    got = kvt_decode_attn(dc, 0, qd, impl="mfma", plan=plan, workspace=ws, deterministic=True)
+    want = kvt_decode_attn(dc, 0, qd, impl="mfma", splits=plan.n_chunks, deterministic=True)
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError):   # a plan serves the full-row kernel's shapes only
+        kvt_decode_plan(dc, 24)
+
+
+def test_decode_q_range(kvt_pkg):
+    """The matrix-core kernels take Q in fp16: a bf16 Q with an entry beyond 65504 or not finite raises ValueError
+    outside graph capture; check_q=False skips the check (an even channel beyond the range becomes inf in fp16: the
+    output is then not finite)."""
+    from kvtier.kvt import kvt_decode_attn
+    dc, oc, q = _build([900], [256], seed=47)
+    for bad in (7.0e4, float("inf"), float("nan")):
+        qb = q.clone()
+        qb[0, 3, 16] = bad
+        with pytest.raises(ValueError):
+            kvt_decode_attn(dc, 0, qb.to(dev), impl="mfma")
+        with pytest.raises(ValueError):
+            kvt_decode_attn(dc, 0, qb.to(dev), impl="mfma", headwise=True)
+    qb = q.clone()
+    qb[0, 3, 16] = 7.0e4
+    out = kvt_decode_attn(dc, 0, qb.to(dev), impl="mfma", check_q=False)
+    assert not bool(torch.isfinite(out[0, 3]).all())
+    ok = q.clone()
+    ok[0, 3, 17] = 6.5e4                      # within the fp16 range: accepted
+    kvt_decode_attn(dc, 0, ok.to(dev), impl="mfma")
 
 
 def test_combine_ignores_unused_slots(kvt_pkg):

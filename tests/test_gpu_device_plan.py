@@ -127,6 +127,90 @@ def test_device_plan_graph_replay(kvt_pkg):
     assert torch.equal(out, want)
 
 
+def _prefilled_pair(seed):
+    """Two caches (rings 512 / 256) holding the same 700 / 300-position prefill through the host planner."""
+    host, devc = _pair([512, 256], n_pages=64, seed=seed)
+    g = torch.Generator(device=dev).manual_seed(seed + 100)
+    k = torch.randn(1000, H, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(1000, H, D, device=dev, generator=g).to(torch.bfloat16)
+    for c in (host, devc):
+        for a in range(0, 700, 256):
+            n0, n1 = min(256, 700 - a), min(256, max(0, 300 - a))
+            seqs, cnts = [0] + ([1] if n1 else []), [n0] + ([n1] if n1 else [])
+            p = c.plan_append(seqs, cnts)
+            c.append(0, p, torch.cat([k[a:a + n0]] + ([k[700 + a:700 + a + n1]] if n1 else [])),
+                     torch.cat([v[a:a + n0]] + ([v[700 + a:700 + a + n1]] if n1 else [])))
+            c.commit(p)
+    return host, devc, g
+
+
+def test_decode_plan_in_graph(kvt_pkg):
+    """A decode step with the step's decode plan -- device append plan, append, kvt_decode_plan, decode with the
+    plan -- captured once and replayed 120 times: the plan is rebuilt from the device state at every replay, so the
+    last output equals an eager decode without plan of the host planner's cache after the same appends (8 splits per
+    sequence on both sides, fixed tile order: bit for bit)."""
+    from kvtier.kvt import kvt_decode_attn, kvt_decode_plan
+    host, devc, g = _prefilled_pair(5)
+    steps = 120
+    knew = torch.randn(steps, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    vnew = torch.randn(steps, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    q = (torch.randn(2, HQ, D, device=dev, generator=g) / 16).to(torch.bfloat16)
+    kin, vin = knew[0].clone(), vnew[0].clone()
+    dp = devc.plan_device([0, 1], [1, 1])
+    ws = {}
+    out = torch.empty(2, HQ, D, device=dev)
+    kvt_decode_attn(devc, 0, q, out=out, impl="mfma", workspace=ws,
+                    plan=kvt_decode_plan(devc, HQ, splits=8, workspace=ws), deterministic=True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        devc.launch_plan(dp)
+        devc.append(0, dp, kin, vin)
+        plan = kvt_decode_plan(devc, HQ, splits=8, workspace=ws)
+        kvt_decode_attn(devc, 0, q, out=out, impl="mfma", workspace=ws, plan=plan, deterministic=True)
+    for i in range(steps):
+        kin.copy_(knew[i])
+        vin.copy_(vnew[i])
+        graph.replay()
+        hp = host.plan_append([0, 1], [1, 1])
+        host.append(0, hp, knew[i], vnew[i])
+        host.commit(hp)
+    torch.cuda.synchronize()
+    devc.sync_host()
+    _same(host, devc)
+    want = kvt_decode_attn(host, 0, q, impl="mfma", splits=8, deterministic=True)
+    assert torch.equal(out, want)
+
+
+def test_host_plan_after_replays(kvt_pkg):
+    """Host planning after graph replays of a captured device plan, without an explicit sync_host(): the cache reads
+    the advanced device state back first, so the pages it hands out are the ones the device has not, and the cache
+    equals the host planner's after the same appends (the device free list is never rewound)."""
+    host, devc, g = _prefilled_pair(6)
+    steps = 40
+    knew = torch.randn(steps + 1, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    vnew = torch.randn(steps + 1, 2, H, D, device=dev, generator=g).to(torch.bfloat16)
+    kin, vin = knew[0].clone(), vnew[0].clone()
+    dp = devc.plan_device([0, 1], [1, 1])
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        devc.launch_plan(dp)
+        devc.append(0, dp, kin, vin)
+    for i in range(steps):
+        kin.copy_(knew[i])
+        vin.copy_(vnew[i])
+        graph.replay()
+        hp = host.plan_append([0, 1], [1, 1])
+        host.append(0, hp, knew[i], vnew[i])
+        host.commit(hp)
+    for c in (host, devc):            # then a host-planned chunk on both (devc without sync_host)
+        p = c.plan_append([0, 1], [200, 100])
+        c.append(0, p, torch.cat([knew[steps]] * 150)[:300], torch.cat([vnew[steps]] * 150)[:300])
+        c.commit(p)
+    torch.cuda.synchronize()
+    _same(host, devc)
+
+
 def test_device_plan_refusals(kvt_pkg):
     """Eagerly, a plan needing more pages than the pool holds raises before any launch; a launch through the C ABI
     with an empty free list raises the status flag, assigns no page, writes no page-table entry, and sync_host()

@@ -48,11 +48,11 @@ def test_noalloc_matches_allocating_entry_points(kvt_pkg):
 
 
 def test_noalloc_ragged_split_map(kvt_pkg):
-    from kvtier.kvt import _split_counts_mfma, _split_map, kvt_decode_attn, kvt_decode_attn_noalloc
+    from kvtier.kvt import _split_map, decode_split_counts, kvt_decode_attn, kvt_decode_attn_noalloc
     cache, q = _cache([9_000, 1_500, 20_000], 1024, seed=9)
     ws = {}
     want = kvt_decode_attn(cache, 0, q, impl="mfma", deterministic=True, workspace=ws)
-    counts = _split_counts_mfma(cache.h_len, H)
+    counts = decode_split_counts(cache, HQ)
     smap, scounts, _ = _split_map(counts, {}, q.device)
     got = torch.empty_like(want)
     kvt_decode_attn_noalloc(cache, 0, q, got, splits=max(counts), split_map=smap, split_counts=scounts,
