@@ -382,6 +382,7 @@ def append_workload(args) -> dict:
         for s in range(S):
             for layer in range(LAYERS):
                 cache.append(layer, plans[s], *kv[s][layer])
+    _settle(g.replay)
     for _ in range(max(1, args.warmup)):
         g.replay()
     torch.cuda.synchronize()
@@ -416,8 +417,28 @@ def append_workload(args) -> dict:
     }
 
 
+SETTLE_S = 0.2   # untimed replays before every timed region (seconds of wall time)
+
+
+def _settle(replay, seconds: float = SETTLE_S) -> int:
+    """Replays a graph, untimed, for `seconds` of wall time and returns how many times.  After an idle stretch (cache
+    building, host work) the GPU's clocks take several milliseconds to come up: the first 20 replays of the 12-layer
+    decode graph run about 10 % slower than every later batch of 20 (501 vs 451 us per step, measured on one box), so
+    each timed region starts on a GPU that has been busy for a while.  Only replays whose repetition leaves the state
+    unchanged are settled this way."""
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            replay()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
 def _graph_time(fn, warmup: int, reps: int) -> float:
-    """Seconds per replay of a HIP graph of fn() (captured after one eager run on a side stream)."""
+    """Seconds per replay of a HIP graph of fn() (captured after one eager run on a side stream), timed after the
+    graph has run for SETTLE_S seconds and then `warmup` more times."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -427,6 +448,7 @@ def _graph_time(fn, warmup: int, reps: int) -> float:
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
         fn()
+    _settle(gr.replay)
     for _ in range(max(1, warmup)):
         gr.replay()
     torch.cuda.synchronize()
@@ -958,6 +980,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         dec_only()
     dgraph.replay()
     torch.cuda.synchronize()
+    _settle(dgraph.replay)
     d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     d0.record()
     for _ in range(20):
@@ -1087,6 +1110,7 @@ def main():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
+    settle = _settle(graph.replay)
     for _ in range(args.warmup):
         graph.replay()
     t_start = torch.cuda.Event(enable_timing=True)
@@ -1136,6 +1160,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"seconds": SETTLE_S, "replays": settle},
         "ms_per_step": round(ms_step, 4),
         "us_per_token_all_layers": round(ms_step * 1e3, 1),
         "hbm_frac_of_step": round(value * 1e9 / PEAK_HBM, 4),
