@@ -860,6 +860,8 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     import kvtier  # noqa: F401
     from kvtier.kvt import PosTieredCache, kvt_decode_attn, kvt_decode_plan
     layers = LAYERS if ragged else 1
+    # a decode plan is one more launch per step that the step's layers share: worth it from two layers on
+    use_plan = args.impl == "mfma" and layers > 1
     if ragged:
         gl = torch.Generator().manual_seed(4)
         lens = [int(math.exp(math.log(1024) + (math.log(65536) - math.log(1024)) * float(u)))
@@ -920,7 +922,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         for layer in range(layers):
             cache.append(layer, plan, knew, vnew)
         cache.commit(plan)
-        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if use_plan else None
         for layer in range(layers):
             kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 
@@ -941,7 +943,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         cache.launch_plan(dplan)
         for layer in range(layers):
             cache.append(layer, dplan, knew, vnew)
-        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if use_plan else None
         for layer in range(layers):
             kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 
@@ -969,7 +971,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
 
     # decode alone over the final state (every layer, one graph): the device's decode rate
     def dec_only():
-        dp = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
+        dp = kvt_decode_plan(cache, HQ, workspace=ws) if use_plan else None
         for layer in range(layers):
             kvt_decode_attn(cache, layer, q[layer], out=out, impl=args.impl, workspace=ws, plan=dp, check_q=False)
 

@@ -358,12 +358,41 @@ def _choose_splits_mfma(max_len: int, items: int, blocks: int = 256, min_pos: in
     return int(max(1, min(n, -(-max_len // min_pos))))
 
 
-def _split_counts_mfma(lens: Sequence[int], items_per_seq: int, blocks: int = 256, min_pos: int = 256) -> List[int]:
-    """Per-sequence split counts of the MFMA kernels for a ragged batch: about `blocks` blocks in all, shared in
-    proportion to the context lengths (each sequence at least 1, each split at least min_pos positions)."""
-    per_item = max(1, blocks // max(1, items_per_seq))
-    tot = max(1, sum(lens))
-    return [int(max(1, min(-(-L // min_pos), round(per_item * L / tot)))) for L in lens]
+HOT_COST4 = 7   # a ring position's share of a split (the kernels' kHotCost4; a paged position costs 4)
+
+
+def _split_counts_mfma(lens: Sequence[int], items_per_seq: int, blocks: int = 256, min_pos: int = 256,
+                       hot: Optional[Sequence[int]] = None) -> List[int]:
+    """Per-sequence split counts of the MFMA kernels for a ragged batch: at most blocks // items_per_seq splits per
+    KV-head item in all (one block per CU: one block more than the CUs would run as a second wave), shared in
+    proportion to each sequence's cost -- 4 per paged position, HOT_COST4 per ring position (hot[i] ring positions
+    of sequence i; all paged if hot is None) -- by largest remainders; each sequence at least 1 split and at most one
+    per min_pos positions."""
+    S = len(lens)
+    per = max(1, blocks // max(1, items_per_seq))
+    hot = hot if hot is not None else [0] * S
+    w = [4 * (L - h) + HOT_COST4 * h for L, h in zip(lens, hot)]
+    caps = [max(1, -(-L // min_pos)) for L in lens]
+    tot = sum(w)
+    if tot <= 0:
+        return [1] * S
+    raw = [per * x / tot for x in w]
+    counts = [max(1, min(cap, int(r))) for r, cap in zip(raw, caps)]
+    left = per - sum(counts)
+    while left > 0:
+        open_ = [i for i in range(S) if counts[i] < caps[i]]
+        if not open_:
+            break
+        open_.sort(key=lambda i: raw[i] - counts[i], reverse=True)
+        for i in open_[:left]:
+            counts[i] += 1
+        left = per - sum(counts)
+    return counts
+
+
+def _hot_counts(cache: "PosTieredCache", S: int) -> List[int]:
+    """Ring (INT8) positions of each of the first S sequences, from the host mirror."""
+    return [cache.h_len[s] - min(cache.h_len[s], cache.hot_start(s)) for s in range(S)]
 
 
 def _decode_grid(cache: "PosTieredCache", Hq: int, splits: Optional[int], ws: dict, device):
@@ -373,7 +402,7 @@ def _decode_grid(cache: "PosTieredCache", Hq: int, splits: Optional[int], ws: di
     rows = _rows_kernel(H, Hq)
     items, min_pos = (1, ROWS_MIN_POS) if rows else (H, 256)
     if splits is None and S > 1:
-        counts = _split_counts_mfma(cache.h_len[:S], items, min_pos=min_pos)
+        counts = _split_counts_mfma(cache.h_len[:S], items, min_pos=min_pos, hot=_hot_counts(cache, S))
         split_map, split_counts, counts = _split_map(counts, ws, device)
         return max(counts), split_map, split_counts, sum(counts), rows
     max_len = max(cache.h_len) if S else 0
@@ -386,7 +415,7 @@ def decode_split_counts(cache: "PosTieredCache", Hq: int) -> List[int]:
     (for callers that prepare a split map themselves, e.g. for the no-allocation entry point)."""
     rows = _rows_kernel(cache.H, Hq)
     items, min_pos = (1, ROWS_MIN_POS) if rows else (cache.H, 256)
-    return _split_counts_mfma(cache.h_len[:cache.n_seqs], items, min_pos=min_pos)
+    return _split_counts_mfma(cache.h_len[:cache.n_seqs], items, min_pos=min_pos, hot=_hot_counts(cache, cache.n_seqs))
 
 
 @dataclass
@@ -495,7 +524,7 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         elif headwise and _rows_kernel(H, Hq):
             # the head-wise kernel's grid (the A/B reference of the full-row kernel)
             if splits is None and S > 1:
-                counts = _split_counts_mfma(cache.h_len[:S], H)
+                counts = _split_counts_mfma(cache.h_len[:S], H, hot=_hot_counts(cache, S))
                 split_map, split_counts, counts = _split_map(counts, ws, q.device)
                 n_chunks, n_map = max(counts), sum(counts)
             else:

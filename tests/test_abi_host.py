@@ -137,6 +137,28 @@ def test_page_allocator_order(kvt_pkg):
         a.pop()
 
 
+def test_ragged_split_counts(kvt_pkg):
+    """Split counts of a ragged decode batch: never more blocks than the budget (a block past one per CU runs as a
+    second wave), at least one per sequence, at most one per min_pos positions, and in proportion to each sequence's
+    cost (a ring position weighs 7 / 4 of a paged one), so the per-block cost spread stays small."""
+    from kvtier.kvt import HOT_COST4, _split_counts_mfma
+    lens = [10498, 10474, 1497, 2452, 1055, 1204, 63627, 45661]           # the ragged 8-sequence workload
+    rings = [min(8192, 1 << (L - 1).bit_length()) for L in lens]
+    hot = [min(L, r) for L, r in zip(lens, rings)]
+    for items, blocks, min_pos in ((1, 256, 64), (2, 256, 256), (1, 100, 64)):
+        c = _split_counts_mfma(lens, items, blocks=blocks, min_pos=min_pos, hot=hot)
+        assert sum(c) <= blocks // items and all(x >= 1 for x in c)
+        assert all(x <= -(-L // min_pos) for x, L in zip(c, lens))
+        cost = [(4 * (L - h) + HOT_COST4 * h) / x for L, h, x in zip(lens, hot, c)]
+        big = [y for y, x in zip(cost, c) if x >= 8]                         # rounding dominates below that
+        assert max(big) / min(big) < 1.3, (c, cost)
+    # length-proportional rounding once gave 257 blocks here; the budget holds for any mix
+    assert sum(_split_counts_mfma(lens, 1, min_pos=64)) <= 256
+    assert _split_counts_mfma([5] * 300, 1, min_pos=64) == [1] * 300       # more sequences than blocks: one each
+    assert _split_counts_mfma([100, 100_000], 1, min_pos=64) == [1, 255]
+    assert _split_counts_mfma([0, 0], 1) == [1, 1]
+
+
 def test_kv_buffer_descs(kvt_pkg):
     """Descriptor names and row sizes of the per-slot buffers (gemv/test_kv_int4.py:311-313): k0.., v0.., ks0..,
     vs0..; payload rows heads * D / 2 bytes (INT4) or heads * D (INT8); scale rows heads * groups * 2 bytes viewed as
