@@ -462,6 +462,58 @@ def _graph_time(fn, warmup: int, reps: int) -> float:
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
+def gather_tier_ratio(args) -> dict:
+    """The reference's tiered-vs-single-tier gather microbench (gemv/test_kv_tiers.py:561-605): 2,048 of a 4,000-token
+    request's positions (sorted), batch 1, through the compact gather into the bf16 scratch -- the tiered pool with
+    every row cold (owner -1) against the INT4 pool alone, and with every row hot (a ring as large as the pool whose
+    rows are the INT8 pool, owner = identity) against the INT8 pool alone.  The reference's plan target is <= 1.10x
+    each.  Device time per call: a HIP graph of 50 back-to-back calls.  Outputs checked bit for bit (all-cold ==
+    INT4, all-hot == INT8), as the reference's bench asserts."""
+    from kvtier import sparse_attn as sa
+    slots, tk, L, reps = 4096, 2048, 4000, 50
+    g = torch.Generator(device="cuda").manual_seed(43)
+    gc = torch.Generator().manual_seed(43)
+    cuda = dict(device="cuda")
+    k4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, generator=g, **cuda)
+    v4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, generator=g, **cuda)
+    ks4 = (0.05 + 0.3 * torch.rand(slots, H, D // 32, generator=g, **cuda)).half()
+    vs4 = (0.05 + 0.3 * torch.rand(slots, H, D // 32, generator=g, **cuda)).half()
+    k8 = torch.randint(-127, 128, (slots, H, D), dtype=torch.int8, generator=g, **cuda)
+    v8 = torch.randint(-127, 128, (slots, H, D), dtype=torch.int8, generator=g, **cuda)
+    ks8 = (0.002 + 0.02 * torch.rand(slots, H, D // 64, generator=g, **cuda)).half()
+    vs8 = (0.002 + 0.02 * torch.rand(slots, H, D // 64, generator=g, **cuda)).half()
+    sm = torch.ones(H, D, dtype=torch.float16, **cuda)
+    r2t = torch.randperm(slots, generator=gc).to(torch.int32)[None].to("cuda")
+    ridx = torch.zeros(1, dtype=torch.int64, **cuda)
+    idx = torch.randperm(L, generator=gc)[:tk].sort().values.to(torch.int32)[None].to("cuda")
+    seq = torch.tensor([L], dtype=torch.int32, **cuda)
+    cu = torch.tensor([0, tk], dtype=torch.int32, **cuda)
+    ok = torch.empty(tk, H, D, dtype=torch.bfloat16, **cuda)
+    ov = torch.empty_like(ok)
+    ring = dict(ring_k=k8, ring_v=v8, ring_ks=ks8, ring_vs=vs8, ring_mask=slots - 1)
+    kw4 = dict(k_scale=ks4, v_scale=vs4, sm_k=sm, sm_v=sm, kv_bits=4)
+    cases = {"tiered_cold": (k4, v4, dict(kw4, owner=torch.full((slots,), -1, dtype=torch.int32, **cuda), **ring)),
+             "int4": (k4, v4, kw4),
+             "tiered_hot": (k4, v4, dict(kw4, owner=torch.arange(slots, dtype=torch.int32, **cuda), **ring)),
+             "int8": (k8, v8, dict(k_scale=ks8, v_scale=vs8, sm_k=sm, sm_v=sm, kv_bits=8))}
+    outs, us = {}, {}
+    for name, (kk, vv, kw) in cases.items():
+        sa.qwen_sparse_kv_extraction_compact_triton(kk, vv, r2t, ridx, idx, seq, cu, ok, ov, 1, tk, **kw)
+        torch.cuda.synchronize()
+        outs[name] = (ok.clone(), ov.clone())
+
+        def calls(kk=kk, vv=vv, kw=kw):
+            for _ in range(reps):
+                sa.qwen_sparse_kv_extraction_compact_triton(kk, vv, r2t, ridx, idx, seq, cu, ok, ov, 1, tk, **kw)
+        us[name] = _graph_time(calls, args.warmup, max(args.steps, 5)) / reps * 1e6
+    same = lambda a, b: all(torch.equal(x, y) for x, y in zip(outs[a], outs[b]))
+    return {"us_per_call": {k: round(v, 2) for k, v in us.items()},
+            "cold_vs_int4": round(us["tiered_cold"] / us["int4"], 3),
+            "hot_vs_int8": round(us["tiered_hot"] / us["int8"], 3),
+            "bit_exact": same("tiered_cold", "int4") and same("tiered_hot", "int8"),
+            "reference_target": 1.10}
+
+
 def sparse_workload(args) -> dict:
     """Top-k sparse decode over the tiered (slot-indexed) pool: 8 requests of 65,536 tokens on randomly allocated
     slots, 12 layers, 2,051 selected positions per request (distinct, random), INT8-G64 ring of 8,192 rows whose
@@ -542,6 +594,7 @@ def sparse_workload(args) -> dict:
                                "2,051 selected positions each, tiered pool (INT8-G64 ring of 8,192 rows + INT4-G32)",
                    "hot_fraction": round(n_hot / hot.numel(), 4)},
         "gather_only_us_per_step": round(t_gather * 1e6, 1),
+        "gather_tier_ratio": gather_tier_ratio(args),
         "kv_bytes_per_layer": bytes_layer,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
@@ -1033,7 +1086,8 @@ def sub_configs(args) -> dict:
 
     def pick_sparse(r):
         return {"us_per_step": r["value"], "GBps": r["roofline"]["achieved"], "hbm_frac": r["roofline"]["frac"],
-                "kv_bytes_per_layer": r["kv_bytes_per_layer"], "gather_only_us_per_step": r["gather_only_us_per_step"]}
+                "kv_bytes_per_layer": r["kv_bytes_per_layer"], "gather_only_us_per_step": r["gather_only_us_per_step"],
+                "gather_tier_ratio": r["gather_tier_ratio"]}
 
     run("prefill10k", prefill_workload,
         lambda r: {"ms_per_prompt": r["value"], "kernel_ms": r["roofline"]["kernel_ms"],

@@ -98,6 +98,14 @@ int kvt_append_evict(const void* k, const void* v, int dtype, int64_t sk_n, int6
 
 /* ----------------------------------------------------------------------------------------- gathers */
 
+/* Valid top-k counts and the packing offsets of kvt_compact_gather, in one launch: counts[b] = the number of columns
+ * c < topk whose position indices[b * idx_stride + c] lies in [0, seq_lens[b]); cu_k[0] = 0 and cu_k[b + 1] =
+ * counts[0] + ... + counts[b] (int32, or int64 if cu_is_int64).  seq_lens, indices and counts are int32; idx_stride
+ * >= 0 (0: every request reads row 0).  Replaces the upstream qwen_sparse_fa2_cu_seqlens_triton the reference calls
+ * before a compact gather (gemv/test_kv_tiers.py:297-301, gemv/test_kv_int4.py:150). */
+int kvt_sparse_cu_seqlens(const void* seq_lens, const void* indices, int64_t idx_stride, void* counts, void* cu_k,
+                          int cu_is_int64, int batch, int topk, void* stream);
+
 /* Top-k gather-dequant into a bf16 scratch [*, H, D]: column c of request b is written at row cu_k[b] + c iff
  * c < cu_k[b+1] - cu_k[b] and 0 <= indices[b][c] < seq_lens[b]; nothing else is written.  kind 0 = INT8 pool
  * (k/v are the int8 codes, ring arguments unused), 1 = INT4 pool, 2 = tiered (owner test per row).  Replaces

@@ -36,6 +36,7 @@ SIGNATURES = {
     "kvt_append_plan": [_I, _P, _P, _P, _P, _P, _P, _L, _I, _P, _I, _P, _P, _P, _P, _P],
     "kvt_append_evict": [_P, _P, _I, _L, _L, _L, _L, _P, _P, _L, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _L, _P, _P, _I, _P],
+    "kvt_sparse_cu_seqlens": [_P, _P, _L, _P, _P, _I, _I, _I, _P],
     "kvt_compact_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P, _P, _I,
                            _I, _I, _I, _I, _I, _P, _P, _P],
     "kvt_sparse_decode": [_I, _P, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L,

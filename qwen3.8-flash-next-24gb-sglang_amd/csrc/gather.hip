@@ -14,6 +14,8 @@
 //                       patches/kv_int4.py:396-460; patches/kv_int8.py:365-420)
 //   kvt_prefix_gather   rows [0, seq_len) -> packed at cu_k[b] (patches/kv_tiers.py:541-683;
 //                       patches/kv_int4.py:463-557; patches/kv_int8.py:423-504)
+//   kvt_sparse_cu_seqlens  valid top-k counts and their prefix sum, the offsets kvt_compact_gather packs at (the
+//                       upstream qwen_sparse_fa2_cu_seqlens_triton the reference calls first, gemv/test_kv_tiers.py:297-301)
 
 #include "kvt_common.h"
 
@@ -214,6 +216,62 @@ bool aligned_args(int kind, const void* k, const void* v, const void* rk, const 
   return al(k, ca) && al(v, ca) && al(rk, 8) && al(rv, 8) && al(ok, 16) && al(ov, 16);
 }
 
+
+// counts[b] = #{c < topk : 0 <= indices[b * idx_stride + c] < seq_lens[b]}; cu_k[0] = 0, cu_k[b + 1] = counts[0] + ..
+// + counts[b].  One block of kCuThreads: rows go to the wavefronts in turn (64 columns per coalesced load, a wavefront
+// sum per row), then the block scans a chunk of kCuThreads counts in LDS (Hillis-Steele, double-buffered) and adds
+// the running total of the earlier chunks.
+constexpr int kCuThreads = 1024;
+
+__global__ void __launch_bounds__(kCuThreads) cu_seqlens_kernel(const int32_t* seq_lens, const int32_t* indices,
+                                                                 int64_t idx_stride, int32_t* counts, void* cu_k,
+                                                                 int cu_is_int64, int batch, int topk) {
+  __shared__ int32_t buf[2][kCuThreads];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  constexpr int kW = kCuThreads / 64;
+  auto put = [&](int64_t i, int64_t v) {
+    if (cu_is_int64) ((int64_t*)cu_k)[i] = v;
+    else ((int32_t*)cu_k)[i] = (int32_t)v;
+  };
+  if (t == 0) put(0, 0);
+  int64_t carry = 0;
+  for (int r0 = 0; r0 < batch; r0 += kCuThreads) {
+    const int nrows = min(kCuThreads, batch - r0);
+    for (int r = wave; r < nrows; r += kW) {
+      const int b = r0 + r;
+      const int64_t L = seq_lens[b];
+      const int32_t* row = indices + (int64_t)b * idx_stride;
+      int n = 0;
+      for (int c0 = 0; c0 < topk; c0 += 64) {
+        const int c = c0 + lane;
+        if (c < topk) {
+          const int64_t p = row[c];
+          n += (p >= 0 && p < L) ? 1 : 0;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o, 64);
+      if (lane == 0) {
+        buf[0][r] = n;
+        counts[b] = n;
+      }
+    }
+    __syncthreads();
+    int cur = 0;
+    if (t >= nrows) buf[0][t] = 0;
+    __syncthreads();
+    for (int d = 1; d < kCuThreads; d <<= 1) {
+      const int v = buf[cur][t] + (t >= d ? buf[cur][t - d] : 0);
+      buf[cur ^ 1][t] = v;
+      cur ^= 1;
+      __syncthreads();
+    }
+    if (t < nrows) put((int64_t)r0 + t + 1, carry + buf[cur][t]);
+    carry += buf[cur][kCuThreads - 1];
+    __syncthreads();   // the next chunk overwrites buf
+  }
+}
+
 }  // namespace
 
 #define KVT_GATHER_DISPATCH(LAUNCH)                        \
@@ -230,6 +288,15 @@ bool aligned_args(int kind, const void* k, const void* v, const void* rk, const 
   }
 
 extern "C" {
+
+int kvt_sparse_cu_seqlens(const void* seq_lens, const void* indices, int64_t idx_stride, void* counts, void* cu_k,
+                          int cu_is_int64, int batch, int topk, void* stream) {
+  if (batch < 0 || topk < 0 || idx_stride < 0) return KVT_EINVAL;
+  hipLaunchKernelGGL(cu_seqlens_kernel, dim3(1), dim3(kCuThreads), 0, (hipStream_t)stream, (const int32_t*)seq_lens,
+                     (const int32_t*)indices, idx_stride, (int32_t*)counts, cu_k, cu_is_int64, batch, topk);
+  KVT_CHECK_LAUNCH();
+  return KVT_OK;
+}
 
 // kind: 0 = INT8 pool, 1 = INT4 pool, 2 = tiered.  All pointers are device pointers of torch-owned tensors.
 int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_scale, const void* v_scale,

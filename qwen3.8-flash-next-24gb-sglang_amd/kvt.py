@@ -656,7 +656,9 @@ def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, 
     assert req_indices.dtype == torch.int64 and seq_lens.dtype == torch.int32
     g8 = D // rks.shape[-1]
     if max_len is None:
-        max_len = int(seq_lens.max())
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("decode_attn_slots: pass max_len (a host int >= every seq_len) under graph capture")
+        max_len = int(seq_lens.max())   # one device reduction and synchronization
     if impl == "mfma":
         from .sparse_attn import qwen_sparse_decode_attn
         ws = workspace if workspace is not None else {}
@@ -746,7 +748,9 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
         kv_lens = cache.seq_lens[:batch]
     assert kv_lens.dtype == torch.int32 and kv_lens.is_cuda and kv_lens.numel() >= batch
     if max_q is None:
-        max_q = int((cu_q[1:] - cu_q[:-1]).max()) if batch else 0
+        if torch.cuda.is_current_stream_capturing():
+            raise ValueError("kvt_prefill_attn: pass max_q (the longest chunk, a host int) under graph capture")
+        max_q = int((cu_q[1:] - cu_q[:-1]).max()) if batch else 0   # one device reduction and synchronization
     if out is None:
         out = torch.empty(q.shape, dtype=out_dtype, device=q.device)
     assert out.shape == q.shape and out.dtype in (torch.bfloat16, torch.float32) and out.stride(2) == 1
@@ -755,7 +759,9 @@ def kvt_prefill_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, cu_q: t
     if k_src is not None:
         assert batch == 1 and k_src.dtype == torch.bfloat16 and v_src.dtype == torch.bfloat16
         assert k_src.stride(2) == 1 and v_src.stride(2) == 1 and k_src.shape[1:] == (H, D) == v_src.shape[1:]
-        if min(k_src.shape[0], v_src.shape[0]) < int(kv_lens[0]):
+        # (a synchronization; skipped under capture, where keys past k_src's rows read as zero: the kernel's reads
+        # of k_src / v_src are bounded by their row count)
+        if not torch.cuda.is_current_stream_capturing() and min(k_src.shape[0], v_src.shape[0]) < int(kv_lens[0]):
             raise ValueError("k_src / v_src hold fewer rows than the context length")
     elif max((cache.hot_start(s) for s in range(batch)), default=0) > 8192 * 64:
         raise ValueError("kvt_prefill_attn: paged key ranges beyond 524,288 positions are not supported")

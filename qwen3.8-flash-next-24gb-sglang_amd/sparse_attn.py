@@ -150,13 +150,17 @@ def _idx_args(t: torch.Tensor):
 def qwen_sparse_fa2_cu_seqlens_triton(seq_lens, indices, counts, cu_k, batch, topk):
     """Valid counts (0 <= pos < seq_len among the first topk columns) and their exclusive prefix sum cu_k
     [batch + 1], in place (the upstream helper the reference's tests call before a compact gather,
-    gemv/test_kv_tiers.py:297-301).  Device tensor ops, no host sync."""
-    idx = indices[:batch, :topk].long()
-    valid = (idx >= 0) & (idx < seq_lens[:batch].long()[:, None])
-    c = valid.sum(1)
-    counts[:batch].copy_(c.to(counts.dtype))
-    cu_k[0] = 0
-    cu_k[1:batch + 1].copy_(c.cumsum(0).to(cu_k.dtype))
+    gemv/test_kv_tiers.py:297-301): one HIP launch (kvt_sparse_cu_seqlens), no host sync.  seq_lens, indices and
+    counts int32; cu_k int32 or int64."""
+    assert seq_lens.dtype == torch.int32 and indices.dtype == torch.int32 and counts.dtype == torch.int32
+    assert cu_k.dtype in (torch.int32, torch.int64) and cu_k.is_contiguous() and counts.is_contiguous()
+    assert seq_lens.is_contiguous() and indices.dim() == 2 and indices.stride(1) == 1
+    assert seq_lens.numel() >= batch and counts.numel() >= batch and cu_k.numel() >= batch + 1
+    assert batch == 0 or indices.shape[0] >= batch or indices.stride(0) == 0
+    assert topk <= indices.shape[1]
+    _lib.require_device(seq_lens, indices, counts, cu_k)
+    _lib.call("kvt_sparse_cu_seqlens", seq_lens.data_ptr(), indices.data_ptr(), indices.stride(0), counts.data_ptr(),
+              cu_k.data_ptr(), int(cu_k.dtype == torch.int64), int(batch), int(topk), _lib.stream())
 
 
 def qwen_sparse_kv_extraction_compact_triton(

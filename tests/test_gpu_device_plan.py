@@ -240,3 +240,58 @@ def test_device_plan_refusals(kvt_pkg):
     assert int(c.plan_status.item()) == 1 and torch.equal(c.page_table, pt0) and int(c.seq_lens[0]) == 256
     with pytest.raises(RuntimeError):
         c.sync_host()
+
+
+def test_capture_requires_host_ints(kvt_pkg):
+    """Wrappers whose defaults would read a device value (a host synchronization, which breaks a graph capture) raise
+    ValueError under capture before any launch: kvt_prefill_attn without max_q, decode_attn_slots without max_len.
+    With the host ints passed the same calls capture and replay."""
+    from kvtier.kvt import decode_attn_slots, kvt_prefill_attn
+    host, devc, g = _prefilled_pair(8)
+    q = (torch.randn(300, HQ, D, device=dev, generator=g) / 16).to(torch.bfloat16)
+    cu_q = torch.tensor([0, 200, 300], dtype=torch.int32, device=dev)
+    kvt_prefill_attn(devc, 0, q, cu_q, max_q=200)   # the workspace exists before the capture
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        gr = torch.cuda.CUDAGraph()
+        with pytest.raises(ValueError, match="max_q"):
+            with torch.cuda.graph(gr, stream=side):
+                kvt_prefill_attn(devc, 0, q, cu_q)
+    torch.cuda.synchronize()
+    out = torch.empty_like(q)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        kvt_prefill_attn(devc, 0, q, cu_q, max_q=200, out=out)
+    gr.replay()
+    torch.cuda.synchronize()
+    want = kvt_prefill_attn(devc, 0, q, cu_q, max_q=200)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    # the slot-indexed decode: max_len under capture
+    slots, R = 1024, 64
+    k4 = torch.randint(0, 256, (slots, H, D // 2), dtype=torch.uint8, device=dev)
+    ks4 = torch.full((slots, H, D // 32), 0.01, dtype=torch.float16, device=dev)
+    rk = torch.randint(-127, 128, (R, H, D), dtype=torch.int8, device=dev)
+    rks = torch.full((R, H, D // 64), 0.01, dtype=torch.float16, device=dev)
+    owner = torch.full((R,), -1, dtype=torch.int32, device=dev)
+    r2t = torch.arange(slots, dtype=torch.int32, device=dev).reshape(2, 512)
+    qd = (torch.randn(2, HQ, D, device=dev, generator=g) / 16).to(torch.bfloat16)
+    sl = torch.tensor([500, 77], dtype=torch.int32, device=dev)
+    ridx = torch.arange(2, dtype=torch.int64, device=dev)
+    args = (qd, sl, r2t, ridx, k4, k4, ks4, ks4, rk, rk, rks, rks, owner, R - 1)
+    ws = {}
+    eager = decode_attn_slots(*args, max_len=512, workspace=ws)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        gr = torch.cuda.CUDAGraph()
+        with pytest.raises(ValueError, match="max_len"):
+            with torch.cuda.graph(gr, stream=side):
+                decode_attn_slots(*args, workspace=ws)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        cap = decode_attn_slots(*args, max_len=512, workspace=ws)
+    gr.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(cap, eager)

@@ -273,3 +273,36 @@ def test_gathers_reject_misaligned_scratch(tiered_state):
         rows = rtt[b, :int(lens[b])].long().cpu()
         a, e = int(cu[b]), int(cu[b + 1])
         assert torch.equal(gk[a:e], st["dk_all"][rows]) and torch.equal(gv[a:e], st["dv_all"][rows])
+
+
+@pytest.mark.parametrize("batch,topk,cu64,shared", [(0, 64, False, False), (1, 1, False, False), (3, 63, True, False),
+                                                     (7, 2051, False, False), (1500, 65, True, False),
+                                                     (2100, 130, False, False), (5, 200, False, True)])
+def test_cu_seqlens_kernel(kvt_pkg, batch, topk, cu64, shared):
+    """kvt_sparse_cu_seqlens against the oracle's count and prefix sum (pinned by brute force on the CPU): columns
+    below 0 (the -1 padding of a top-k), at or past seq_len, ragged lengths including 0, more rows than the block's
+    1024 threads (two scan chunks with a carry), a row stride of 0 (one index row shared by every request) and the
+    int64 offsets; counts and cu_k bit-exact, nothing written past cu_k[batch]."""
+    from kvtier import sparse_attn as sa
+    g = torch.Generator().manual_seed(batch * 7 + topk)
+    seq = torch.randint(0, 3000, (max(batch, 1),), generator=g, dtype=torch.int32)
+    if batch:
+        seq[0] = 0
+    width = topk + 5
+    rows = 1 if shared else max(batch, 1)
+    idx = torch.randint(-3, 3200, (rows, width), generator=g, dtype=torch.int32)
+    idx[:, ::7] = -1
+    idx_dev = idx.to(dev)
+    if shared:
+        idx_dev = idx_dev[:1].expand(batch, width)
+        idx_full = idx.expand(batch, width)
+    else:
+        idx_full = idx[:batch]
+    counts = torch.full((batch + 2,), -7, dtype=torch.int32, device=dev)
+    cu = torch.full((batch + 3,), -7, dtype=torch.int64 if cu64 else torch.int32, device=dev)
+    sa.qwen_sparse_fa2_cu_seqlens_triton(seq.to(dev), idx_dev, counts, cu, batch, topk)
+    torch.cuda.synchronize()
+    want = ref.cu_seqlens_valid(seq[:batch], idx_full, topk)
+    assert torch.equal(cu.cpu()[:batch + 1].to(torch.int32), want)
+    assert torch.equal(counts.cpu()[:batch], (want[1:] - want[:-1]))
+    assert bool((cu.cpu()[batch + 1:] == -7).all()) and bool((counts.cpu()[batch:] == -7).all())
