@@ -219,7 +219,8 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
     res = {"impl": impl}
     for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
         acc = per_kernel(path, counter)
-        dec = [v for k, v in acc.items() if "decode_mfma_kernel" in k or "decode_ref_kernel" in k]
+        dec = [v for k, v in acc.items()
+               if "decode_rows_kernel" in k or "decode_mfma_kernel" in k or "decode_ref_kernel" in k]
         cal = [v for k, v in acc.items() if "copy" in k.lower() and max(v) * 1024 > CAL_BYTES / 4]
         assert dec and cal, (counter, list(acc))
         dec_v = [x for v in dec for x in v]
@@ -1178,15 +1179,32 @@ def main():
     t_end.record()
     torch.cuda.synchronize()
     ms_step = t_start.elapsed_time(t_end) / args.steps
-    # kernel timing: HIP events on the launch stream around each split-K launch of eager steps
-    kev = []
-    for _ in range(args.steps):
-        step(kev)
+    # kernel timing: HIP events on the launch stream around K replays of a graph of the 12 split-K launches alone
+    # (the step's plan built before), per launch = elapsed / (K x 12): the kernel's device time plus the boundary to
+    # the next launch, no host gaps (events around eager launches also count the launch latency)
+    kplan = kvt_decode_plan(cache, HQ, workspace=ws) if args.impl == "mfma" else None
+
+    def splitk_only():
+        for layer in range(LAYERS):
+            kvt_decode_attn(cache, layer, q[layer], out=outs[layer], impl=args.impl, workspace=ws, plan=kplan,
+                            check_q=False, partials_only=True)
+
+    kgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(kgraph):
+        splitk_only()
+    _settle(kgraph.replay)
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    kern_ms = [a.elapsed_time(b) for a, b, _ in kev]
-    comb_ms = [b.elapsed_time(c) for _, b, c in kev]
-    kern_avg_s = sum(kern_ms) / len(kern_ms) / 1e3
-    comb_avg_us = sum(comb_ms) / len(comb_ms) * 1e3
+    k0.record()
+    for _ in range(args.steps):
+        kgraph.replay()
+    k1.record()
+    torch.cuda.synchronize()
+    kern_avg_s = k0.elapsed_time(k1) / 1e3 / (args.steps * LAYERS)
+    # the rest of a step per layer: the combine launch and its boundary (plus 1 / 12 of the plan launch)
+    comb_avg_us = (ms_step / 1e3 / LAYERS - kern_avg_s) * 1e6
+    graph.replay()   # the outputs of a full step again, for the parity check below
+    torch.cuda.synchronize()
     bytes_layer = cache.kv_bytes()
     bytes_step = bytes_layer * LAYERS
     value = bytes_step / (ms_step / 1e3) / 1e9
@@ -1243,7 +1261,8 @@ def main():
             "traffic": traffic,
             "kernel": "decode split-K (per layer launch)",
             "kernel_avg_us": round(kern_avg_s * 1e6, 2),
-            "combine_avg_us": round(comb_avg_us, 2),
+            "kernel_timing": "graph of the 12 split-K launches alone, HIP events, per launch incl. the boundary",
+            "rest_of_layer_us": round(comb_avg_us, 2),
         },
         "cpu_baseline": cpu,
         "parity": parity,

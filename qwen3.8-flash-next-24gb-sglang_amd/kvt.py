@@ -479,7 +479,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
                     out_dtype: torch.dtype = torch.float32, workspace: Optional[dict] = None,
                     events: Optional[list] = None, splits: Optional[int] = None,
                     deterministic: bool = False, tile_order: Optional[str] = None,
-                    plan: Optional[DecodePlan] = None, headwise: bool = False, check_q: bool = True) -> torch.Tensor:
+                    plan: Optional[DecodePlan] = None, headwise: bool = False, check_q: bool = True,
+                    partials_only: bool = False) -> Optional[torch.Tensor]:
     """Decode attention of one query token per sequence over the tiered cache of `layer`.
 
     q: bf16 [S, Hq, D] (S = cache.n_seqs); returns out [S, Hq, D] (fp32 or bf16) = softmax(q K^T / sqrt(D)) V over
@@ -492,6 +493,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
     every block starts from its plan entry instead of computing its ranges; a plan older than the cache's state raises
     ValueError.
     events: if a list, timing events (start, after the split-K kernel, after the combine) are appended.
+    partials_only: launch the split-K kernel alone (its partials stay in the workspace; returns None) -- to time
+    the kernel by itself.
     deterministic (impl "mfma"): bit-identical results from call to call: tiles go to the wavefronts of a block in
     a fixed order and the combine kernel merges the splits.  By default tiles go first come (the block's wavefronts
     finish together) and the fp32 summation order varies in the last bits.
@@ -581,6 +584,8 @@ def kvt_decode_attn(cache: PosTieredCache, layer: int, q: torch.Tensor, out: Opt
         raise ValueError(f"unknown decode implementation {impl!r}")
     if events is not None:
         ev1.record()
+    if partials_only:
+        return None
     _lib.call("kvt_decode_combine", po.data_ptr(), pml.data_ptr(), S, H, Hq, D, n_chunks, chunk,
               cache.seq_lens.data_ptr(), _lib.ptr(split_counts), out.data_ptr() if out.dtype == torch.float32 else None,
               out.data_ptr() if out.dtype == torch.bfloat16 else None, out.stride(0), _lib.stream())
