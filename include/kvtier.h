@@ -267,12 +267,14 @@ int kvt_decode_mfma_noalloc(const void* q, int64_t q_stride_b, const void* seq_l
  * chunks.  Hq / H <= 16, D = 256; q 16-byte aligned with sq_n, sq_h multiples of 8 (Q rows are read 16 bytes at a
  * time); pool_rows = rows of the INT4 pool and kb_rows = rows of the bf16 source (byte offsets are 32-bit, else
  * KVT_ERANGE).  A block stages the page ids of its paged positions in LDS: at most 8,192
- * pages (paged positions below 524,288) per sequence; the caller checks this bound (lengths live on the device).
+ * pages (paged positions below 524,288) per sequence; a query tile whose paged key range exceeds it gets NaN outputs
+ * (never keys from the wrong pages), and the Python wrapper refuses such a call from its host lengths.
  * spread_blocks > 0: that many blocks share the launch's key tiles equally (query tiles are split where a share
  * ends; of a query tile's pieces, the one that finishes last merges them in piece order), instead of one block
  * per query tile -- the latest query tiles of a causal chunk see up to a chunk length more keys than the earliest,
  * so one block per CU with equal shares ends them all together.  It needs `work`, at least kvt_prefill_work_bytes
- * bytes, whose counter area (its first bytes) is zero before the first call -- each call leaves it at zero again;
+ * bytes, whose counter area (its first 16 KB, the same for every call) is zero before the first call -- each call
+ * leaves it at zero again;
  * calls that share a workspace must not overlap; at most 4,096 query tiles (batch x H x tiles of 128 rows), else
  * KVT_ERANGE.  The output does not depend on which block merges. */
 int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q, int cu_q_is_int64,

@@ -598,6 +598,7 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
   const int qpw = 16 / gs;   // queries per wavefront
   const int64_t qs = Q.qs, q_len = Q.q_len, L = Q.L, q_pos0 = Q.q_pos0, qt0 = Q.qt0, key_end = Q.key_end;
   constexpr uint32_t NG8 = kD / G8;
+  bool pages_fit = true;   // the paged key range fits the kMaxLdsPages page ids staged in LDS
   Tier T;
   T.H = H;
   T.h = h;
@@ -627,7 +628,9 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
     T.rks = make_rsrc(S.rks + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
     T.rvs = make_rsrc(S.rvs + rbase * H * NG8, (uint32_t)R * (uint32_t)H * NG8 * 2u);
     // page ids of the paged key range, once per block
-    const int64_t npg = min((min((int64_t)T.hs, key_end) + kPage - 1) / kPage, (int64_t)kMaxLdsPages);
+    const int64_t need = (min((int64_t)T.hs, key_end) + kPage - 1) / kPage;
+    pages_fit = need <= kMaxLdsPages;
+    const int64_t npg = min(need, (int64_t)kMaxLdsPages);
     for (int64_t i = tid; i < npg; i += 64 * kWaves) lds.pages[i] = S.page_table[b * S.pt_stride + i];
     if (tid == 0 && npg == 0) lds.pages[0] = 0;
   }
@@ -646,7 +649,9 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
   // 32 st + 8 kb .. + 7 of the row in one 16-byte load per st (the host checks the 16-byte alignment)
   bf8 qop[8];
   int64_t qpos;   // position of this lane's query row (as the S^T column)
-  const float qmul = scale * kLog2e;
+  // a paged range beyond the staged page ids would read clamped pages: the tile's outputs become NaN instead (NaN
+  // scores give NaN weights, sums and outputs), never silently wrong keys
+  const float qmul = pages_fit ? scale * kLog2e : __builtin_nanf("");
   {
     const int rq = n16 / gs, hq = n16 - rq * gs;
     const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
@@ -1073,12 +1078,14 @@ prefill_mfma_kernel(KVSrc S, const uint16_t* q, int64_t sq_n, int64_t sq_h, cons
   }
 }
 
-// query tiles of a launch, and the counter area at the start of the spread workspace (256-byte aligned)
+// query tiles of a launch, and the counter area at the start of the spread workspace: one int32 per possible item
+// (kMaxItems), the same for every call, so the slots of one call never overlap the counters of another (a call with
+// more items than the previous one would otherwise find that call's slot data in its counters and merge early)
 int prefill_qtiles(int max_q, int H, int Hq) {
   const int qb = kWaves * (16 / (Hq / H));   // queries per block
   return (max_q + qb - 1) / qb;
 }
-int64_t prefill_counter_bytes(int bh_n, int n_qtiles) { return ((int64_t)bh_n * n_qtiles * 4 + 255) & ~(int64_t)255; }
+constexpr int64_t kCounterBytes = (int64_t)kMaxItems * 4;   // 16 KB, a multiple of 256
 
 }  // namespace
 
@@ -1093,7 +1100,7 @@ int kvt_prefill_work_bytes(int batch, int H, int Hq, int max_q, int spread_block
   }
   const int64_t n_items = (int64_t)batch * H * prefill_qtiles(max_q, H, Hq);
   if (n_items > kMaxItems || spread_blocks > (1 << 20)) return KVT_ERANGE;
-  *bytes = prefill_counter_bytes((int)n_items, 1) + (n_items + spread_blocks - 1) * kSlotFloats * 4;
+  *bytes = kCounterBytes + (n_items + spread_blocks - 1) * kSlotFloats * 4;
   return KVT_OK;
 }
 
@@ -1132,7 +1139,7 @@ int kvt_prefill_attn(const void* q, int64_t sq_n, int64_t sq_h, const void* cu_q
     if (rc != KVT_OK) return rc;
     if (work == nullptr || work_bytes < need) return KVT_EINVAL;
     ctr = static_cast<int32_t*>(work);
-    part = reinterpret_cast<float*>(static_cast<char*>(work) + prefill_counter_bytes(bh_n, n_qtiles));
+    part = reinterpret_cast<float*>(static_cast<char*>(work) + kCounterBytes);
   } else if ((int64_t)n_qtiles * bh_n > 0x7fffffffLL) {
     return KVT_ERANGE;
   }

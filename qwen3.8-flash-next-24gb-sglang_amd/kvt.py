@@ -702,7 +702,7 @@ def decode_attn_slots(q, seq_lens, req_to_token, req_indices, k4, v4, ks4, vs4, 
     return out
 
 
-_prefill_ws: dict = {}   # device index -> zeroed kvt_prefill_attn workspace (counters stay zero between calls)
+_prefill_ws: dict = {}   # (device index, stream) -> zeroed kvt_prefill_attn workspace (counters stay zero between calls)
 _cu_count: dict = {}
 PREFILL_MAX_ITEMS = 4096   # (sequence, KV head, query tile) items of a spread prefill launch
 
@@ -719,13 +719,16 @@ def prefill_spread_blocks(items: int, device: torch.device) -> int:
 
 
 def prefill_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The device's cached prefill workspace, at least nbytes, zeroed when (re)allocated.  Calls on one stream
-    share it; calls that may overlap (several streams) pass their own `work`."""
+    """The cached prefill workspace of (device, current stream), at least nbytes, zeroed when (re)allocated.  Calls
+    on one stream run one after another and share it (each call leaves its merge counters at zero); calls on other
+    streams get their own, so launches that may overlap never share counters.  (Allocate it before a graph capture:
+    capture records on a side stream, which then owns a workspace of its own.)"""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _prefill_ws.get(idx)
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    ws = _prefill_ws.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
-        _prefill_ws[idx] = ws
+        _prefill_ws[key] = ws
     return ws
 
 

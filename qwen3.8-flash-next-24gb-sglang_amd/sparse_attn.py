@@ -314,7 +314,9 @@ def sparse_gqa_fwd_interface_paged(
     fp16 [rows, H, D / 64] for kv_bits 8, uint8 [rows, H, D / 2] + fp16 [rows, H, D / 32] for kv_bits 4); sm_k / sm_v
     [H, D]; the ring arguments select the tiered pool.  Query j of chunk b attends the entries of its index row
     among the first min(topk, j + kv_len - q_len + 1) that lie in [0, kv_len); an entry outside is ignored, and a row
-    with none comes out NaN (0/0), as the reference.  K/V rows are dequantized exactly as the gathers write them,
+    with none comes out NaN (0/0), as the reference.  (The reference kernel reads on to the next multiple of its
+    16-column tile, patches/kv_paged_prefix.py:201-202; the columns between hold -1 in an indexer row, and entries
+    planted there are ignored here, as the reference test's oracle does.)  K/V rows are dequantized exactly as the gathers write them,
     QK^T and P.V on bf16 matrix cores with fp32 accumulation.  max_q = the longest chunk (host int).  `config` is the
     reference's Triton tile configuration and has no meaning here (accepted and ignored).  Returns a new bf16 tensor
     shaped like q, as the reference; `out` (an addition: bf16 or fp32, shaped like q, unit last stride) receives the

@@ -20,9 +20,10 @@ def test_library_exports_header_symbols(kvt_pkg):
 
 
 def test_prefill_work_bytes(kvt_pkg):
-    """Workspace of a spread prefill launch: a 4-byte counter per (sequence, KV head, query tile of 128 rows), padded
-    to 256 bytes, then one 132,096-byte slot (O of 128 rows x 256 dims, m and l of 128 rows, fp32) per query tile
-    and per block beyond the first."""
+    """Workspace of a spread prefill launch: a counter area of 16 KB (one 4-byte counter for each of the at most
+    4,096 (sequence, KV head, query tile of 128 rows) items, the same for every call, so one call's slots never
+    overlap another call's counters), then one 132,096-byte slot (O of 128 rows x 256 dims, m and l of 128 rows,
+    fp32) per query tile and per block beyond the first."""
     lib = kvt_pkg._lib
     need = ctypes.c_int64(-1)
 
@@ -33,9 +34,9 @@ def test_prefill_work_bytes(kvt_pkg):
     slot = (128 * 256 + 128 * 2) * 4
     assert slot == 132_096
     assert work(1, 2, 16, 2048, 0) == 0                        # one block per query tile: no workspace
-    assert work(1, 2, 16, 2048, 256) == 1024 + (256 + 255) * slot
+    assert work(1, 2, 16, 2048, 256) == 16384 + (256 + 255) * slot
     # 24 / 2 heads: a wavefront's 16 rows hold one query (12 rows), so a tile is 8 queries: 13 tiles of 100
-    assert work(3, 2, 24, 100, 7) == 512 + (6 * 13 + 6) * slot
+    assert work(3, 2, 24, 100, 7) == 16384 + (6 * 13 + 6) * slot
     assert work(2, 2, 16, 0, 3) == 0
     for bad in ((1, 2, 16, 64, -1), (1, 2, 15, 64, 2), (1, 1, 32, 64, 2)):
         with pytest.raises(ValueError):

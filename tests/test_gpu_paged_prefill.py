@@ -170,6 +170,35 @@ def test_paged_prefill_dirty_indices_ignored(kvt_pkg):
     close(got, exp)
 
 
+def test_paged_prefill_row_limit_is_visible(kvt_pkg):
+    """A query reads exactly the first min(topk, visible) entries of its index row (the reference test's oracle,
+    gemv/test_kv_paged_prefix.py:515-517).  The reference kernel reads on to the next multiple of its 16-column tile
+    (row_limit = min(topk, roundup16(row_topk)), patches/kv_paged_prefix.py:201-202) and would attend valid positions
+    placed there; an indexer row holds -1 at those columns, so the two agree on the reference's inputs.  Pinned here:
+    valid positions (< kv_len, beyond the query's own) planted at columns visible .. roundup16(visible) - 1 change
+    nothing, bit for bit.  Parity with the reference kernel on such rows stays unpinned (its rows never have them)."""
+    gen = torch.Generator().manual_seed(45)
+    slots, R = 8192, 1024
+    p = slot_pools(slots, R, 64, gen)
+    c = _case(gen, [0, 3000, 1500], [256, 300, 128], slots, 16)
+    planted, clean = c["idx"].clone(), c["idx"].clone()
+    n_planted = 0
+    for r in range(planted.shape[0]):
+        b = int((c["cu_q"] <= r).sum()) - 1
+        j = r - int(c["cu_q"][b])
+        vis = c["prefix_lens"][b] + j + 1
+        n = min(TOPK, vis)
+        lim = min(TOPK, -(-n // 16) * 16)
+        if lim > n:
+            planted[r, n:lim] = torch.randint(0, c["seq_lens"][b], (lim - n,), generator=gen).to(torch.int32)
+            clean[r, n:lim] = -1
+            n_planted += lim - n
+    assert n_planted > 1000
+    for kind in ("tiered", "int4", "int8"):
+        assert torch.equal(_run(c, kind, p, R, idx=planted).view(torch.int16),
+                           _run(c, kind, p, R, idx=clean).view(torch.int16)), kind
+
+
 def test_paged_prefill_per_head_indices(kvt_pkg):
     """3-d indices [total_q, H, topk]: each KV head attends its own selection; topk 700 (< the prefix)."""
     gen = torch.Generator().manual_seed(44)

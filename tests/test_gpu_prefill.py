@@ -373,3 +373,79 @@ def test_prefill_clamp_regime_scores(kvt_pkg):
             assert bool((err[ok] <= 2e-3).all()), (a, h, float(err[ok].max()))
             checked += int(ok.sum())
     assert checked > 2000
+
+
+def test_prefill_paged_range_beyond_staged_pages(kvt_pkg):
+    """A sequence whose paged key range needs more than the 8,192 page ids a block stages in LDS (524,288 paged
+    positions): the wrapper refuses it from its host lengths (ValueError), and the kernel, called through the C ABI
+    without that check, returns NaN for every query of the chunk instead of reading keys from clamped pages."""
+    import math
+    from kvtier import _lib
+    from kvtier.kvt import PosTieredCache, kvt_prefill_attn
+    ring, n_pages = 8192, 8200
+    L = 8192 * 64 + ring + 128                          # hot_start = 524,416: 8,194 pages below the ring
+    dc = PosTieredCache(1, H, D, n_pages=n_pages, ring_total=ring, max_seqs=1, max_pages=n_pages, device=dev,
+                        page_seed=3)
+    dc.add_seq(ring)
+    g = torch.Generator(device=dev).manual_seed(3)
+    k = torch.randn(ring, H, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(ring, H, D, device=dev, generator=g).to(torch.bfloat16)
+    done = 0
+    while done < L:
+        n = min(ring, L - done)
+        plan = dc.plan_append([0], [n])
+        dc.append(0, plan, k[:n], v[:n])
+        dc.commit(plan)
+        done += n
+    assert dc.hot_start(0) > 8192 * 64
+    nq = 16
+    q = (torch.randn(nq, HQ, D, device=dev, generator=g) / 16).to(torch.bfloat16)
+    cu = torch.tensor([0, nq], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        kvt_prefill_attn(dc, 0, q, cu, max_q=nq)
+    out = torch.zeros(nq, HQ, D, dtype=torch.float32, device=dev)
+    _lib.call("kvt_prefill_attn", q.data_ptr(), q.stride(0), q.stride(1), cu.data_ptr(), 0, dc.seq_lens.data_ptr(),
+              1, nq, H, HQ, D, dc.group8, dc.k4[0].data_ptr(), dc.v4[0].data_ptr(), dc.ks4[0].data_ptr(),
+              dc.vs4[0].data_ptr(), dc.rk[0].data_ptr(), dc.rv[0].data_ptr(), dc.rks[0].data_ptr(),
+              dc.rvs[0].data_ptr(), dc.ring_base.data_ptr(), dc.ring_len.data_ptr(), dc.ring_start.data_ptr(),
+              dc.page_table.data_ptr(), dc.page_table.stride(0), dc.k4[0].shape[0], None, None, 0, 0, 0, 0, 0,
+              1.0 / math.sqrt(D), out.data_ptr(), 1, out.stride(0), out.stride(1), 0, None, 0, _lib.stream())
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all()
+
+
+def test_prefill_spread_workspace_reuse(kvt_pkg):
+    """One spread workspace used by a launch of few query tiles, then by one of many: the second result equals the
+    same launch on a fresh zeroed workspace, bit for bit, and the oracle.  (With a counter area sized per call, the
+    first launch's slot data sat where the second launch's counters are, and the second merged pieces early.)"""
+    import ctypes
+    from kvtier import _lib
+    from kvtier.kvt import kvt_prefill_attn
+
+    def work_bytes(max_q):
+        b = ctypes.c_int64(0)
+        _lib.call("kvt_prefill_work_bytes", 1, H, HQ, max_q, 256, ctypes.byref(b))
+        return b.value
+
+    for a, n, xk, xv, dc, oc, gen in _chunked([1024, 1024], 512, seed=61):
+        if a == 0:
+            continue
+        q = ref.make_q(HQ, D, gen, n=n)
+        kk, vv = oc.rows(0)
+        L = kk.shape[0]
+        small = torch.tensor([0, 96], dtype=torch.int32, device=dev)
+        full = torch.tensor([0, n], dtype=torch.int32, device=dev)
+        kv_small = torch.tensor([L - n + 96], dtype=torch.int32, device=dev)   # the chunk's first 96 queries
+        need = max(work_bytes(n), work_bytes(96))
+        shared = torch.zeros(need, dtype=torch.uint8, device=dev)
+        q_dev = q.to(dev)
+        kvt_prefill_attn(dc, 0, q_dev[:96], small, kv_lens=kv_small, max_q=96, out_dtype=torch.float32, spread=256,
+                         work=shared)
+        got = kvt_prefill_attn(dc, 0, q_dev, full, max_q=n, out_dtype=torch.float32, spread=256, work=shared)
+        fresh = kvt_prefill_attn(dc, 0, q_dev, full, max_q=n, out_dtype=torch.float32, spread=256,
+                                 work=torch.zeros(need, dtype=torch.uint8, device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(got, fresh)
+        exp = _oracle_chunk(q[-64:], L - 64, kk, vv)
+        err = (got[-64:].cpu() - exp).abs()
+        assert float(err.max()) < 2e-3 and float(err.mean()) < 1e-3
