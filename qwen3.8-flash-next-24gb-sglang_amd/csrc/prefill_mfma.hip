@@ -631,7 +631,9 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
     const int64_t need = (min((int64_t)T.hs, key_end) + kPage - 1) / kPage;
     pages_fit = need <= kMaxLdsPages;
     const int64_t npg = min(need, (int64_t)kMaxLdsPages);
-    for (int64_t i = tid; i < npg; i += 64 * kWaves) lds.pages[i] = S.page_table[b * S.pt_stride + i];
+    // (through a buffer resource over the sequence's row: 32-bit lane offsets, no per-lane 64-bit address kept live)
+    const Rsrc pt = make_rsrc(S.page_table + b * S.pt_stride, (uint32_t)npg * 4u);
+    for (int i = tid; i < (int)npg; i += 64 * kWaves) lds.pages[i] = (int32_t)ld32(pt, 4u * (uint32_t)i);
     if (tid == 0 && npg == 0) lds.pages[0] = 0;
   }
   __syncthreads();
@@ -653,7 +655,9 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
   // scores give NaN weights, sums and outputs), never silently wrong keys
   const float qmul = pages_fit ? scale * kLog2e : __builtin_nanf("");
   {
-    const int rq = n16 / gs, hq = n16 - rq * gs;
+    int gs_q = gs;                      // (computed per segment, not hoisted to the kernel start: see the output)
+    asm volatile("" : "+s"(gs_q));
+    const int rq = n16 / gs_q, hq = n16 - rq * gs_q;
     const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
     const bool ok = rq < qpw && qi < q_len;
     qpos = q_pos0 + qi;
@@ -847,8 +851,11 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
 #pragma unroll
   for (int i = 0; i < 4; ++i) lrow[i] = __shfl(l, 4 * kb + i, 64);
   if (nseg > 1) {   // ---- publish this segment's state, or merge every segment's if it is the last
+    // (lane-derived slot offsets computed here, not hoisted to the kernel start and kept live across the loops)
+    int wave_t = wave, n16_t = n16;
+    asm volatile("" : "+s"(wave_t), "+v"(n16_t));
     const Rsrc rs = make_rsrc(slots, (uint32_t)nseg * kSlotFloats * 4u);
-    const uint32_t olane = (uint32_t)(wave * 16 * 64 + lane) * 16u;   // + 1024 c: this lane's O of column block c
+    const uint32_t olane = (uint32_t)(wave_t * 16 * 64 + lane) * 16u;   // + 1024 c: this lane's O of column block c
     if (tid == 0) lds.flag = ld_dev_i32(count) == nseg - 1;   // every other segment is in: merge at once
     __syncthreads();
     if (lds.flag == 0) {
@@ -858,8 +865,8 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(v4i, acc[c]), rs, (int)(mine + olane + 1024u * c),
                                                0, kSc1);
       if (kb == 0) {
-        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave + n16)], m_run);
-        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave + n16) + 1], l);
+        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave_t + n16_t)], m_run);
+        st_dev(&slots[ord * kSlotFloats + kSlotO + 2 * (16 * wave_t + n16_t) + 1], l);
       }
       drain();          // the stores have reached the coherence point
       __syncthreads();  // (and every thread has read lds.flag)
@@ -878,7 +885,7 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
       M[i] = -INFINITY;
       Ls[i] = 0.f;
     }
-    const int mlrow = kSlotO + 2 * (16 * wave + 4 * kb);
+    const int mlrow = kSlotO + 2 * (16 * wave_t + 4 * kb);
     if (nseg == 2) {   // (the common case) every load of the other segment at once
       const int oth = 1 - ord;
       float mx[4], lx[4];
@@ -953,19 +960,25 @@ KVT_DEV void attend_segment(const KVSrc& S, const uint16_t* q, int64_t sq_n, int
   // ---- normalize and store: accumulator row r = 4 kb + i = query qt0 + qpw wave + r / gs, head r % gs;
   // column n16 of block c = dim 16 c + n16
   // (one correctly rounded division per row: 128 / l, exact for a single visible key, where l = 1)
+  // The rows' (query, head) split is computed here, after the key tiles: gs passes through an empty asm statement,
+  // so the compiler cannot hoist these divisions to the kernel start, where their results stayed live across every
+  // loop and spilled.
+  int gs_t = gs;
+  void* out_t = out;
+  asm volatile("" : "+s"(gs_t), "+s"(out_t));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = 4 * kb + i, rq = r / gs, hq = r - rq * gs;
+    const int r = 4 * kb + i, rq = r / gs_t, hq = r - rq * gs_t;
     const int64_t qi = qt0 + (int64_t)qpw * wave + rq;
     if (rq < qpw && qi < q_len) {
-      const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs + hq) * so_h;
+      const int64_t o0 = (qs + qi) * so_n + (int64_t)(h * gs_t + hq) * so_h;
       const float rl = 128.0f / lrow[i];
       if (out_f32) {
-        float* orow = reinterpret_cast<float*>(out) + o0;
+        float* orow = reinterpret_cast<float*>(out_t) + o0;
 #pragma unroll
         for (int c = 0; c < 16; ++c) orow[16 * c + n16] = acc[c][i] * rl;
       } else {
-        uint16_t* orow = reinterpret_cast<uint16_t*>(out) + o0;
+        uint16_t* orow = reinterpret_cast<uint16_t*>(out_t) + o0;
 #pragma unroll
         for (int c = 0; c < 16; ++c) orow[16 * c + n16] = bf16_rne(acc[c][i] * rl);
       }
