@@ -519,9 +519,10 @@ def sparse_workload(args) -> dict:
     """Top-k sparse decode over the tiered (slot-indexed) pool: 8 requests of 65,536 tokens on randomly allocated
     slots, 12 layers, 2,051 selected positions per request (distinct, random), INT8-G64 ring of 8,192 rows whose
     owner table names one slot per row; args.hq query heads over 2 KV heads (16, or 24 as the served model).
-    Times one HIP graph of the 12 layers' fused top-k decode (split-K + combine) and, for scale, one of the 12
-    layers' gathers into the bf16 scratch alone (the reference's unfused path runs an attention over that scratch on
-    top).  Byte model per layer: each selected position's K and V rows of both KV heads from the tier that serves
+    Times one HIP graph of the 12 layers' fused top-k decode (split-K + combine: 33 splits per request and KV
+    head; the same with the splits merged inside the launch beside it, slower at this split count) and, for scale,
+    one of the 12 layers' gathers into the bf16 scratch alone (the reference's unfused path runs an attention over
+    that scratch on top).  Byte model per layer: each selected position's K and V rows of both KV heads from the tier that serves
     it (codes + fp16 scales), plus the index entry, its req_to_token slot and the ring owner probe (4 B each).
     Synthetic random codes and scales."""
     hq = getattr(args, "hq", HQ)
@@ -566,12 +567,12 @@ def sparse_workload(args) -> dict:
     n_cold = hot.numel() - n_hot
     bytes_layer = H * 2 * (n_hot * (D + 2 * (D // 64)) + n_cold * (D // 2 + 2 * (D // 32))) + 3 * 4 * hot.numel()
 
-    def fused():
+    def fused(merge="auto"):
         for layer in range(LAYERS):
             pl = pools[layer]
             sa.qwen_sparse_decode_attn(q[layer], pl["k4"], pl["v4"], r2t, req_idx, idx, seq_lens, cu_k, B, TOPK,
                                        pl["ks4"], pl["vs4"], sm, sm, 4, pl["rk"], pl["rv"], pl["rks"], pl["rvs"],
-                                       owner, R - 1, out=outs[layer], workspace=ws[layer])
+                                       owner, R - 1, out=outs[layer], workspace=ws[layer], merge=merge)
 
     def gather():
         for layer in range(LAYERS):
@@ -584,6 +585,7 @@ def sparse_workload(args) -> dict:
         return _graph_time(fn, args.warmup, args.steps)
 
     t_fused = graph_time(fused)
+    t_in = graph_time(lambda: fused("launch"))
     t_gather = graph_time(gather)
     gbps = bytes_layer * LAYERS / t_fused / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline_sparse(pools[0], owner, r2t, idx, q[0], R, sm)
@@ -594,6 +596,7 @@ def sparse_workload(args) -> dict:
         "config": {"workload": f"8 requests x 65,536 tokens on random slots, 12 layers, {hq} Q / 2 KV heads, D 256, "
                                "2,051 selected positions each, tiered pool (INT8-G64 ring of 8,192 rows + INT4-G32)",
                    "hot_fraction": round(n_hot / hot.numel(), 4)},
+        "merged_in_launch_us_per_step": round(t_in * 1e6, 1),
         "gather_only_us_per_step": round(t_gather * 1e6, 1),
         "gather_tier_ratio": gather_tier_ratio(args),
         "kv_bytes_per_layer": bytes_layer,
@@ -1044,6 +1047,21 @@ def decode_steps_workload(args, ragged: bool) -> dict:
     d1.record()
     torch.cuda.synchronize()
     dec_graph = d0.elapsed_time(d1) / 1e3 / 20
+    # the same decode 12 times in one graph (the 1-layer workload only): device time per decode without the cost of
+    # launching a graph per decode
+    dec_b2b = None
+    if layers == 1:
+        bgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(bgraph):
+            for _ in range(12):
+                dec_only()
+        _settle(bgraph.replay)
+        d0.record()
+        for _ in range(20):
+            bgraph.replay()
+        d1.record()
+        torch.cuda.synchronize()
+        dec_b2b = d0.elapsed_time(d1) / 1e3 / (20 * 12)
     name = ("ragged decode: 8 sequences, 12 layers, shared 4,096-token prefix, 256 iterations" if ragged
             else "decode with append: 10,001-token context, 1 layer, 1,000 steps")
     return {
@@ -1059,6 +1077,7 @@ def decode_steps_workload(args, ragged: bool) -> dict:
         "kv_bytes_per_step": int(kv_avg),
         "decode_graph_us_per_step": round(dec_graph * 1e6, 1),
         "decode_graph_kv_GBps": round(kv_last / dec_graph / 1e9, 1),
+        "decode_back_to_back_us": None if dec_b2b is None else round(dec_b2b * 1e6, 1),
     }
 
 
@@ -1083,7 +1102,8 @@ def sub_configs(args) -> dict:
     def pick_steps(r):
         return {"us_per_step": r["value"], "device_us_per_step": r["device_us_per_step"],
                 "kv_GBps": r["kv_GBps_per_step"], "decode_graph_us_per_step": r["decode_graph_us_per_step"],
-                "decode_graph_kv_GBps": r["decode_graph_kv_GBps"]}
+                "decode_graph_kv_GBps": r["decode_graph_kv_GBps"],
+                "decode_back_to_back_us": r["decode_back_to_back_us"]}
 
     def pick_sparse(r):
         return {"us_per_step": r["value"], "GBps": r["roofline"]["achieved"], "hbm_frac": r["roofline"]["frac"],

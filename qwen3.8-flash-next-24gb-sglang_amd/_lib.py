@@ -40,7 +40,7 @@ SIGNATURES = {
     "kvt_compact_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L, _P, _P, _I,
                            _I, _I, _I, _I, _I, _P, _P, _P],
     "kvt_sparse_decode": [_I, _P, _L, _P, _P, _P, _P, _L, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _L,
-                          _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P],
+                          _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _P, _P, _L, _P],
     "kvt_sparse_prefill": [_I, _P, _L, _L, _P, _I, _P, _I, _I, _P, _L, _L, _L, _I, _P, _P, _P, _P, _L, _P, _P, _P,
                            _P, _P, _L, _P, _P, _P, _L, _P, _I, _I, _I, _I, _I, _F, _P, _I, _L, _L, _P],
     "kvt_prefix_gather": [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _P, _P, _P, _L, _P, _I, _P, _P, _I, _I, _L,

@@ -81,6 +81,10 @@ struct SparseArgs {
   int64_t si_m, si_g, si_n;  // indices of row r, KV head h, column c at indices + r si_m + h si_g + c si_n
   float* part_o;           // decode: [(b H + h) n_splits + split][gs][D]
   float* part_ml;          // decode: [(b H + h) n_splits + split][gs][2]
+  int32_t* counters;       // decode, merged in the launch: [b H + h] arrivals (zero between calls); null: partials only
+  float* mout_f32;         // decode, merged in the launch: out[b][h gs + j][D] fp32 or bf16, batch stride mout_b
+  uint16_t* mout_bf16;
+  int64_t mout_b;
   // prefill rows: chunk b holds rows cu_q[b] .. cu_q[b + 1] over a context of kv_lens[b] positions
   const void* cu_q;
   int cuq64;
@@ -346,6 +350,7 @@ struct BlockLds {
   uint16_t qs[kHeads * kKPitch];
   uint2 cols[CAP];             // prefill rows: the query's resolved columns, ring rows first and INT4 rows last
   int counts[2 * kWaves];
+  int last;                    // decode merged in the launch: this block counted last for its (request, KV head)
 };
 constexpr int kRowCols = 4096;   // prefill rows: selected columns resolved per pass (74 KB of LDS per block)
 constexpr int kMultiCols = 1024; // decode blocks of several tiles per wavefront (50 KB of LDS per block)
@@ -436,6 +441,98 @@ KVT_DEV TileCols table_tile(const BlockLds<CAP>& S, int t, int th, int nh, int n
 
 // ROWS: prefill rows (one query row per block) instead of decode splits; MULTI: a decode block of several tiles per
 // wavefront; CAP > 1: the block resolves its columns into a column table of CAP entries partitioned by tier first.
+// Device-scope stores and loads of the split partials when the launch merges them itself: the partials cross XCDs
+// (each has its own L2), so they are written through to the coherence point and read past the reader's L2 (cache
+// policy sc1 on the raw buffer accesses).
+typedef unsigned int u4v __attribute__((vector_size(16)));   // the raw buffer builtins' 16- and 8-byte operands
+typedef unsigned int u2v __attribute__((vector_size(8)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+constexpr int kSc1 = 16;
+KVT_DEV void wait_vm0() {   // s_waitcnt vmcnt(0), the other counters untouched
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+// The partials of (request b, KV head h): n_splits x gs rows of D floats, then n_splits x gs (m, l) pairs.
+KVT_DEV __amdgpu_buffer_rsrc_t part_o_rsrc(const SparseArgs& A, int64_t bh) {
+  const int64_t rows = (int64_t)A.n_splits * A.gs;
+  return rsrc(A.part_o + bh * rows * kD, (uint32_t)(rows * kD * 4));
+}
+KVT_DEV __amdgpu_buffer_rsrc_t part_ml_rsrc(const SparseArgs& A, int64_t bh) {
+  const int64_t rows = (int64_t)A.n_splits * A.gs;
+  return rsrc(A.part_ml + bh * rows * 2, (uint32_t)(rows * 8));
+}
+
+// The split merge inside the decode launch: after its partial's device-scope stores have completed, a block counts
+// itself on its (request, KV head) counter; the block that counts last resets the counter for the next call and
+// merges the n_splits partials in split order (so the result does not depend on which block is last), as
+// kvt_decode_combine does for a separate launch: (m, num, den) <- (max(m, m_s), num e^(m - m') + o_s e^(m_s - m'),
+// den e^(m - m') + l_s e^(m_s - m')), out = num / den (0 / 0 = NaN when no column was attended).  No block waits for
+// another.  Thread t merges q head t / 16, dims 16 (t % 16) .. + 15, with the loads of 4 splits in flight at once.
+template <int CAP>
+KVT_DEV void merge_last(const SparseArgs& A, BlockLds<CAP>& S, int b, int h) {
+  wait_vm0();
+  __syncthreads();   // every thread's partial stores have completed
+  const int64_t bh = (int64_t)b * A.H + h;
+  if (threadIdx.x == 0)
+    S.last = __hip_atomic_fetch_add(&A.counters[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == A.n_splits - 1;
+  __syncthreads();
+  if (!S.last) return;
+  if (threadIdx.x == 0) __hip_atomic_store(&A.counters[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  constexpr float kL2e = 1.4426950408889634f;
+  constexpr int kB = 4;
+  const int gs = A.gs, ns = A.n_splits;
+  const int hq = (int)(threadIdx.x >> 4), c0 = 16 * (int)(threadIdx.x & 15);
+  if (hq >= gs) return;
+  const auto ro = part_o_rsrc(A, bh), rml = part_ml_rsrc(A, bh);
+  float m = -INFINITY, den = 0.f, num[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) num[i] = 0.f;
+  for (int s0 = 0; s0 < ns; s0 += kB) {
+    f4 o[kB][4];
+    f2 ml[kB];
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const int s = s0 + k < ns ? s0 + k : s0;
+      const int row = s * gs + hq;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[k][j] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(ro, (row * kD + c0 + 4 * j) * 4, 0,
+                                                                                kSc1));
+      ml[k] = __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(rml, row * 8, 0, kSc1));
+    }
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      if (s0 + k >= ns) break;
+      const float ms = ml[k][0], ls = ml[k][1];
+      const float mn = fmaxf(m, ms);
+      if (mn == -INFINITY) continue;   // both empty
+      const float a = __builtin_amdgcn_exp2f((m - mn) * kL2e), c = __builtin_amdgcn_exp2f((ms - mn) * kL2e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) num[4 * j + i] = num[4 * j + i] * a + o[k][j][i] * c;
+      den = den * a + ls * c;
+      m = mn;
+    }
+  }
+  const int64_t off = (int64_t)b * A.mout_b + (int64_t)(h * gs + hq) * kD + c0;
+  if (A.mout_f32 != nullptr) {
+    float* dst = A.mout_f32 + off;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<float4*>(dst + 4 * j) =
+          float4{num[4 * j] / den, num[4 * j + 1] / den, num[4 * j + 2] / den, num[4 * j + 3] / den};
+  } else {
+    uint16_t* dst = A.mout_bf16 + off;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<uint4*>(dst + 8 * j) =
+          uint4{bf16x2(num[8 * j] / den, num[8 * j + 1] / den), bf16x2(num[8 * j + 2] / den, num[8 * j + 3] / den),
+                bf16x2(num[8 * j + 4] / den, num[8 * j + 5] / den), bf16x2(num[8 * j + 6] / den, num[8 * j + 7] / den)};
+  }
+}
+
 template <int KIND, int G8, bool ROWS, bool MULTI, int CAP>
 KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   auto& kv = S.kv;
@@ -604,15 +701,31 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
       } else {
         const int64_t item = ((int64_t)b * H + h) * A.n_splits + blockIdx.x;
         float* dst = A.part_o + (item * gs + hq) * kD + c0;
-        *reinterpret_cast<float4*>(dst) = float4{acc[0], acc[1], acc[2], acc[3]};
-        *reinterpret_cast<float4*>(dst + 4) = float4{acc[4], acc[5], acc[6], acc[7]};
-        if (c0 == 0) {   // (m, l) of the block's partial, m in natural-log units
-          constexpr float kLn2 = 0.6931471805599453f;
-          A.part_ml[(item * gs + hq) * 2 + 0] = M == -INFINITY ? -INFINITY : M * kLn2;
-          A.part_ml[(item * gs + hq) * 2 + 1] = lt;
+        constexpr float kLn2 = 0.6931471805599453f;
+        const float mnat = M == -INFINITY ? -INFINITY : M * kLn2;   // m of the block's partial in natural-log units
+        if (A.counters == nullptr) {   // read by the combine kernel after the launch
+          *reinterpret_cast<float4*>(dst) = float4{acc[0], acc[1], acc[2], acc[3]};
+          *reinterpret_cast<float4*>(dst + 4) = float4{acc[4], acc[5], acc[6], acc[7]};
+          if (c0 == 0) {
+            A.part_ml[(item * gs + hq) * 2 + 0] = mnat;
+            A.part_ml[(item * gs + hq) * 2 + 1] = lt;
+          }
+        } else {                       // read by another block of this launch, maybe on another XCD: device scope
+          const int row = (int)blockIdx.x * gs + hq;
+          const auto ro = part_o_rsrc(A, (int64_t)b * H + h);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f4{acc[0], acc[1], acc[2], acc[3]}), ro,
+                                                 (row * kD + c0) * 4, 0, kSc1);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f4{acc[4], acc[5], acc[6], acc[7]}), ro,
+                                                 (row * kD + c0 + 4) * 4, 0, kSc1);
+          if (c0 == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, f2{mnat, lt}),
+                                                  part_ml_rsrc(A, (int64_t)b * H + h), row * 8, 0, kSc1);
         }
       }
     }
+  }
+  if constexpr (!ROWS) {
+    if (A.counters != nullptr) merge_last(A, S, b, h);
   }
 }
 
@@ -694,8 +807,13 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
                       const void* req_to_token, int64_t req_stride, const void* req_indices, int req_is_int64,
                       const void* indices, int64_t idx_stride, const void* seq_lens, const void* cu_k,
                       int cu_is_int64, int batch, int topk, int H, int Hq, int D, int group8, float scale,
-                      int n_splits, void* part_o, void* part_ml, void* stream) {
+                      int n_splits, void* part_o, void* part_ml, void* counters, void* out_f32, void* out_bf16,
+                      int64_t out_stride_b, void* stream) {
   if (batch <= 0 || topk <= 0 || n_splits <= 0) return KVT_EINVAL;
+  if (counters != nullptr && ((out_f32 == nullptr) == (out_bf16 == nullptr) || out_stride_b < (int64_t)Hq * D ||
+                              ((uintptr_t)(out_f32 != nullptr ? out_f32 : out_bf16) & 15) != 0 ||
+                              (out_stride_b & 7) != 0 || (int64_t)n_splits * (Hq / (H > 0 ? H : 1)) * D * 4 >= (1ll << 31)))
+    return KVT_EINVAL;   // merged in the launch: one (request, KV head)'s partials addressed with 32-bit offsets
   // n_splits blocks per (request, KV head) cover the topk columns with `tiles` 16-column tiles per wavefront
   const int tiles64 = (topk + kCols - 1) / kCols;
   const int tiles = (tiles64 + n_splits - 1) / n_splits;
@@ -714,6 +832,8 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
   A.H = H, A.gs = Hq / H, A.n_splits = n_splits, A.tiles = tiles, A.rows8 = (uint32_t)rows8;
   A.rows4 = (uint32_t)rows4, A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = q_stride_b, A.sq_h = kD;
   A.si_m = idx_stride, A.si_g = 0, A.si_n = 1, A.part_o = (float*)part_o, A.part_ml = (float*)part_ml;
+  A.counters = (int32_t*)counters, A.mout_f32 = (float*)out_f32, A.mout_bf16 = (uint16_t*)out_bf16;
+  A.mout_b = out_stride_b;
   return launch<false>(kind, group8, dim3((unsigned)n_splits, (unsigned)(batch * H)), (hipStream_t)stream, A);
 }
 

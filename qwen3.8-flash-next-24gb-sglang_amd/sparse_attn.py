@@ -220,11 +220,16 @@ def qwen_sparse_decode_attn(
     q, k, v, req_to_token, req_indices, indices, seq_lens, cu_k, batch, topk,
     k_scale=None, v_scale=None, sm_k=None, sm_v=None, kv_bits=None,
     ring_k=None, ring_v=None, ring_ks=None, ring_vs=None, owner=None, ring_mask=None,
-    scale=None, out=None, workspace=None, splits=None,
+    scale=None, out=None, workspace=None, splits=None, merge="auto",
 ):
     """Top-k sparse decode attention fused over the quantized pool: what qwen_sparse_kv_extraction_compact_triton
     followed by FlashAttention-2 over its bf16 scratch computes for one query row per request (flat patch
-    sglang/qwen4exp-serving-73a255206f.patch:1832-1882), in one split-K launch + the combine, with no scratch.
+    sglang/qwen4exp-serving-73a255206f.patch:1832-1882), in one split-K launch, with no scratch.  merge="launch": the
+    block of a (request, KV head) that finishes last merges the column splits inside the launch (counters in the
+    workspace: calls sharing a workspace must not overlap); merge="combine": the splits go through
+    kvt_decode_combine, a second launch; merge="auto" (default): in the launch for at most 8 splits per (request, KV
+    head), where it is the faster of the two (one block then reads at most 8 partials of up to 16 x 1 KB), else the
+    combine launch, whose blocks (one per request, q head and slice of dims) read the partials side by side.
 
     q: bf16 [batch, Hq, D]; the pool/ring/owner/scale arguments as the compact gather; cu_k: the valid counts'
     prefix sum (qwen_sparse_fa2_cu_seqlens_triton).  Column c of request b is attended when c < cu_k[b+1] - cu_k[b]
@@ -280,6 +285,13 @@ def qwen_sparse_decode_attn(
     if ws.get("sparse_o") is None or ws["sparse_o"].numel() < need * dim:
         ws["sparse_o"] = torch.empty(need * dim, dtype=torch.float32, device=q.device)
         ws["sparse_ml"] = torch.empty(need * 2, dtype=torch.float32, device=q.device)
+    if merge not in ("auto", "launch", "combine"):
+        raise ValueError(f"merge must be 'auto', 'launch' or 'combine', not {merge!r}")
+    fused = merge == "launch" or (merge == "auto" and n_splits <= 8)
+    if fused and (ws.get("sparse_ctr") is None or ws["sparse_ctr"].numel() < batch * heads):
+        ws["sparse_ctr"] = torch.zeros(batch * heads, dtype=torch.int32, device=q.device)   # each call leaves 0
+    if fused:
+        assert out.stride(0) % 8 == 0 and out.data_ptr() % 16 == 0
     rq, rq64 = _idx_args(req_indices)
     cu, cu64 = _idx_args(cu_k)
     tier = kind == _KIND_TIERED
@@ -292,7 +304,11 @@ def qwen_sparse_decode_attn(
               _lib.ptr(owner) if tier else None, R - 1, _lib.ptr(smk), _lib.ptr(smv), req_to_token.data_ptr(),
               req_to_token.stride(0), rq, rq64, indices.data_ptr(), indices.stride(0), seq_lens.data_ptr(), cu, cu64,
               int(batch), int(topk), heads, Hq, dim, g8, scale, n_splits, ws["sparse_o"].data_ptr(),
-              ws["sparse_ml"].data_ptr(), st)
+              ws["sparse_ml"].data_ptr(), ws["sparse_ctr"].data_ptr() if fused else None,
+              out.data_ptr() if fused and out.dtype == torch.float32 else None,
+              out.data_ptr() if fused and out.dtype == torch.bfloat16 else None, out.stride(0), st)
+    if fused:
+        return out
     o32 = out.data_ptr() if out.dtype == torch.float32 else None
     o16 = out.data_ptr() if out.dtype == torch.bfloat16 else None
     _lib.call("kvt_decode_combine", ws["sparse_o"].data_ptr(), ws["sparse_ml"].data_ptr(), int(batch), heads, Hq, dim,

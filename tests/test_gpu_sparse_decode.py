@@ -186,3 +186,41 @@ def test_sparse_decode_gqa12(kvt_pkg):
     for kind in ("tiered", "int8"):
         got = _call(kind, p, q, r2t, req_idx, idx, sl, cu_k, 3, 2051, R).cpu()
         _close(got, _oracle(kind, p, q, r2t, req_idx, idx, sl, cu_k, 2051, R, 64))
+
+
+def test_sparse_decode_merge_in_launch_against_combine(kvt_pkg):
+    """The split merge inside the launch (the last block of each (request, KV head) merges, counters left at zero)
+    against the separate combine launch, on one shared workspace: 3 requests, then 2 other requests with another
+    split count, then the first case again, fp32 and bf16 outputs; both within the oracle bound, and within 1e-5 of
+    each other (the same partials, merged in the same split order).  The default (merge="auto") takes the in-launch
+    merge for at most 8 splits: bit-identical to merge="launch" there."""
+    from kvtier import sparse_attn as sa
+    gen = torch.Generator().manual_seed(35)
+    slots, R = 4096, 64
+    p = _pools(slots, R, 64, gen)
+    d = {k: v.to(dev) for k, v in p.items()}
+    cases = []
+    for lens, topk in (([3000, 700, 9], 2051), ([1500, 2600], 1200)):
+        r2t, req_idx, idx, sl, cu_k = _case(gen, lens, topk, slots)
+        q = (torch.randn(len(lens), 24, D, generator=gen) / 4).to(torch.bfloat16)
+        cases.append((r2t, req_idx, idx, sl, cu_k, q, topk))
+    ws = {}
+    for ci, splits in ((0, None), (1, 5), (0, 7), (1, 1)):
+        r2t, req_idx, idx, sl, cu_k, q, topk = cases[ci]
+        batch = q.shape[0]
+        args = (q.to(dev), d["k4"], d["v4"], r2t.to(dev), req_idx.to(dev), idx.to(dev), sl.to(dev), cu_k.to(dev),
+                batch, topk, d["ks4"], d["vs4"], d["sm_k"], d["sm_v"], 4, d["rk"], d["rv"], d["rks"], d["rvs"],
+                d["owner"], R - 1)
+        fused = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=splits, merge="launch").cpu()
+        assert int(ws["sparse_ctr"].abs().sum()) == 0
+        sep = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=splits, merge="combine").cpu()
+        _close(fused, _oracle("tiered", p, q, r2t, req_idx, idx, sl, cu_k, topk, R, 64))
+        assert float((fused - sep).abs().max()) <= 1e-5
+        o16 = torch.empty(batch, 24, D, dtype=torch.bfloat16, device=dev)
+        f16 = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=splits, out=o16,
+                                         merge="launch").cpu()
+        assert float((f16.float() - fused).abs().max()) <= 2 ** -8 * float(fused.abs().max())
+        auto = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=splits).cpu()
+        assert torch.equal(auto, fused if (splits or 33) <= 8 else sep)
+    with pytest.raises(ValueError):
+        sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, merge="fold")
