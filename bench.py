@@ -192,18 +192,31 @@ def pmc_sample(impl: str) -> None:
         for layer in range(LAYERS):
             kvt_decode_attn(cache, layer, q[layer], out=out, impl=impl, workspace=ws, plan=plan, check_q=False)
         torch.cuda.synchronize()
+    calibration_copy()
+    print(json.dumps({"pmc_sample": impl, "kv_bytes_per_layer": cache.kv_bytes(), "cal_bytes": CAL_BYTES}))
+
+
+def calibration_copy() -> None:
+    """One device copy of CAL_BYTES, whose counter reading calibrates FETCH_SIZE / WRITE_SIZE."""
     src = torch.empty(CAL_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_sample": impl, "kv_bytes_per_layer": cache.kv_bytes(), "cal_bytes": CAL_BYTES}))
 
 
-def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, impl: str) -> None:
+DECODE_KERNELS = ("decode_rows_kernel", "decode_mfma_kernel", "decode_ref_kernel")
+
+
+def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, impl: str,
+                    kernels: str = "") -> None:
     """Average FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the decode kernel from two rocprofv3 --pmc counter
     CSVs, scaled by the ratio of the calibration copy's known bytes to its counter reading; also the median per
-    dispatch of the cache build's append launches, scaled the same way."""
+    dispatch of the cache build's append launches, scaled the same way.  `kernels` (comma-separated kernel-name
+    parts) measures those kernels instead: the average per dispatch of each, and their sum as bytes per launch
+    group (one layer of the top-k decode: split-K + combine)."""
+    if kernels:
+        return _traffic_of(fetch_csv, write_csv, out_json, out_txt, kernels.split(","))
     import csv
 
     def per_kernel(path, counter):
@@ -249,6 +262,51 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
     with open(out_txt, "a") as f:  # appended under the commands already written at the top of the file
         f.write("\n".join(lines) + "\n")
     print(json.dumps(res))
+
+
+def _traffic_of(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, names) -> None:
+    import csv
+
+    def per_kernel(path, counter):
+        acc = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") == counter:
+                    acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return acc
+
+    res, lines = {"kernels": list(names)}, []
+    for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
+        acc = per_kernel(path, counter)
+        cal = [v for k, v in acc.items() if "copy" in k.lower() and max(v) * 1024 > CAL_BYTES / 4]
+        assert cal, (counter, list(acc))
+        cal_kib = max(max(cal, key=max))
+        factor = CAL_BYTES / (cal_kib * 1024)
+        per, total = {}, 0
+        for name in names:
+            vals = [x for k, v in acc.items() if name in k for x in v]
+            assert vals, (counter, name, list(acc))
+            kib = sum(vals) / len(vals)
+            per[name] = round(kib * 1024 * factor)
+            total += per[name]
+            lines.append(f"{counter}: {name} {kib:.1f} KiB/dispatch over {len(vals)} dispatches; copy of {CAL_BYTES} "
+                         f"B {key}s {cal_kib:.1f} KiB -> factor {factor:.4f} -> {per[name]} B")
+        res[key] = {"factor": round(factor, 4), "bytes_per_dispatch": per, "bytes_per_launch": total}
+    res["hbm_bytes_per_launch"] = res["read"]["bytes_per_launch"] + res["write"]["bytes_per_launch"]
+    with open(out_json, "w") as f:
+        json.dump(res, f, indent=1)
+    with open(out_txt, "a") as f:
+        f.write("\n".join(lines) + "\n")
+    print(json.dumps(res))
+
+
+def _measured_traffic(name: str):
+    """HBM bytes per launch (group) from a committed profiles/<name>.json written by --traffic-summary, or None."""
+    path = os.path.join(ROOT, "profiles", name + ".json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["hbm_bytes_per_launch"]
 
 
 def _layer_kv(n: int, layer: int, seed: int):
@@ -584,6 +642,13 @@ def sparse_workload(args) -> dict:
     def graph_time(fn):
         return _graph_time(fn, args.warmup, args.steps)
 
+    if getattr(args, "pmc_sample", False):   # eager 12-layer steps under rocprofv3 --pmc, then the calibration copy
+        for _ in range(3):
+            fused()
+        torch.cuda.synchronize()
+        calibration_copy()
+        print(json.dumps({"pmc_sample": "sparse", "kv_bytes_per_layer": bytes_layer, "cal_bytes": CAL_BYTES}))
+        return None
     t_fused = graph_time(fused)
     t_in = graph_time(lambda: fused("launch"))
     t_gather = graph_time(gather)
@@ -601,7 +666,8 @@ def sparse_workload(args) -> dict:
         "gather_tier_ratio": gather_tier_ratio(args),
         "kv_bytes_per_layer": bytes_layer,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": round(gbps * 1e9 / PEAK_HBM, 4), "traffic": None,
+                     "frac": round(gbps * 1e9 / PEAK_HBM, 4),
+                     "traffic": _measured_traffic(f"sparse_topk2051_{hq}q_traffic"),
                      "kernel": "sparse_decode + combine (per layer)"},
         "cpu_baseline": cpu,
     }
@@ -740,6 +806,13 @@ def paged_prefix_workload(args) -> dict:
                                           pool["vs4"], sm_k, sm_v, D ** -0.5, CHUNK, 4, pool["rk"], pool["rv"],
                                           pool["rks"], pool["rvs"], owner, R - 1, out=out)
 
+    if getattr(args, "pmc_sample", False):   # eager calls under rocprofv3 --pmc, then the calibration copy
+        for _ in range(5):
+            call()
+        torch.cuda.synchronize()
+        calibration_copy()
+        print(json.dumps({"pmc_sample": "paged_prefix", "cal_bytes": CAL_BYTES}))
+        return None
     t_dev = _graph_time(call, args.warmup, max(args.steps, 10))
     host = []
     for _ in range(10):
@@ -790,8 +863,9 @@ def paged_prefix_workload(args) -> dict:
         "kv_bytes_per_call": kv_bytes,
         "TFLOPs": round(flops / t_dev / 1e12, 2),
         "roofline": {"bound": "hbm", "achieved": round(kv_bytes / t_dev / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(kv_bytes / t_dev / PEAK_HBM, 4), "traffic": None,
-                     "kernel": "sparse_prefill (row requests; the 35 MB pool itself stays in the caches)"},
+                     "unit": "GB/s", "frac": round(kv_bytes / t_dev / PEAK_HBM, 4),
+                     "traffic": _measured_traffic("paged_prefix_60k_traffic"),
+                     "kernel": "sparse_prefill (row requests; the 21.9 MB pool is re-read through the caches)"},
         "cpu_baseline": cpu,
     }
 
@@ -1145,9 +1219,14 @@ def main():
     ap.add_argument("--pmc-sample", action="store_true", help="run the rocprofv3 --pmc traffic sample and exit")
     ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON", "OUT_TXT"),
                     help="summarize two rocprofv3 --pmc counter CSVs into the traffic file and exit")
+    ap.add_argument("--traffic-kernels", default="",
+                    help="with --traffic-summary: comma-separated kernel-name parts to measure instead of the decode")
     args = ap.parse_args()
     if args.traffic_summary:
-        traffic_summary(*args.traffic_summary, impl=args.impl)
+        traffic_summary(*args.traffic_summary, impl=args.impl, kernels=args.traffic_kernels)
+        return
+    if args.pmc_sample and args.workload in ("sparse", "paged_prefix"):
+        (sparse_workload if args.workload == "sparse" else paged_prefix_workload)(args)
         return
     if args.pmc_sample:
         pmc_sample(args.impl)

@@ -439,8 +439,6 @@ KVT_DEV TileCols table_tile(const BlockLds<CAP>& S, int t, int th, int nh, int n
   return x;
 }
 
-// ROWS: prefill rows (one query row per block) instead of decode splits; MULTI: a decode block of several tiles per
-// wavefront; CAP > 1: the block resolves its columns into a column table of CAP entries partitioned by tier first.
 // Device-scope stores and loads of the split partials when the launch merges them itself: the partials cross XCDs
 // (each has its own L2), so they are written through to the coherence point and read past the reader's L2 (cache
 // policy sc1 on the raw buffer accesses).
@@ -533,6 +531,40 @@ KVT_DEV void merge_last(const SparseArgs& A, BlockLds<CAP>& S, int b, int h) {
   }
 }
 
+// XCD-aware work mapping.  The workgroups of a launch go to the 8 XCDs round robin by linear id, and each XCD has
+// its own L2, so the block with linear id L takes the work item that shares lines with the items of ids L +- 8:
+// * decode (grid n_splits x batch H): item i = b n_splits + split, in groups of 8 items whose H KV heads take ids
+//   8 H g + 8 h + (i % 8) -- the blocks of one (request, split) run on one XCD side by side and share the lines of
+//   the index, req_to_token and owner reads and of the rows' scales (both heads' scales sit in one 32-byte run);
+// * prefill rows (grid max_q x batch H): XCD x takes the x-th eighth of the (query, KV head) items, consecutive
+//   queries of one chunk, whose selections overlap.
+// A tail of fewer than 8 items (decode) or ids (rows) keeps a plain order.
+constexpr int kXcds = 8;
+template <bool ROWS>
+KVT_DEV void work_of_block(int H, int& wx, int& wy) {
+  const uint32_t nx = gridDim.x, n = nx * gridDim.y, L = blockIdx.x + blockIdx.y * nx;
+  if constexpr (ROWS) {
+    const uint32_t m = n / kXcds * kXcds;
+    const uint32_t w = L < m ? (L % kXcds) * (m / kXcds) + L / kXcds : L;
+    wx = (int)(w % nx), wy = (int)(w / nx);
+  } else {
+    const uint32_t T = n / (uint32_t)H, full = T / kXcds * kXcds, gh = kXcds * (uint32_t)H;
+    uint32_t i, hh;
+    if (L < full * (uint32_t)H) {
+      hh = (L % gh) / kXcds;
+      i = L / gh * kXcds + L % kXcds;
+    } else {
+      const uint32_t t = T - full, r = L - full * (uint32_t)H;
+      hh = r / t;
+      i = full + r % t;
+    }
+    const uint32_t b = i / nx;
+    wx = (int)(i - b * nx), wy = (int)(b * (uint32_t)H + hh);
+  }
+}
+
+// ROWS: prefill rows (one query row per block) instead of decode splits; MULTI: a decode block of several tiles per
+// wavefront; CAP > 1: the block resolves its columns into a column table of CAP entries partitioned by tier first.
 template <int KIND, int G8, bool ROWS, bool MULTI, int CAP>
 KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   auto& kv = S.kv;
@@ -540,13 +572,15 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int H = A.H, gs = A.gs;
-  const int b = blockIdx.y / H;
-  const int h = blockIdx.y - b * H;
+  int wx, wy;   // the work item: split (decode) or query (rows), and request / chunk x H + KV head
+  work_of_block<ROWS>(H, wx, wy);
+  const int b = wy / H;
+  const int h = wy - b * H;
   // the block's query row, context length and column range
   int64_t qrow, L, c_begin, c_end;
   if constexpr (ROWS) {
     const int64_t q0 = load_idx(A.cu_q, A.cuq64, b), q1 = load_idx(A.cu_q, A.cuq64, b + 1);
-    const int64_t j = blockIdx.x;
+    const int64_t j = wx;
     if (q0 + j >= q1) return;   // block-uniform: the chunk is shorter than the grid
     qrow = q0 + j;
     L = A.kv_lens[b];
@@ -558,7 +592,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
     L = A.seq_lens[b];
     const int64_t vcount = load_idx(A.cu_k, A.cu64, b + 1) - load_idx(A.cu_k, A.cu64, b);
     const int64_t span = (int64_t)kCols * (MULTI ? A.tiles : 1);
-    c_begin = (int64_t)blockIdx.x * span;
+    c_begin = (int64_t)wx * span;
     const int64_t lim = vcount < (int64_t)A.topk ? vcount : (int64_t)A.topk;
     c_end = c_begin + span < lim ? c_begin + span : lim;
   }
@@ -699,7 +733,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
                                                  bf16x2(acc[4] / lt, acc[5] / lt), bf16x2(acc[6] / lt, acc[7] / lt)};
         }
       } else {
-        const int64_t item = ((int64_t)b * H + h) * A.n_splits + blockIdx.x;
+        const int64_t item = ((int64_t)b * H + h) * A.n_splits + wx;
         float* dst = A.part_o + (item * gs + hq) * kD + c0;
         constexpr float kLn2 = 0.6931471805599453f;
         const float mnat = M == -INFINITY ? -INFINITY : M * kLn2;   // m of the block's partial in natural-log units
@@ -711,7 +745,7 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
             A.part_ml[(item * gs + hq) * 2 + 1] = lt;
           }
         } else {                       // read by another block of this launch, maybe on another XCD: device scope
-          const int row = (int)blockIdx.x * gs + hq;
+          const int row = wx * gs + hq;
           const auto ro = part_o_rsrc(A, (int64_t)b * H + h);
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, f4{acc[0], acc[1], acc[2], acc[3]}), ro,
                                                  (row * kD + c0) * 4, 0, kSc1);
