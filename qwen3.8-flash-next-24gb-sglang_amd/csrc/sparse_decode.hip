@@ -563,6 +563,30 @@ KVT_DEV void work_of_block(int H, int& wx, int& wy) {
   }
 }
 
+// The buffer resources of one tier (HOT: the INT8 tensors -- the ring when tiered --, else the INT4 pool), the
+// other tier's left empty.  A block with a column table builds them just before that tier's tiles: the pointers
+// pass through empty asm statements, so the compiler cannot hoist them to the kernel start and keep both tiers'
+// 8 descriptors (32 scalar registers) live through the tile loops.
+template <int KIND, int G8, bool HOT>
+KVT_DEV PoolRsrc tier_rsrc(const SparseArgs& A, int H) {
+  const void* pk = HOT && KIND == 2 ? (const void*)A.rk : A.k;
+  const void* pv = HOT && KIND == 2 ? (const void*)A.rv : A.v;
+  const void* pks = HOT && KIND == 2 ? (const void*)A.rks : (const void*)A.ks;
+  const void* pvs = HOT && KIND == 2 ? (const void*)A.rvs : (const void*)A.vs;
+  asm volatile("" : "+s"(pk), "+s"(pv), "+s"(pks), "+s"(pvs));
+  PoolRsrc P{};
+  if constexpr (HOT) {
+    const uint32_t n8 = A.rows8 * (uint32_t)H * kD, s8 = A.rows8 * (uint32_t)H * (kD / G8) * 2;
+    P.k8 = rsrc(pk, n8), P.v8 = rsrc(pv, n8), P.ks8 = rsrc(pks, s8), P.vs8 = rsrc(pvs, s8);
+    P.k4 = P.v4 = P.ks4 = P.vs4 = rsrc(nullptr, 0u);
+  } else {
+    const uint32_t n4 = A.rows4 * (uint32_t)H * (kD / 2), s4 = A.rows4 * (uint32_t)H * (kD / kG4) * 2;
+    P.k4 = rsrc(pk, n4), P.v4 = rsrc(pv, n4), P.ks4 = rsrc(pks, s4), P.vs4 = rsrc(pvs, s4);
+    P.k8 = P.v8 = P.ks8 = P.vs8 = rsrc(nullptr, 0u);
+  }
+  return P;
+}
+
 // ROWS: prefill rows (one query row per block) instead of decode splits; MULTI: a decode block of several tiles per
 // wavefront; CAP > 1: the block resolves its columns into a column table of CAP entries partitioned by tier first.
 template <int KIND, int G8, bool ROWS, bool MULTI, int CAP>
@@ -662,12 +686,18 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
         __syncthreads();
       }
       const int th = (nh + kRows - 1) / kRows, nt = th + (nc + kRows - 1) / kRows;
-      for (int t = wave; t < nt; t += kWaves) {
-        const TileCols tc = table_tile(S, t, th, nh, nc, lane);
-        if (t < th)
-          attend_tile<KIND, G8, kRowsInt8>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
-        else
-          attend_tile<KIND, G8, kRowsInt4>(A, P, qs, kv[wave], tc, lane, smk, smv, m_run, l_run, o, [](int) {});
+      int t = wave;
+      if constexpr (KIND != 1) {   // the ring (INT8) tiles, then the INT4 ones, each tier's descriptors in turn
+        const PoolRsrc P8 = tier_rsrc<KIND, G8, true>(A, H);
+        for (; t < th; t += kWaves)
+          attend_tile<KIND, G8, kRowsInt8>(A, P8, qs, kv[wave], table_tile(S, t, th, nh, nc, lane), lane, smk, smv,
+                                           m_run, l_run, o, [](int) {});
+      }
+      if constexpr (KIND != 0) {
+        const PoolRsrc P4 = tier_rsrc<KIND, G8, false>(A, H);
+        for (; t < nt; t += kWaves)
+          attend_tile<KIND, G8, kRowsInt4>(A, P4, qs, kv[wave], table_tile(S, t, th, nh, nc, lane), lane, smk, smv,
+                                           m_run, l_run, o, [](int) {});
       }
     }
   } else {   // at most one tile per wavefront (64 columns per block): no state is live across its loads

@@ -216,6 +216,9 @@ def qwen_sparse_kv_extraction_compact_triton(
               out_v.data_ptr(), _lib.stream())
 
 
+_MULTI_BLOCKS = 768   # blocks of a long-selection launch: one per resident slot, 3 per CU (50 KB of LDS, <= 168 VGPRs)
+
+
 def qwen_sparse_decode_attn(
     q, k, v, req_to_token, req_indices, indices, seq_lens, cu_k, batch, topk,
     k_scale=None, v_scale=None, sm_k=None, sm_v=None, kv_bits=None,
@@ -273,11 +276,11 @@ def qwen_sparse_decode_attn(
     _lib.require_device(q, k, v, req_to_token, indices, out)
     scale = float(dim ** -0.5) if scale is None else float(scale)
     # blocks of 64 selected columns (a 16-column tile per wavefront) while the launch holds at most 1,024 of them;
-    # longer selections take `tiles` tiles per wavefront in about one block per resident slot (2 per CU), each
+    # longer selections take `tiles` tiles per wavefront in about one block per resident slot (3 per CU), each
     # partial then covering 64 x tiles columns
     tiles64 = (int(topk) + 63) // 64
     blocks = batch * heads * tiles64
-    tiles = 1 if blocks <= 1024 else -(-blocks // 512)
+    tiles = 1 if blocks <= 1024 else -(-blocks // _MULTI_BLOCKS)
     n_splits = -(-tiles64 // tiles) if splits is None else int(splits)
     assert n_splits >= 1
     ws = workspace if workspace is not None else {}
