@@ -73,6 +73,32 @@ def test_device_plan_matches_host_plan(kvt_pkg):
     assert sorted(used) == sorted(order[:devc.alloc.next])
 
 
+def test_device_plan_many_sequences(kvt_pkg):
+    """80 sequences in one call (the plan kernel's scan over more than one wavefront) and 3 in another: chunked
+    appends, then single-token steps of all 80; both caches agree bit for bit after every call."""
+    rings = [64 << (i % 2) for i in range(80)]
+    host, devc = _pair(rings, n_pages=512, seed=5)
+    g = torch.Generator(device=dev).manual_seed(11)
+    chunk = [20 + (i * 7) % 44 for i in range(80)]   # at most one ring (64 rows) per append
+    layouts = [(list(range(80)), chunk), (list(range(80)), chunk), ([5, 79, 40], [64, 64, 1]),
+               (list(range(80)), [1] * 80)]
+    for step in range(14):
+        seqs, counts = layouts[min(step, 3)]
+        n = sum(counts)
+        k = torch.randn(n, H, D, device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn(n, H, D, device=dev, generator=g).to(torch.bfloat16)
+        hp = host.plan_append(seqs, counts)
+        host.append(0, hp, k, v)
+        host.commit(hp)
+        dp = devc.plan_device(seqs, counts)
+        devc.launch_plan(dp)
+        devc.append(0, dp, k, v)
+        devc.commit(dp)
+        torch.cuda.synchronize()
+        _same(host, devc)
+    assert int(devc.plan_status.item()) == 0
+
+
 def test_device_plan_graph_replay(kvt_pkg):
     """One decode step -- device plan (one token per sequence), append, decode -- captured once and replayed 300
     times with fresh inputs copied in between: the cache then equals the host planner's after the same 300 appends,
