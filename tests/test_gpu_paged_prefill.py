@@ -199,6 +199,19 @@ def test_paged_prefill_row_limit_is_visible(kvt_pkg):
                            _run(c, kind, p, R, idx=clean).view(torch.int16)), kind
 
 
+@pytest.mark.parametrize("kind", ["tiered", "int8"])
+def test_paged_prefill_long_selection(kvt_pkg, kind):
+    """Index rows of up to 5,000 entries over a 6,000-position prefix: a query's selection takes two passes of the
+    block's 4,096-entry column table (each pass runs the ring tiles, then the INT4 tiles); empty, single-position and
+    short rows among them."""
+    gen = torch.Generator().manual_seed(47)
+    slots, R = 8192, 1024
+    p = slot_pools(slots, R, 64, gen)
+    c = _case(gen, [6000], [40], slots, 16, topk=5000)
+    assert max(int((c["idx"][j] >= 0).sum()) for j in range(40)) > 4096
+    close(_run(c, kind, p, R, f32=True), _oracle(c, kind, p, R, 64))
+
+
 def test_paged_prefill_per_head_indices(kvt_pkg):
     """3-d indices [total_q, H, topk]: each KV head attends its own selection; topk 700 (< the prefix)."""
     gen = torch.Generator().manual_seed(44)
