@@ -217,23 +217,13 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
     group (one layer of the top-k decode: split-K + combine)."""
     if kernels:
         return _traffic_of(fetch_csv, write_csv, out_json, out_txt, kernels.split(","))
-    import csv
-
-    def per_kernel(path, counter):
-        acc = {}
-        with open(path) as f:
-            for row in csv.DictReader(f):
-                if row.get("Counter_Name") != counter:
-                    continue
-                acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
-        return acc
+    per_kernel = _pmc_per_kernel
 
     lines = []
     res = {"impl": impl}
     for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
         acc = per_kernel(path, counter)
-        dec = [v for k, v in acc.items()
-               if "decode_rows_kernel" in k or "decode_mfma_kernel" in k or "decode_ref_kernel" in k]
+        dec = [v for k, v in acc.items() if any(name in k for name in DECODE_KERNELS)]
         cal = [v for k, v in acc.items() if "copy" in k.lower() and max(v) * 1024 > CAL_BYTES / 4]
         assert dec and cal, (counter, list(acc))
         dec_v = [x for v in dec for x in v]
@@ -264,20 +254,21 @@ def traffic_summary(fetch_csv: str, write_csv: str, out_json: str, out_txt: str,
     print(json.dumps(res))
 
 
-def _traffic_of(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, names) -> None:
+def _pmc_per_kernel(path: str, counter: str) -> dict:
+    """Kernel name -> the counter's values per dispatch, from a rocprofv3 --pmc counter_collection CSV."""
     import csv
+    acc = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") == counter:
+                acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    return acc
 
-    def per_kernel(path, counter):
-        acc = {}
-        with open(path) as f:
-            for row in csv.DictReader(f):
-                if row.get("Counter_Name") == counter:
-                    acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
-        return acc
 
+def _traffic_of(fetch_csv: str, write_csv: str, out_json: str, out_txt: str, names) -> None:
     res, lines = {"kernels": list(names)}, []
     for counter, path, key in (("FETCH_SIZE", fetch_csv, "read"), ("WRITE_SIZE", write_csv, "write")):
-        acc = per_kernel(path, counter)
+        acc = _pmc_per_kernel(path, counter)
         cal = [v for k, v in acc.items() if "copy" in k.lower() and max(v) * 1024 > CAL_BYTES / 4]
         assert cal, (counter, list(acc))
         cal_kib = max(max(cal, key=max))
@@ -580,9 +571,9 @@ def sparse_workload(args) -> dict:
     Times one HIP graph of the 12 layers' fused top-k decode (split-K + combine: 33 splits per request and KV
     head; the same with the splits merged inside the launch beside it, slower at this split count) and, for scale,
     one of the 12 layers' gathers into the bf16 scratch alone (the reference's unfused path runs an attention over
-    that scratch on top).  Byte model per layer: each selected position's K and V rows of both KV heads from the tier that serves
-    it (codes + fp16 scales), plus the index entry, its req_to_token slot and the ring owner probe (4 B each).
-    Synthetic random codes and scales."""
+    that scratch on top).  Byte model per layer: each selected position's K and V rows of both KV heads from the tier
+    that serves it (codes + fp16 scales), plus the index entry, its req_to_token slot and the ring owner probe (4 B
+    each).  Synthetic random codes and scales."""
     hq = getattr(args, "hq", HQ)
     import kvtier  # noqa: F401
     from kvtier import sparse_attn as sa
