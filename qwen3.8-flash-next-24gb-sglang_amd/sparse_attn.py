@@ -290,11 +290,12 @@ def qwen_sparse_decode_attn(
         ws["sparse_ml"] = torch.empty(need * 2, dtype=torch.float32, device=q.device)
     if merge not in ("auto", "launch", "combine"):
         raise ValueError(f"merge must be 'auto', 'launch' or 'combine', not {merge!r}")
-    fused = merge == "launch" or (merge == "auto" and n_splits <= 8)
-    if fused and (ws.get("sparse_ctr") is None or ws["sparse_ctr"].numel() < batch * heads):
-        ws["sparse_ctr"] = torch.zeros(batch * heads, dtype=torch.int32, device=q.device)   # each call leaves 0
+    rows_ok = out.stride(0) % 8 == 0 and out.data_ptr() % 16 == 0   # the in-launch merge writes 16-byte pieces
+    fused = merge == "launch" or (merge == "auto" and n_splits <= 8 and rows_ok)
     if fused:
-        assert out.stride(0) % 8 == 0 and out.data_ptr() % 16 == 0
+        assert rows_ok, "merge='launch' needs out rows 16-byte aligned with a batch stride that is a multiple of 8"
+        if ws.get("sparse_ctr") is None or ws["sparse_ctr"].numel() < batch * heads:
+            ws["sparse_ctr"] = torch.zeros(batch * heads, dtype=torch.int32, device=q.device)   # each call leaves 0
     rq, rq64 = _idx_args(req_indices)
     cu, cu64 = _idx_args(cu_k)
     tier = kind == _KIND_TIERED

@@ -224,3 +224,13 @@ def test_sparse_decode_merge_in_launch_against_combine(kvt_pkg):
         assert torch.equal(auto, fused if (splits or 33) <= 8 else sep)
     with pytest.raises(ValueError):
         sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, merge="fold")
+    # output rows the in-launch merge cannot write (batch stride not a multiple of 8): the default takes the combine
+    # launch, an explicit merge="launch" is refused
+    batch = args[8]
+    wide = torch.full((batch, 24 * D + 4), float("nan"), dtype=torch.float32, device=dev)
+    odd = wide[:, :24 * D].view(batch, 24, D)
+    got = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=1, out=odd).cpu()
+    ref_ = sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=1, merge="combine").cpu()
+    assert torch.equal(got, ref_)
+    with pytest.raises(AssertionError):
+        sa.qwen_sparse_decode_attn(*args, scale=D ** -0.5, workspace=ws, splits=1, out=odd, merge="launch")
