@@ -245,3 +245,22 @@ def test_hybrid_forwarders_and_backend_kwargs(kvt_pkg, monkeypatch):
     bf = torch.zeros(4, 2, 256, dtype=torch.bfloat16)
     assert gp._int8_gather_kwargs(bf, lay) == {} and gp._kv_scratch_dtype(bf) == torch.bfloat16
     assert gp._kv_scratch_dtype(torch.zeros(4, 2, 256, dtype=torch.float16)) == torch.float16
+
+
+def test_sparse_decode_merge_arguments_refused(kvt_pkg):
+    """kvt_sparse_decode with merge counters refuses, before any launch, an output it cannot write: both or neither
+    output pointer, a batch stride below Hq x D or not a multiple of 8, an output not 16-byte aligned, and partials of
+    one (request, KV head) that 32-bit offsets cannot address.  No kernel runs (the pointers are never touched)."""
+    lib = kvt_pkg._lib
+    P = 0x10000   # a 16-byte aligned stand-in; every case returns before it would be used
+    H, Hq, D = 2, 16, 256
+
+    def call(out_f32=P, out_bf16=None, stride=Hq * D, n_splits=4, counters=P):
+        lib.call("kvt_sparse_decode", 2, P, Hq * D, P, P, P, P, 4096, P, P, P, P, P, 1023, None, None, P, 8192, P, 1,
+                 P, 2051, P, P, 0, 1, 2051, H, Hq, D, 64, 0.0625, n_splits, P, P, counters, out_f32, out_bf16, stride,
+                 None)
+
+    for kw in (dict(out_bf16=P), dict(out_f32=None), dict(stride=Hq * D - 8), dict(stride=Hq * D + 4),
+               dict(out_f32=P + 4), dict(n_splits=(1 << 31) // ((Hq // H) * D * 4))):
+        with pytest.raises(ValueError):
+            call(**kw)
