@@ -84,7 +84,11 @@ KVT_DEV i32x4 buffer_rsrc(const void* p, uint32_t bytes) {
 }
 
 // 16 bytes per lane from rsrc + voffset into lds + 16 * lane.  M0 (the LDS base) is an input operand of the
-// statement, so the compiler sets it; the s_nop is the wait state an LDS DMA needs after an SALU write of M0.
+// statement, so the compiler sets it.  The s_nop 4 gives the 5 wait states a vector-memory instruction needs after a
+// VALU write of an SGPR it reads (v_readfirstlane of the descriptor words, below): the compiler's hazard checks do
+// not look inside inline assembly, and with fewer wait states the load may use stale descriptor words (a wrong base
+// or range: an access outside the buffer).  It also covers the one wait state an LDS DMA needs after an SALU write
+// of M0.
 // Inline assembly rather than the builtin so that the compiler does not treat every later LDS read as dependent on
 // the copy: completion is tracked explicitly with wait_vmcnt by the caller.  The loads are non-temporal (nt): a
 // layer streams its KV bytes through the caches once, and marked as streaming they leave the small per-step metadata
@@ -98,14 +102,14 @@ KVT_DEV i32x4 uniform_rsrc(i32x4 r) {
 
 KVT_DEV void copy16_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" : : "v"(voffset), "s"(uniform_rsrc(rsrc)),
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds" : : "v"(voffset), "s"(uniform_rsrc(rsrc)),
                "{m0}"(base) : "memory");
 }
 
 // 4 bytes per lane from rsrc + voffset into lds + 4 * lane (same conventions).
 KVT_DEV void copy4_to_lds(i32x4 rsrc, void* lds, uint32_t voffset) {
   const uint32_t base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(uniform_rsrc(rsrc)),
+  asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(uniform_rsrc(rsrc)),
                "{m0}"(base) : "memory");
 }
 
