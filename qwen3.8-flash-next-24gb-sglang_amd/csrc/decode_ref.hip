@@ -173,32 +173,50 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
 // grid (D / 32, Hq, batch), 256 threads = 4 wavefronts: lane l of wavefront w holds dims 4 (l & 7) .. + 3 of the
-// block's 32 and merges splits c = 32 k + 4 (l >> 3) + w, k < 8, of each round of 256 (8 16-byte loads of o and 8
-// of (m, l) per lane, all in flight at once: one round for up to 256 splits), with a running max: (m, num, den) <-
-// (max(m, m_c), num e^(m - m') + o_c e^(m_c - m'), den e^(m - m') + l_c e^(m_c - m')).  The 32 merges of a dim quad
-// then combine across lanes (xor 8, 16, 32) and wavefronts (LDS).  An empty context gives 0/0 = NaN
+// block's 32 and takes splits c = 32 k + 4 (l >> 3) + w, k < 8, of each round of 256 (8 16-byte loads of o and 8
+// 8-byte loads of (m, l) per lane, all in flight at once: one round for up to 256 splits).  A round's maximum over the
+// wavefront's splits comes first (the partials' m is per split and q head, the same for every dim), then every split's
+// weight e^(m_c - M_w) independently of the others; a later round rescales the running sums once.  The sums of the 32
+// lanes of a dim quad reduce without LDS traffic (a DPP row rotation by 8 lanes, then the permlane16 / permlane32
+// swaps), and the 4 wavefronts merge with e^(M_w - M) in LDS.  Slots beyond the splits in use may hold anything, NaN
+// included: they are selected out, never scaled by zero.  An empty context gives 0/0 = NaN
 // (gemv/test_kv_paged_prefix.py:524-526).
 constexpr int kCombDims = 32;     // dims per block
 constexpr int kCombRound = 256;   // splits per round
 
 typedef float f4c __attribute__((ext_vector_type(4)));
 
-// Partial maxima are in natural-log units; the weights use the hardware exp2 on log2-scaled differences (<= 0).
-KVT_DEV void merge_into(float& m, f4c& num, float& den, float mc, f4c oc, float lc) {
-  constexpr float kL2e = 1.4426950408889634f;
-  const float mn = fmaxf(m, mc);
-  if (mn == -INFINITY) return;   // both empty
-  const float a = __builtin_amdgcn_exp2f((m - mn) * kL2e), c = __builtin_amdgcn_exp2f((mc - mn) * kL2e);
-  num = num * a + oc * c;
-  den = den * a + lc * c;
-  m = mn;
+// The value of lane l ^ 8 (DPP rotation by 8 within each row of 16 lanes) and the sum / max with the lane 16 and 32
+// apart (gfx950 permlane swaps: with both operands the same register, the two results are the value of the lane
+// itself and of its partner).  All 64 lanes must be active.
+KVT_DEV float lane_x8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));
+}
+KVT_DEV float sum_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+KVT_DEV float sum_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+KVT_DEV float max_x16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+KVT_DEV float max_x32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __global__ void __launch_bounds__(256) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
     const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
     int64_t out_stride_b) {
-  __shared__ float red[4][8][6];
+  constexpr float kL2e = 1.4426950408889634f;   // partial maxima are in natural-log units
+  __shared__ f4c nred[4][8];
+  __shared__ float dred[4][8];
+  __shared__ float mred[4];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
@@ -207,21 +225,20 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
   const int d0 = blockIdx.x * kCombDims + 4 * dq;
   const int sl = 4 * sub + w;   // the lane's split in each group of 32
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
-  float m = -INFINITY, den = 0.0f;
+  float m_run = -INFINITY, den = 0.0f;   // m_run: the wavefront's running maximum (uniform)
   f4c num = {0.f, 0.f, 0.f, 0.f};
   // the loads of a round index the n_chunks slots only: the first round's go out before the sequence length (which
-  // bounds the splits in use) has arrived; splits beyond it are dropped at the merge
+  // bounds the splits in use) has arrived
   int used = 0;
   for (int r0 = 0; r0 < n_chunks; r0 += kCombRound) {
     f4c ov[8];
-    float mv[8], lv[8];
+    float2 ml[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int c = r0 + 32 * k + sl;
       const int64_t it = (base + (c < n_chunks ? c : 0)) * gs + j;
       ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
-      mv[k] = part_ml[it * 2];
-      lv[k] = part_ml[it * 2 + 1];
+      ml[k] = *reinterpret_cast<const float2*>(&part_ml[it * 2]);
     }
     if (r0 == 0) {
       // chunk > 0: split c covers positions [c chunk, (c + 1) chunk); chunk 0: every split holds a partial
@@ -230,37 +247,53 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
       used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
                        : (split_counts != nullptr ? split_counts[b] : n_chunks);
     }
+    float mk[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {   // (slots beyond `used` may hold anything, NaN included: select, not scale)
-      const int c = r0 + 32 * k + sl;
-      if (c < used) merge_into(m, num, den, mv[k], ov[k], lv[k]);
+    for (int k = 0; k < 8; ++k) mk[k] = (r0 + 32 * k + sl < used) ? ml[k].x : -INFINITY;
+    float mr = fmaxf(fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3])), fmaxf(fmaxf(mk[4], mk[5]), fmaxf(mk[6], mk[7])));
+    mr = fmaxf(mr, lane_x8(mr));
+    mr = max_x32(max_x16(mr));
+    const float mn = fmaxf(m_run, mr);
+    if (mn != -INFINITY) {   // (uniform)
+      if (m_run != mn) {
+        const float a = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run - mn) * kL2e);
+        num *= a;
+        den *= a;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const bool ok = mk[k] != -INFINITY;
+        const float wk = ok ? __builtin_amdgcn_exp2f((mk[k] - mn) * kL2e) : 0.f;
+        num += (ok ? ov[k] : f4c{0.f, 0.f, 0.f, 0.f}) * wk;
+        den += (ok ? ml[k].y : 0.f) * wk;
+      }
+      m_run = mn;
     }
     if (r0 + kCombRound >= used) break;
   }
 #pragma unroll
-  for (int x = 8; x < 64; x <<= 1) {
-    f4c no;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) no[i] = __shfl_xor(num[i], x, 64);
-    merge_into(m, num, den, __shfl_xor(m, x, 64), no, __shfl_xor(den, x, 64));
-  }
+  for (int i = 0; i < 4; ++i) num[i] = sum_x32(sum_x16(num[i] + lane_x8(num[i])));
+  den = sum_x32(sum_x16(den + lane_x8(den)));
   if (sub == 0) {
-    red[w][dq][0] = m;
-    red[w][dq][1] = den;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) red[w][dq][2 + i] = num[i];
+    nred[w][dq] = num;
+    dred[w][dq] = den;
   }
+  if (lane == 0) mred[w] = m_run;
   __syncthreads();
   if (w == 0 && sub == 0) {
+    const float M = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+    f4c n4 = {0.f, 0.f, 0.f, 0.f};
+    float d4 = 0.f;
 #pragma unroll
-    for (int v = 1; v < 4; ++v) {
-      const f4c no = {red[v][dq][2], red[v][dq][3], red[v][dq][4], red[v][dq][5]};
-      merge_into(m, num, den, red[v][dq][0], no, red[v][dq][1]);
+    for (int v = 0; v < 4; ++v) {
+      const float a = mred[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mred[v] - M) * kL2e);
+      n4 += nred[v][dq] * a;
+      d4 += dred[v][dq] * a;
     }
     const int64_t oi = b * out_stride_b + (int64_t)hq * D + d0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float o = num[i] / den;
+      const float o = n4[i] / d4;
       if (out_f32) out_f32[oi + i] = o;
       if (out_bf16) out_bf16[oi + i] = bf16_rne(o);
     }
