@@ -172,17 +172,16 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 }
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
-// grid (D / 32, Hq, batch), 256 threads = 4 wavefronts: lane l of wavefront w holds dims 4 (l & 7) .. + 3 of the
-// block's 32 and takes splits c = 32 k + 4 (l >> 3) + w, k < 8, of each round of 256 (8 16-byte loads of o and 8
-// 8-byte loads of (m, l) per lane, all in flight at once: one round for up to 256 splits).  A round's maximum over the
-// wavefront's splits comes first (the partials' m is per split and q head, the same for every dim), then every split's
-// weight e^(m_c - M_w) independently of the others; a later round rescales the running sums once.  The sums of the 32
-// lanes of a dim quad reduce without LDS traffic (a DPP row rotation by 8 lanes, then the permlane16 / permlane32
-// swaps), and the 4 wavefronts merge with e^(M_w - M) in LDS.  Slots beyond the splits in use may hold anything, NaN
-// included: they are selected out, never scaled by zero.  An empty context gives 0/0 = NaN
-// (gemv/test_kv_paged_prefix.py:524-526).
+// grid (D / 32, Hq, batch), WAVES = min(4, ceil(n_chunks / 64)) wavefronts per block: lane l of wavefront w holds
+// dims 4 (l & 7) .. + 3 of the block's 32 and takes splits c = 8 WAVES k + WAVES (l >> 3) + w, k < 8, of each round of
+// 64 WAVES (8 16-byte loads of o and 8 8-byte loads of (m, l) per lane, all in flight at once: one round for up to
+// 256 splits).  A round's maximum over the wavefront's splits comes first (the partials' m
+// is per split and q head, the same for every dim), then every split's weight e^(m_c - M_w) independently of the
+// others; a later round rescales the running sums once.  The sums of the 32 lanes of a dim quad reduce without LDS
+// traffic (a DPP row rotation by 8 lanes, then the permlane16 / permlane32 swaps), and the wavefronts merge with
+// e^(M_w - M) in LDS.  Slots beyond the splits in use may hold anything, NaN included: they are selected out, never
+// scaled by zero.  An empty context gives 0/0 = NaN (gemv/test_kv_paged_prefix.py:524-526).
 constexpr int kCombDims = 32;     // dims per block
-constexpr int kCombRound = 256;   // splits per round
 
 typedef float f4c __attribute__((ext_vector_type(4)));
 
@@ -209,21 +208,23 @@ KVT_DEV float max_x32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-__global__ void __launch_bounds__(256) decode_combine_kernel(
+template <int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
     const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
     int64_t out_stride_b) {
   constexpr float kL2e = 1.4426950408889634f;   // partial maxima are in natural-log units
-  __shared__ f4c nred[4][8];
-  __shared__ float dred[4][8];
-  __shared__ float mred[4];
+  constexpr int kCombRound = 64 * WAVES;        // splits per round
+  __shared__ f4c nred[WAVES][8];
+  __shared__ float dred[WAVES][8];
+  __shared__ float mred[WAVES];
   const int hq = blockIdx.y;
   const int b = blockIdx.z;
   const int h = hq / gs, j = hq - h * gs;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = WAVES == 1 ? 0 : (int)(threadIdx.x >> 6);
   const int dq = lane & 7, sub = lane >> 3;
   const int d0 = blockIdx.x * kCombDims + 4 * dq;
-  const int sl = 4 * sub + w;   // the lane's split in each group of 32
+  const int sl = WAVES * sub + w;   // the lane's split in each group of 8 WAVES
   const int64_t base = ((int64_t)b * H + h) * n_chunks;
   float m_run = -INFINITY, den = 0.0f;   // m_run: the wavefront's running maximum (uniform)
   f4c num = {0.f, 0.f, 0.f, 0.f};
@@ -235,7 +236,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
     float2 ml[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int c = r0 + 32 * k + sl;
+      const int c = r0 + 8 * WAVES * k + sl;
       const int64_t it = (base + (c < n_chunks ? c : 0)) * gs + j;
       ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
       ml[k] = *reinterpret_cast<const float2*>(&part_ml[it * 2]);
@@ -249,7 +250,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
     }
     float mk[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) mk[k] = (r0 + 32 * k + sl < used) ? ml[k].x : -INFINITY;
+    for (int k = 0; k < 8; ++k) mk[k] = (r0 + 8 * WAVES * k + sl < used) ? ml[k].x : -INFINITY;
     float mr = fmaxf(fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3])), fmaxf(fmaxf(mk[4], mk[5]), fmaxf(mk[6], mk[7])));
     mr = fmaxf(mr, lane_x8(mr));
     mr = max_x32(max_x16(mr));
@@ -274,6 +275,18 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) num[i] = sum_x32(sum_x16(num[i] + lane_x8(num[i])));
   den = sum_x32(sum_x16(den + lane_x8(den)));
+  if constexpr (WAVES == 1) {
+    if (sub == 0) {
+      const int64_t oi = b * out_stride_b + (int64_t)hq * D + d0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float o = num[i] / den;
+        if (out_f32) out_f32[oi + i] = o;
+        if (out_bf16) out_bf16[oi + i] = bf16_rne(o);
+      }
+    }
+    return;
+  }
   if (sub == 0) {
     nred[w][dq] = num;
     dred[w][dq] = den;
@@ -281,11 +294,13 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(
   if (lane == 0) mred[w] = m_run;
   __syncthreads();
   if (w == 0 && sub == 0) {
-    const float M = fmaxf(fmaxf(mred[0], mred[1]), fmaxf(mred[2], mred[3]));
+    float M = mred[0];
+#pragma unroll
+    for (int v = 1; v < WAVES; ++v) M = fmaxf(M, mred[v]);
     f4c n4 = {0.f, 0.f, 0.f, 0.f};
     float d4 = 0.f;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < WAVES; ++v) {
       const float a = mred[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((mred[v] - M) * kL2e);
       n4 += nred[v][dq] * a;
       d4 += dred[v][dq] * a;
@@ -347,12 +362,23 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
                        int64_t chunk, const void* seq_lens, const void* split_counts, void* out_f32, void* out_bf16,
                        int64_t out_stride_b, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % kCombDims != 0) return KVT_EINVAL;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch),
-                     dim3(256), 0,
-                     (hipStream_t)stream,
-                     (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,
-                     (const int32_t*)seq_lens, (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16,
-                     out_stride_b);
+  const dim3 grid((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch);
+#define KVT_COMB(W_)                                                                                               \
+  hipLaunchKernelGGL((decode_combine_kernel<W_>), grid, dim3(64 * W_), 0, (hipStream_t)stream, (const float*)part_o, \
+                     (const float*)part_ml, H, Hq / H, D, n_chunks, chunk, (const int32_t*)seq_lens,               \
+                     (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b)
+  // one round of ceil(n_chunks / 64) wavefronts (4 from 193 splits on, in rounds of 256): no lane issues loads
+  // that only repeat slot 0, and with one wavefront there is no LDS merge
+  if (n_chunks <= 64) {
+    KVT_COMB(1);
+  } else if (n_chunks <= 128) {
+    KVT_COMB(2);
+  } else if (n_chunks <= 192) {
+    KVT_COMB(3);
+  } else {
+    KVT_COMB(4);
+  }
+#undef KVT_COMB
   KVT_CHECK_LAUNCH();
   return KVT_OK;
 }

@@ -6,7 +6,7 @@ slot (b * H + h) * n_chunks + c, q head j of the group at row slot * gs + j).  T
 splits and several rounds, empty splits (m = -inf, o = 0, l = 0), slots past the splits in use filled with NaN (they
 must be selected out, not scaled by zero), a sequence with no split at all (0/0 = NaN, as the reference's chunk kernel,
 gemv/test_kv_paged_prefix.py:524-526), the chunk > 0 mode (splits in use from the sequence length) and bf16 output
-(the fp32 result rounded to nearest even).
+(the fp32 result rounded to nearest even), at split counts that give the kernel one to four wavefronts per block.
 """
 from __future__ import annotations
 
@@ -79,7 +79,7 @@ def _check(got, want):
     assert float((err / (np.abs(w) + 1.0)).max()) < 2e-5, float(err.max())
 
 
-@pytest.mark.parametrize("n_chunks", [1, 33, 256, 257, 600])
+@pytest.mark.parametrize("n_chunks", [1, 33, 64, 65, 100, 150, 192, 256, 257, 600])
 def test_combine_split_counts(kvt_pkg, n_chunks):
     """chunk = 0: sequence b uses its first split_counts[b] slots (all, about half, none)."""
     batch = 3
@@ -100,10 +100,12 @@ def test_combine_chunk_mode(kvt_pkg, n_chunks, chunk, lens):
     _check(got, _merge64(o, ml, use, batch, n_chunks))
 
 
-def test_combine_bf16_is_rounded_fp32(kvt_pkg):
-    """bf16 output = the fp32 output rounded to nearest even, bit for bit (NaN rows included)."""
-    batch, n_chunks = 2, 300
-    used = [300, 0]
+@pytest.mark.parametrize("n_chunks", [40, 300])
+def test_combine_bf16_is_rounded_fp32(kvt_pkg, n_chunks):
+    """bf16 output = the fp32 output rounded to nearest even, bit for bit (NaN rows included); one wavefront per
+    block (40 splits) and four (300)."""
+    batch = 2
+    used = [n_chunks, 0]
     o, ml, _ = _partials(batch, n_chunks, used, seed=7)
     f32 = _combine(o, ml, batch, n_chunks, 0, [1, 1], used, torch.float32)
     b16 = _combine(o, ml, batch, n_chunks, 0, [1, 1], used, torch.bfloat16)
