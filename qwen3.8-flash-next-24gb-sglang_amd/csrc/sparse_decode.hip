@@ -94,8 +94,22 @@ struct SparseArgs {
   int64_t so_n, so_h;
 };
 
-KVT_DEV int64_t load_idx(const void* p, int is64, int64_t i) {
-  return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t) reinterpret_cast<const int32_t*>(p)[i];
+// Entry i of an int32 or int64 index array (is64: exactly 0 or 1, as the launchers store it) without a branch on the
+// width: both words are loaded unconditionally (an int32 entry reads its own word twice) and combined with integer
+// arithmetic only.  Split in two (the loads, then the value) so that a caller can issue several entries' loads
+// before it waits for any of them.
+struct IdxWords {
+  uint32_t lo, hi, wide;
+};
+KVT_DEV IdxWords idx_words(const void* p, int is64, int64_t i) {
+  const uint32_t wide = (uint32_t)is64;
+  const int32_t* w = reinterpret_cast<const int32_t*>(p) + (i << wide);
+  return IdxWords{(uint32_t)w[0], (uint32_t)w[wide], wide};
+}
+KVT_DEV int64_t idx_value(const IdxWords& x) {
+  const uint32_t mask = 0u - x.wide;   // all ones for int64 entries
+  const uint32_t top = (x.hi & mask) | ((uint32_t)((int32_t)x.lo >> 31) & ~mask);
+  return (int64_t)(((uint64_t)top << 32) | x.lo);
 }
 
 KVT_DEV f4 mfma_bf16(bf4 a, bf4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0); }
@@ -600,31 +614,60 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
   work_of_block<ROWS>(H, wx, wy);
   const int b = wy / H;
   const int h = wy - b * H;
-  // the block's query row, context length and column range
-  int64_t qrow, L, c_begin, c_end;
+  // The start-up loads go out in as few dependent rounds as the data allows: the request's index-array entries and
+  // length together (no wait between them), with the decode's q rows and the smoothing factors into registers; then
+  // the first tile's resolve chain (position, slot, owner).  The q rows reach LDS after the chain.
+  const IdxWords wreq = idx_words(A.req_indices, A.req64, b);
+  const IdxWords w0 = ROWS ? idx_words(A.cu_q, A.cuq64, b) : idx_words(A.cu_k, A.cu64, b);
+  const IdxWords w1 = ROWS ? idx_words(A.cu_q, A.cuq64, b + 1) : idx_words(A.cu_k, A.cu64, b + 1);
+  const int32_t len = ROWS ? A.kv_lens[b] : A.seq_lens[b];   // widened after the barrier (no wait before it)
+  // the group's q heads (512 16-byte chunks, 2 per thread; heads beyond the group read head 0 and are zeroed)
+  constexpr int kQChunks = kHeads * kD / 8 / (64 * kWaves);
+  uint4 qv[kQChunks];
+  auto load_q = [&](int64_t row) {
+#pragma unroll
+    for (int k = 0; k < kQChunks; ++k) {
+      const int i = (int)threadIdx.x + 64 * kWaves * k;
+      const int hq = i / (kD / 8), ch = i - hq * (kD / 8);
+      const int hr = hq < gs ? hq : 0;
+      const uint4 w = *reinterpret_cast<const uint4*>(A.q + row * A.sq_n + (int64_t)(h * gs + hr) * A.sq_h + 8 * ch);
+      qv[k] = hq < gs ? w : uint4{0u, 0u, 0u, 0u};
+    }
+  };
+  if constexpr (!ROWS) load_q(b);
+  // smoothing factors of this lane's channels 4 lane .. 4 lane + 3 (an absent factor: an empty buffer, read as 0)
+  const uint32_t smb = (uint32_t)H * kD * 2;
+  const uint2 wsk = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                  rsrc(A.sm_k, A.sm_k != nullptr ? smb : 0u), (h * kD + 4 * lane) * 2, 0, 0));
+  const uint2 wsv = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                  rsrc(A.sm_v, A.sm_v != nullptr ? smb : 0u), (h * kD + 4 * lane) * 2, 0, 0));
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t req = idx_value(wreq), x0 = idx_value(w0), x1 = idx_value(w1), L = len;
+  // the block's query row and column range
+  int64_t qrow, c_begin, c_end;
   if constexpr (ROWS) {
-    const int64_t q0 = load_idx(A.cu_q, A.cuq64, b), q1 = load_idx(A.cu_q, A.cuq64, b + 1);
     const int64_t j = wx;
-    if (q0 + j >= q1) return;   // block-uniform: the chunk is shorter than the grid
-    qrow = q0 + j;
-    L = A.kv_lens[b];
-    const int64_t visible = j + L - (q1 - q0) + 1;
+    if (x0 + j >= x1) return;   // block-uniform: the chunk is shorter than the grid
+    qrow = x0 + j;
+    load_q(qrow);
+    const int64_t visible = j + L - (x1 - x0) + 1;
     c_begin = 0;
     c_end = visible < (int64_t)A.topk ? (visible > 0 ? visible : 0) : (int64_t)A.topk;
   } else {
     qrow = b;
-    L = A.seq_lens[b];
-    const int64_t vcount = load_idx(A.cu_k, A.cu64, b + 1) - load_idx(A.cu_k, A.cu64, b);
+    const int64_t vcount = x1 - x0;
     const int64_t span = (int64_t)kCols * (MULTI ? A.tiles : 1);
     c_begin = (int64_t)wx * span;
     const int64_t lim = vcount < (int64_t)A.topk ? vcount : (int64_t)A.topk;
     c_end = c_begin + span < lim ? c_begin + span : lim;
   }
 
-  const int64_t req = load_idx(A.req_indices, A.req64, b);
   const int32_t* idx_row = A.indices + qrow * A.si_m + (int64_t)h * A.si_g;
-  // the wavefront's first tile (prefill rows: the first pass of the column table) is resolved first, so that the
-  // chains of dependent loads run beside the Q copy
+  // every scalar the resolve chain needs, in registers here: the compiler would otherwise sink these loads (and the
+  // kernel-argument reads) into the chain's branch, one wait each, behind the index load
+  asm volatile("" ::"s"(idx_row), "s"(L), "s"(req), "s"(c_end), "s"(A.req_to_token), "s"(A.req_stride),
+               "s"(A.owner), "s"(A.ring_mask), "s"(A.si_n));
+  // the wavefront's first tile (prefill rows: the first pass of the column table)
   TileCols tc0{};
   const bool has_tile = c_begin + kRows * wave < c_end;
   int nh = 0, nc = 0;
@@ -633,13 +676,11 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
                                                      L, req, h, S, nh, nc);
   else if (has_tile)
     tc0 = resolve_tile<KIND, G8>(A, c_begin + kRows * wave, c_end, idx_row, L, req, h, lane);
-  // the group's q heads into LDS (512 16-byte chunks; heads beyond the group read as zero)
 #pragma unroll
-  for (int i = threadIdx.x; i < kHeads * kD / 8; i += 64 * kWaves) {
+  for (int k = 0; k < kQChunks; ++k) {
+    const int i = (int)threadIdx.x + 64 * kWaves * k;
     const int hq = i / (kD / 8), ch = i - hq * (kD / 8);
-    uint4 w = {0u, 0u, 0u, 0u};
-    if (hq < gs) w = *reinterpret_cast<const uint4*>(A.q + qrow * A.sq_n + (int64_t)(h * gs + hq) * A.sq_h + 8 * ch);
-    *reinterpret_cast<uint4*>(&qs[hq * kKPitch + 8 * ch]) = w;
+    *reinterpret_cast<uint4*>(&qs[hq * kKPitch + 8 * ch]) = qv[k];
   }
   PoolRsrc P;
   {
@@ -654,21 +695,12 @@ KVT_DEV void sparse_attn_block(const SparseArgs& A, BlockLds<CAP>& S) {
     P.ks4 = rsrc(A.ks, KIND == 0 ? 0u : s4);
     P.vs4 = rsrc(A.vs, KIND == 0 ? 0u : s4);
   }
-  // smoothing factors of this lane's channels 4 lane .. 4 lane + 3
-  float smk[4] = {1.f, 1.f, 1.f, 1.f}, smv[4] = {1.f, 1.f, 1.f, 1.f};
-  if (A.sm_k != nullptr) {
-    const uint2 w = *reinterpret_cast<const uint2*>(A.sm_k + (int64_t)h * kD + 4 * lane);
-    smk[0] = f16_bits_to_f32((uint16_t)w.x);
-    smk[1] = f16_bits_to_f32((uint16_t)(w.x >> 16));
-    smk[2] = f16_bits_to_f32((uint16_t)w.y);
-    smk[3] = f16_bits_to_f32((uint16_t)(w.y >> 16));
-  }
-  if (A.sm_v != nullptr) {
-    const uint2 w = *reinterpret_cast<const uint2*>(A.sm_v + (int64_t)h * kD + 4 * lane);
-    smv[0] = f16_bits_to_f32((uint16_t)w.x);
-    smv[1] = f16_bits_to_f32((uint16_t)(w.x >> 16));
-    smv[2] = f16_bits_to_f32((uint16_t)w.y);
-    smv[3] = f16_bits_to_f32((uint16_t)(w.y >> 16));
+  float smk[4], smv[4];
+  const uint32_t swk[4] = {wsk.x, wsk.x >> 16, wsk.y, wsk.y >> 16}, swv[4] = {wsv.x, wsv.x >> 16, wsv.y, wsv.y >> 16};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    smk[i] = A.sm_k != nullptr ? f16_bits_to_f32((uint16_t)swk[i]) : 1.f;
+    smv[i] = A.sm_v != nullptr ? f16_bits_to_f32((uint16_t)swv[i]) : 1.f;
   }
   __syncthreads();   // q staged
 
@@ -891,8 +923,8 @@ int kvt_sparse_decode(int kind, const void* q, int64_t q_stride_b, const void* k
   A.rvs = (const uint16_t*)ring_vs, A.owner = (const int32_t*)owner, A.ring_mask = ring_mask;
   A.sm_k = (const uint16_t*)sm_k, A.sm_v = (const uint16_t*)sm_v;
   A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
-  A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.idx_stride = idx_stride;
-  A.seq_lens = (const int32_t*)seq_lens, A.cu_k = cu_k, A.cu64 = cu_is_int64, A.topk = topk;
+  A.req64 = req_is_int64 != 0, A.indices = (const int32_t*)indices, A.idx_stride = idx_stride;
+  A.seq_lens = (const int32_t*)seq_lens, A.cu_k = cu_k, A.cu64 = cu_is_int64 != 0, A.topk = topk;
   A.H = H, A.gs = Hq / H, A.n_splits = n_splits, A.tiles = tiles, A.rows8 = (uint32_t)rows8;
   A.rows4 = (uint32_t)rows4, A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = q_stride_b, A.sq_h = kD;
   A.si_m = idx_stride, A.si_g = 0, A.si_n = 1, A.part_o = (float*)part_o, A.part_ml = (float*)part_ml;
@@ -923,11 +955,11 @@ int kvt_sparse_prefill(int kind, const void* q, int64_t sq_n, int64_t sq_h, cons
   A.rvs = (const uint16_t*)ring_vs, A.owner = (const int32_t*)owner, A.ring_mask = ring_mask;
   A.sm_k = (const uint16_t*)sm_k, A.sm_v = (const uint16_t*)sm_v;
   A.req_to_token = (const int32_t*)req_to_token, A.req_stride = req_stride, A.req_indices = req_indices;
-  A.req64 = req_is_int64, A.indices = (const int32_t*)indices, A.topk = topk;
+  A.req64 = req_is_int64 != 0, A.indices = (const int32_t*)indices, A.topk = topk;
   A.H = H, A.gs = Hq / H, A.n_splits = 1, A.tiles = 1, A.rows8 = (uint32_t)rows8, A.rows4 = (uint32_t)rows4;
   A.scale = scale, A.q = (const uint16_t*)q, A.sq_n = sq_n, A.sq_h = sq_h;
   A.si_m = si_m, A.si_g = si_g, A.si_n = si_n;
-  A.cu_q = cu_q, A.cuq64 = cu_q_is_int64, A.kv_lens = (const int32_t*)kv_lens;
+  A.cu_q = cu_q, A.cuq64 = cu_q_is_int64 != 0, A.kv_lens = (const int32_t*)kv_lens;
   A.out = out, A.out_f32 = out_f32, A.so_n = so_n, A.so_h = so_h;
   return launch<true>(kind, group8, dim3((unsigned)max_q, (unsigned)(batch * H)), (hipStream_t)stream, A);
 }
