@@ -173,9 +173,9 @@ __global__ void __launch_bounds__(kThreads) decode_ref_kernel(TierArgs A, const 
 
 // out[b, hq, d] = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c over the splits of (b, hq / gs).
 // grid (D / 32, Hq, batch), WAVES = min(4, ceil(n_chunks / 64)) wavefronts per block: lane l of wavefront w holds
-// dims 4 (l & 7) .. + 3 of the block's 32 and takes splits c = 8 WAVES k + WAVES (l >> 3) + w, k < 8, of each round of
-// 64 WAVES (8 16-byte loads of o and 8 8-byte loads of (m, l) per lane, all in flight at once: one round for up to
-// 256 splits).  A round's maximum over the wavefront's splits comes first (the partials' m
+// dims 4 (l & 7) .. + 3 of the block's 32 and takes splits c = 8 WAVES k + WAVES (l >> 3) + w, k < KL, of each round
+// of 8 WAVES KL (KL 16-byte loads of o and KL 8-byte loads of (m, l) per lane, all in flight at once: one round for
+// up to 256 splits; KL = 8, or ceil(n_chunks / 8) in a one-wavefront block, so that few lanes repeat slot 0).  A round's maximum over the wavefront's splits comes first (the partials' m
 // is per split and q head, the same for every dim), then every split's weight e^(m_c - M_w) independently of the
 // others; a later round rescales the running sums once.  The sums of the 32 lanes of a dim quad reduce without LDS
 // traffic (a DPP row rotation by 8 lanes, then the permlane16 / permlane32 swaps), and the wavefronts merge with
@@ -208,13 +208,13 @@ KVT_DEV float max_x32(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int WAVES>
+template <int WAVES, int KL>
 __global__ void __launch_bounds__(64 * WAVES) decode_combine_kernel(
     const float* part_o, const float* part_ml, int H, int gs, int D, int n_chunks, int64_t chunk,
     const int32_t* seq_lens, const int32_t* split_counts, float* out_f32, uint16_t* out_bf16,
     int64_t out_stride_b) {
   constexpr float kL2e = 1.4426950408889634f;   // partial maxima are in natural-log units
-  constexpr int kCombRound = 64 * WAVES;        // splits per round
+  constexpr int kCombRound = 8 * WAVES * KL;    // splits per round (KL loads of o and (m, l) per lane)
   __shared__ f4c nred[WAVES][8];
   __shared__ float dred[WAVES][8];
   __shared__ float mred[WAVES];
@@ -232,10 +232,10 @@ __global__ void __launch_bounds__(64 * WAVES) decode_combine_kernel(
   // bounds the splits in use) has arrived
   int used = 0;
   for (int r0 = 0; r0 < n_chunks; r0 += kCombRound) {
-    f4c ov[8];
-    float2 ml[8];
+    f4c ov[KL];
+    float2 ml[KL];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < KL; ++k) {
       const int c = r0 + 8 * WAVES * k + sl;
       const int64_t it = (base + (c < n_chunks ? c : 0)) * gs + j;
       ov[k] = *reinterpret_cast<const f4c*>(&part_o[it * D + d0]);
@@ -248,10 +248,12 @@ __global__ void __launch_bounds__(64 * WAVES) decode_combine_kernel(
       used = chunk > 0 ? (int)min((int64_t)n_chunks, (L + chunk - 1) / chunk)
                        : (split_counts != nullptr ? split_counts[b] : n_chunks);
     }
-    float mk[8];
+    float mk[KL];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) mk[k] = (r0 + 8 * WAVES * k + sl < used) ? ml[k].x : -INFINITY;
-    float mr = fmaxf(fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3])), fmaxf(fmaxf(mk[4], mk[5]), fmaxf(mk[6], mk[7])));
+    for (int k = 0; k < KL; ++k) mk[k] = (r0 + 8 * WAVES * k + sl < used) ? ml[k].x : -INFINITY;
+    float mr = mk[0];
+#pragma unroll
+    for (int k = 1; k < KL; ++k) mr = fmaxf(mr, mk[k]);
     mr = fmaxf(mr, lane_x8(mr));
     mr = max_x32(max_x16(mr));
     const float mn = fmaxf(m_run, mr);
@@ -262,7 +264,7 @@ __global__ void __launch_bounds__(64 * WAVES) decode_combine_kernel(
         den *= a;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < KL; ++k) {
         const bool ok = mk[k] != -INFINITY;
         const float wk = ok ? __builtin_amdgcn_exp2f((mk[k] - mn) * kL2e) : 0.f;
         num += (ok ? ov[k] : f4c{0.f, 0.f, 0.f, 0.f}) * wk;
@@ -363,20 +365,31 @@ int kvt_decode_combine(const void* part_o, const void* part_ml, int batch, int H
                        int64_t out_stride_b, void* stream) {
   if (batch <= 0 || H <= 0 || Hq % H != 0 || n_chunks <= 0 || chunk < 0 || D % kCombDims != 0) return KVT_EINVAL;
   const dim3 grid((unsigned)(D / kCombDims), (unsigned)Hq, (unsigned)batch);
-#define KVT_COMB(W_)                                                                                               \
-  hipLaunchKernelGGL((decode_combine_kernel<W_>), grid, dim3(64 * W_), 0, (hipStream_t)stream, (const float*)part_o, \
-                     (const float*)part_ml, H, Hq / H, D, n_chunks, chunk, (const int32_t*)seq_lens,               \
-                     (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16, out_stride_b)
+#define KVT_COMB(W_, KL_)                                                                                          \
+  hipLaunchKernelGGL((decode_combine_kernel<W_, KL_>), grid, dim3(64 * W_), 0, (hipStream_t)stream,                \
+                     (const float*)part_o, (const float*)part_ml, H, Hq / H, D, n_chunks, chunk,                   \
+                     (const int32_t*)seq_lens, (const int32_t*)split_counts, (float*)out_f32, (uint16_t*)out_bf16, \
+                     out_stride_b)
   // one round of ceil(n_chunks / 64) wavefronts (4 from 193 splits on, in rounds of 256): no lane issues loads
-  // that only repeat slot 0, and with one wavefront there is no LDS merge
+  // that only repeat slot 0, and with one wavefront there is no LDS merge; a one-wavefront block issues
+  // ceil(n_chunks / 8) loads per lane (33 splits: 5)
   if (n_chunks <= 64) {
-    KVT_COMB(1);
+    switch ((n_chunks + 7) / 8) {
+      case 1: KVT_COMB(1, 1); break;
+      case 2: KVT_COMB(1, 2); break;
+      case 3: KVT_COMB(1, 3); break;
+      case 4: KVT_COMB(1, 4); break;
+      case 5: KVT_COMB(1, 5); break;
+      case 6: KVT_COMB(1, 6); break;
+      case 7: KVT_COMB(1, 7); break;
+      default: KVT_COMB(1, 8); break;
+    }
   } else if (n_chunks <= 128) {
-    KVT_COMB(2);
+    KVT_COMB(2, 8);
   } else if (n_chunks <= 192) {
-    KVT_COMB(3);
+    KVT_COMB(3, 8);
   } else {
-    KVT_COMB(4);
+    KVT_COMB(4, 8);
   }
 #undef KVT_COMB
   KVT_CHECK_LAUNCH();
