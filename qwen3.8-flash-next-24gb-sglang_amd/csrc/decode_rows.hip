@@ -718,10 +718,13 @@ decode_rows_kernel(const int32_t* plan, const int32_t* seq_lens, const int32_t* 
     c = bid - b * n_splits;
     n_b = n_splits;
   }
-  const int64_t L = seq_lens[b];
-  const int64_t R = ring_len[b];
+  const int32_t len32 = seq_lens[b], ring32 = ring_len[b];
   const int64_t rs = ring_start[b];
   const int64_t rbase = ring_base[b];
+  // the four placement loads in flight together: the compiler would widen each int32 right after its load, one wait
+  // before the next load's issue
+  asm volatile("" ::"s"(len32), "s"(ring32), "s"(rs), "s"(rbase));
+  const int64_t L = len32, R = ring32;
   // the plan holds this block's ranges and first tile rows when it was made for the current placement
   const bool planned = plan != nullptr && __builtin_amdgcn_readlane(pv, 0) == b &&
                        __builtin_amdgcn_readlane(pv, 1) == c && __builtin_amdgcn_readlane(pv, 2) == n_b &&
