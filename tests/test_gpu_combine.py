@@ -6,7 +6,8 @@ slot (b * H + h) * n_chunks + c, q head j of the group at row slot * gs + j).  T
 splits and several rounds, empty splits (m = -inf, o = 0, l = 0), slots past the splits in use filled with NaN (they
 must be selected out, not scaled by zero), a sequence with no split at all (0/0 = NaN, as the reference's chunk kernel,
 gemv/test_kv_paged_prefix.py:524-526), the chunk > 0 mode (splits in use from the sequence length) and bf16 output
-(the fp32 result rounded to nearest even), at split counts that give the kernel one to four wavefronts per block.
+(the fp32 result rounded to nearest even), at split counts that give the kernel one to four wavefronts per block
+and, with one wavefront, each of its 1 to 8 loads per lane.
 """
 from __future__ import annotations
 
@@ -79,7 +80,7 @@ def _check(got, want):
     assert float((err / (np.abs(w) + 1.0)).max()) < 2e-5, float(err.max())
 
 
-@pytest.mark.parametrize("n_chunks", [1, 33, 64, 65, 100, 150, 192, 256, 257, 600])
+@pytest.mark.parametrize("n_chunks", [1, 9, 17, 25, 33, 41, 49, 57, 64, 65, 100, 150, 192, 256, 257, 600])
 def test_combine_split_counts(kvt_pkg, n_chunks):
     """chunk = 0: sequence b uses its first split_counts[b] slots (all, about half, none)."""
     batch = 3
