@@ -127,12 +127,13 @@ int kvt_compact_gather(int kind, const void* k, const void* v, const void* k_sca
  * kind 2, the owner table, dequantized as kvt_compact_gather writes them (bf16(q * s * sm)) and attended with scale;
  * bf16 matrix-core products, fp32 accumulation.  Split s of a (request, KV head) covers columns [64 T s, 64 T (s + 1))
  * with T = ceil(ceil(topk / 64) / n_splits) (T > 1: each wavefront loops over T 16-column tiles) and writes one
- * unnormalized partial to part_o (fp32 [batch * H * n_splits, Hq / H, D]) and part_ml ([..., 2]).  counters NULL:
+ * unnormalized partial to part_o (fp32 [batch * H * n_splits, Hq / H, D]) and part_ml ([..., 2]); one (request, KV
+ * head)'s partials n_splits * Hq / H * D * 4 bytes < 2^31, else KVT_EINVAL.  counters NULL:
  * merge them afterwards with kvt_decode_combine(n_chunks = n_splits, chunk = 0, split_counts = NULL).  counters
  * (int32 [batch * H], zero before the first call; every call leaves them zero): the launch merges them itself -- the
  * block of a (request, KV head) that counts last merges its n_splits partials in split order and writes out_f32 or
  * out_bf16 (exactly one; [batch, Hq, D] rows with batch stride out_stride_b >= Hq * D, a multiple of 8, 16-byte
- * aligned; one (request, KV head)'s partials n_splits * Hq / H * D * 4 bytes < 2^31); calls sharing the counters and
+ * aligned); calls sharing the counters and
  * partials must not overlap.  Faster than the combine launch for few splits (<= 8), slower for many: one block
  * reads all of a (request, KV head)'s partials.  A request with no attended column comes out
  * NaN (0/0).  n_splits >= 1; Hq / H <= 16, D = 256.  Kinds and buffers as kvt_compact_gather; pool_rows = rows of k / v (byte offsets
